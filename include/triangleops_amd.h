@@ -1,0 +1,131 @@
+/*
+ * triangleops_amd — C ABI of the MI355X (gfx950) kernels behind the triangle_ops Python API.
+ *
+ * Plain C: raw device pointers, element counts/strides (in elements, not bytes), scalars and
+ * an opaque HIP stream handle (`hipStream_t` passed as `void*`; NULL = default stream).
+ * Every function enqueues work on `stream` and returns immediately; none allocates, frees or
+ * synchronizes.  Return value: TOPS_OK (0) or a TOPS_E* code; the message for the calling
+ * thread is then available from tops_last_error().
+ *
+ * Each entry point names the reference function it replaces (paths relative to the
+ * youngchan2/TriangleOps repository root).  Dtype codes select the I/O type of the io-typed
+ * pointers ("io" below); the LayerNorm-fold vectors are always fp32.
+ */
+#ifndef TRIANGLEOPS_AMD_H
+#define TRIANGLEOPS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { TOPS_DTYPE_F16 = 1, TOPS_DTYPE_BF16 = 2, TOPS_DTYPE_F32 = 3 };
+enum { TOPS_OK = 0, TOPS_EINVAL = 1, TOPS_EUNSUPPORTED = 2, TOPS_ELAUNCH = 3 };
+
+/* Message describing the last error returned on the calling thread ("" if none). */
+const char* tops_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int tops_abi_version(void);
+
+/*
+ * triangle_multiplicative_update, input phase.
+ * Replaces `input_phase` + its Triton kernel (triangle_mul/kernel.py:235-279, :54-162).
+ *   x      io   (B, L, L, C) contiguous, C == 128
+ *   mask   int8 (B, L, L) contiguous (bool storage is accepted: 0/1), or NULL; multiplies the output
+ *   Wp, Wg io   (C_out, C) LN-folded weights (out, in);  sWp, sWg, Bp, Bg fp32 (C_out,)
+ *   ab     io   out[f * B*L*ld + (b*L + r)*ld + c] for f < C_out, r < L, c < ld (ld >= L)
+ *               = sigmoid(G) * P * mask of token (b, i, j) with (i, j) = (r, c), or (c, r) when
+ *               transpose != 0; positions c >= L are written as 0.
+ * C_out must be 128 or 256.
+ */
+int tops_tmu_input_phase(const void* x, const void* mask, const void* Wp, const void* Wg, const float* sWp,
+                         const float* sWg, const float* Bp, const float* Bg, void* ab, int64_t B, int64_t L,
+                         int64_t C, int64_t C_out, int64_t ld, int transpose, float eps, int dtype, void* stream);
+
+/*
+ * triangle_multiplicative_update, triangle einsum (replaces the torch.einsum calls at
+ * triangle_mul/module.py:80-84).  For every channel-batch slab s < nslab:
+ *   y[s*L*ldy + i*ldy + j] = sum_{k < ld} a[s*L*ld + i*ld + k] * b[s*L*ld + j*ld + k]
+ * with a = ab, b = ab + nslab*L*ld, for i, j < L.  ld must be a multiple of 64 and the
+ * columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them).  Outgoing feeds
+ * the natural token grid, incoming the transposed one (transpose=1 above).
+ */
+int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
+                    void* stream);
+
+/*
+ * triangle_multiplicative_update, output phase.
+ * Replaces `output_phase` + its Triton kernel (triangle_mul/kernel.py:282-326).
+ *   y      io   channel-major: y[c * B*L*ldy + (b*L + i)*ldy + j], c < C
+ *   x      io   (B, L, L, C) contiguous
+ *   Wp, Wg io   (C_out, C);  sWp, sWg, Bp, Bg fp32 (C_out,)
+ *   out    io   (B, L, L, C_out) contiguous = p_out(LN_out(y)) * sigmoid(g_out(LN_in(x)))
+ */
+int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
+                          const float* sWg, const float* Bp, const float* Bg, void* out, int64_t B, int64_t L,
+                          int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype, void* stream);
+
+/*
+ * triangle_attention: LayerNorm + row-shared pair-bias projection in one pass.
+ * Replaces F.layer_norm (triangle_attn/module.py:77-83) and `bias_proj_kernel`
+ * (triangle_attn/kernel.py:36-98, launched at :303-322).
+ *   x      io   element (q, k, c) at x[q*sx0 + k*sx1 + c], c < C (channel stride 1)
+ *   w_ln, b_ln  io (C,) LayerNorm affine (b_ln may be NULL); ignored when apply_ln == 0
+ *   WZ     io   (H, C);  BZ fp32 (H,) or NULL
+ *   x_ln   io   (N, N, C) contiguous LN(x), or NULL (not written); must be NULL when apply_ln == 0
+ *   bias   io   (H, N, N) contiguous: bias[h,q,k] = x_ln[q,k,:] . WZ[h,:] + BZ[h]
+ * With apply_ln == 0 the input is taken as already normalized (the reference's bias kernel).
+ */
+int tops_tri_ln_bias(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
+                     const void* WZ, const float* BZ, void* x_ln, void* bias, int64_t N, int64_t C, int64_t H,
+                     float eps, int dtype, void* stream);
+
+/*
+ * triangle_attention core (starting node).  Replaces `triangle_attn_kernel`
+ * (triangle_attn/kernel.py:110-253, launched at :335-373).
+ *   x_ln   io   (N, N, C) contiguous, C == 128
+ *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T (feature-major)
+ *   bias   io   (H, N, N) from tops_tri_ln_bias
+ *   mask   int8 (N, N) with strides (sm0, sm1), nonzero = valid key, or NULL
+ *   out    io   O[i, q, h*D + d] at out[i*so0 + q*so1 + h*D + d]
+ * out[i,q,h] = softmax_k(scale * Q.K + bias[h,q,k] - 1e9 * (mask[i,k] == 0)) V, D == 32.
+ */
+int tops_tri_attention(const void* x_ln, const void* wqkv, const void* bias, const void* mask, int64_t sm0,
+                       int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t C, int64_t H, int64_t D,
+                       float scale, int dtype, void* stream);
+
+/*
+ * Gate + output projection over M1*M2 tokens.  Replaces `fused_gate_forward` /
+ * `fused_gate_kernel` (triangle_attn/kernel.py:387-470) and the apb epilogue
+ * (attn_pair_bias/module.py:69-70):
+ *   out[t] = ((o[t] * sigmoid(gin[t] Wg^T + bg)) -> io) Wo^T + bo
+ *   o      io   token (m1, m2) at o[m1*so0 + m2*so1 + c], c < C
+ *   gin    io   (M1*M2, C) contiguous;  Wg, Wo io (C, C) in (out, in) layout;  bg, bo io (C,) or NULL
+ *   out    io   (M1*M2, C) contiguous.  C == 128.
+ */
+int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, const void* Wg, const void* bg,
+                  const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2, int64_t C, int dtype,
+                  void* stream);
+
+/*
+ * attention_pair_bias core.  Replaces `apb_forward` + `_apb_kernel`
+ * (attn_pair_bias/kernel.py:205-257, :24-202).
+ *   X      io   (M, C) contiguous, C == 128;  W_QKV io (C, 3*H*D) per-head [Q_h | K_h | V_h]
+ *   Z      io   element (q, k, c) at Z[q*sz0 + k*sz1 + c], c < Cz, Cz == 128
+ *   Wc     fp32 (H, Cz) LN-folded bias weight;  sWc, Bc fp32 (H,)
+ *   mask   int8 (M,) key mask (nonzero = valid) or NULL; masked keys get -inf
+ *   Og     io   (M, H*D) contiguous: softmax_k(scale * Q.K + LN(Z[q,k]) . W + b) V
+ *   work   device scratch of tops_apb_workspace_bytes(M, H, D) bytes (caller-owned)
+ */
+int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D);
+int tops_apb_forward(const void* X, const void* W_QKV, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
+                     const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M, int64_t C,
+                     int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIANGLEOPS_AMD_H */

@@ -1,0 +1,267 @@
+"""GPU parity: each op through the HIP library vs the CPU fp32 oracle on the same seeded inputs.
+
+Bar (written here, applied to every output element): bf16 max|out - oracle| <= 3e-2 and
+cosine >= 0.9999 (fp16: max|diff| <= 1e-2).  Masking is checked bit-exactly where the
+semantics fix it: masked tokens give exact zeros in the triangle_mul gated projection, and a
+padded+masked problem restricted to its valid block equals the cropped problem bitwise.
+Large configurations are checked on a sample of output rows (rows are independent).
+"""
+
+import pytest
+import torch
+from _inputs import TOL_COS, TOL_MAX_ABS, apb_inputs, compare, pad_pair_mask, tmu_inputs, to_dev, tri_inputs
+
+import triangleops_amd as tops
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+TMU_W = ("norm_in_weight", "norm_in_bias", "p_in_weight", "g_in_weight", "norm_out_weight", "norm_out_bias",
+         "p_out_weight", "g_out_weight")
+
+
+def _check(out, expect, dtype, what):
+    diff, cos = compare(out, expect)
+    assert torch.isfinite(out.float()).all(), f"{what}: non-finite output"
+    assert diff <= TOL_MAX_ABS[dtype] and cos >= TOL_COS, f"{what}: max|d|={diff:.3e} cos={cos:.6f}"
+    return diff, cos
+
+
+# --------------------------------------------------------------------------- #
+# triangle_multiplicative_update
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("L", [33, 64, 130, 256])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("mask", ["none", "pad", "random"])
+def test_tmu_matches_oracle(device, L, direction, mask):
+    x, m, w = tmu_inputs(L, seed=L, mask=mask)
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction,
+                                              mask=None if m is None else m.to(device), **to_dev(w, device))
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.bfloat16, f"tmu L={L} {direction} mask={mask}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_fp16(device, dtype, direction):
+    x, m, w = tmu_inputs(96, seed=5, mask="random", dtype=dtype)
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device))
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, dtype, f"tmu fp16 {direction}")
+
+
+def test_tmu_batch(device):
+    x, m, w = tmu_inputs(48, B=3, seed=7, mask="random")
+    for direction in ("outgoing", "incoming"):
+        out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                                  **to_dev(w, device))
+        expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+        _check(out, expect, torch.bfloat16, f"tmu B=3 {direction}")
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+def test_tmu_input_phase_and_mask_zeros(device, transpose):
+    """Gated projection vs oracle; masked tokens are exactly zero (bit-exact masking)."""
+    L = 80
+    x, m, w = tmu_inputs(L, seed=3, mask="random")
+    pre = tops.triangle_mul.precompute(*[w[k].to(device) for k in TMU_W])
+    ld = 128
+    ab = tops.triangle_mul.input_phase(to_dev(x, device), m.to(device), pre["p_in_combined"], pre["g_in_combined"],
+                                       pre["sum_W_p_in"], pre["sum_W_g_in"], pre["B_p_in_const"],
+                                       pre["B_g_in_const"], 1e-5, transpose=transpose, ld=ld)
+    ab = ab.cpu()
+    assert torch.all(ab[..., L:] == 0), "padding columns must be zero"
+    ab = ab[..., :L]
+    if transpose:
+        ab = ab.transpose(-1, -2)
+    g = ref.tmu_gated_input(x, m, w["norm_in_weight"], w["norm_in_bias"], w["p_in_weight"], w["g_in_weight"])
+    _check(ab.permute(1, 2, 3, 0), g, torch.bfloat16, "tmu input phase")
+    masked = ~m
+    assert torch.all(ab.permute(1, 2, 3, 0)[masked] == 0), "masked tokens must be exactly zero"
+
+
+def test_tmu_default_layout_low_level(device):
+    """Reference-layout low-level path: input_phase (2C,B,L,L) -> torch einsum -> output_phase."""
+    L = 72
+    x, m, w = tmu_inputs(L, seed=9, mask="pad")
+    xd = to_dev(x, device)
+    pre = tops.triangle_mul.precompute(*[w[k].to(device) for k in TMU_W])
+    ab = tops.triangle_mul.input_phase(xd, m.to(device), pre["p_in_combined"], pre["g_in_combined"],
+                                       pre["sum_W_p_in"], pre["sum_W_g_in"], pre["B_p_in_const"],
+                                       pre["B_g_in_const"], 1e-5)
+    assert ab.shape == (256, 1, L, L)
+    a, b = torch.chunk(ab.float(), 2, 0)
+    y = torch.einsum("dbik,dbjk->dbij", a, b).to(torch.bfloat16).contiguous()
+    out = tops.triangle_mul.output_phase(y, xd, pre["p_out_combined"], pre["g_out_combined"], pre["sum_W_p_out"],
+                                         pre["sum_W_g_out"], pre["B_p_out_const"], pre["B_g_out_const"], 1e-5)
+    expect = ref.triangle_multiplicative_update(x, direction="outgoing", mask=m, **w)
+    _check(out, expect, torch.bfloat16, "tmu low-level reference layout")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_pad_crop_bitwise(device, direction):
+    """op(x, padding mask)[valid block] == op(x[valid block]) bitwise."""
+    L, Lv = 128, 100
+    x, _, w = tmu_inputs(L, seed=11, mask="none")
+    idx = torch.arange(L)
+    m = ((idx[:, None] < Lv) & (idx[None, :] < Lv)).unsqueeze(0)
+    wd = to_dev(w, device)
+    full = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device), **wd)
+    crop = tops.triangle_multiplicative_update(to_dev(x[:, :Lv, :Lv].contiguous(), device), direction=direction,
+                                               mask=None, **wd)
+    assert torch.equal(full[:, :Lv, :Lv], crop)
+
+
+def test_tmu_precompute_forward_matches_oneshot(device):
+    x, m, w = tmu_inputs(256, seed=1, mask="ones")
+    xd, md, wd = to_dev(x, device), m.to(device), to_dev(w, device)
+    pre = tops.triangle_mul.precompute(*[wd[k] for k in TMU_W])
+    a = tops.triangle_mul.forward(xd, pre, direction="outgoing", mask=md)
+    b = tops.triangle_multiplicative_update(xd, direction="outgoing", mask=md, **wd)
+    assert torch.equal(a, b)
+    assert torch.equal(a, tops.triangle_mul.forward(xd, pre, direction="outgoing", mask=md)), "not deterministic"
+
+
+@pytest.mark.parametrize("L", [512, 1024])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_config_sizes_sampled_rows(device, L, direction):
+    """BASELINE config 1 sizes (pad mask), checked on 6 sampled output rows."""
+    x, m, w = tmu_inputs(L, seed=0, mask="pad")
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device))
+    rows = torch.tensor([0, 1, L // 3, L // 2, L - L // 10 - 1, L - 1])
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, rows=rows, **w)
+    _check(out[:, rows].cpu(), expect, torch.bfloat16, f"tmu L={L} {direction}")
+
+
+# --------------------------------------------------------------------------- #
+# triangle_attention
+# --------------------------------------------------------------------------- #
+def _tri_call(inp, device, X=None, mask="inp"):
+    d = to_dev(inp, device)
+    return tops.triangle_attention(d["X"] if X is None else X, d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"],
+                                   d["W_proj_z"], d["B_proj_z"], d["W_proj_g"], None, d["W_proj_o"], None, d["H"],
+                                   d["D"], scale=d["scale"], eps=1e-5, mask=d["mask"] if mask == "inp" else mask)
+
+
+def _tri_ref(inp, X=None, mask="inp", rows=None):
+    return ref.triangle_attention(inp["X"] if X is None else X, inp["W_ln"], inp["B_ln"], inp["WQ"], inp["WK"],
+                                  inp["WV"], inp["W_proj_z"], inp["B_proj_z"], inp["W_proj_g"], None, inp["W_proj_o"],
+                                  None, inp["H"], inp["D"], scale=inp["scale"], eps=1e-5,
+                                  mask=inp["mask"] if mask == "inp" else mask, rows=rows)
+
+
+@pytest.mark.parametrize("N", [33, 128, 130, 256])
+@pytest.mark.parametrize("mask", ["none", "pad", "random"])
+def test_tri_matches_oracle(device, N, mask):
+    inp = tri_inputs(N, seed=N, mask=mask, bias_z=True)
+    out = _tri_call(inp, device)
+    _check(out, _tri_ref(inp), torch.bfloat16, f"tri N={N} mask={mask}")
+
+
+def test_tri_fp16(device):
+    inp = tri_inputs(96, seed=4, mask="random", dtype=torch.float16)
+    _check(_tri_call(inp, device), _tri_ref(inp), torch.float16, "tri fp16")
+
+
+def test_tri_ending_node(device):
+    """Ending node = op on X^T (a strided view, no copy) with mask^T, output transposed back."""
+    N = 160
+    inp = tri_inputs(N, seed=21, mask="pad")
+    Xd = inp["X"].to(device)
+    out = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T).transpose(0, 1)
+    expect = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T).transpose(0, 1)
+    _check(out, expect, torch.bfloat16, "tri ending node")
+
+
+def test_tri_masked_rows_uniform_and_pad_crop(device):
+    """Fully masked rows average V uniformly; valid block equals the cropped problem bitwise."""
+    N, Nv = 128, 96
+    inp = tri_inputs(N, seed=5, mask="none")
+    idx = torch.arange(N)
+    m = (idx[:, None] < Nv) & (idx[None, :] < Nv)
+    full = _tri_call(inp, device, mask=m.to(device))
+    crop_inp = dict(inp, X=inp["X"][:Nv, :Nv].contiguous(), mask=None)
+    crop = _tri_call(crop_inp, device)
+    assert torch.equal(full[:Nv, :Nv], crop)
+    _check(full, _tri_ref(inp, mask=m), torch.bfloat16, "tri padded rows")
+
+
+def test_tri_low_level_entry_points(device):
+    """triangle_attn_forward + fused_gate_forward reproduce forward() (reference call sequence)."""
+    N = 64
+    inp = to_dev(tri_inputs(N, seed=8, mask="random"), device)
+    H, D = inp["H"], inp["D"]
+    pre = tops.triangle_attn.precompute(inp["W_ln"], inp["B_ln"], inp["WQ"], inp["WK"], inp["WV"], inp["W_proj_z"],
+                                        inp["B_proj_z"], H, D)
+    X_ln = torch.nn.functional.layer_norm(inp["X"], (128,), inp["W_ln"], inp["B_ln"], 1e-5)
+    O = torch.empty(N, N, H * D, device=device, dtype=torch.bfloat16)
+    tops.triangle_attn.triangle_attn_forward(X_ln, pre["WQ_c"], pre["WKV_c"], pre["WZ_c"], pre["BZ"], O,
+                                             scale=inp["scale"], mask=inp["mask"])
+    out = tops.triangle_attn.fused_gate_forward(O.view(N, N, H, D), X_ln, inp["W_proj_g"], inp["W_proj_o"])
+    _check(out, _tri_ref(to_dev(inp, "cpu")), torch.bfloat16, "tri low-level")
+
+
+@pytest.mark.parametrize("N", [512, 1024, 2048])
+def test_tri_config_sizes_sampled_rows(device, N):
+    """BASELINE configs 3/4 sizes (pad mask): starting node on sampled rows; ending node at N <= 1024."""
+    inp = tri_inputs(N, seed=0, mask="pad")
+    out = _tri_call(inp, device)
+    rows = torch.tensor([0, N // 2, N - N // 10 - 1, N - 1])
+    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} start")
+    if N <= 1024:
+        Xd = inp["X"].to(device)
+        out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
+        exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T, rows=rows)
+        _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri N={N} end")
+
+
+# --------------------------------------------------------------------------- #
+# attention_pair_bias
+# --------------------------------------------------------------------------- #
+def _apb_call(inp, device, mask="inp"):
+    d = to_dev(inp, device)
+    return tops.attention_pair_bias(d["X"], d["WQ"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                    d["B_proj_z"], d["W_proj_g"], d["B_proj_g"], d["W_proj_o"], d["B_proj_o"], d["H"],
+                                    d["D"], scale=d["scale"], eps=1e-5, mask=d["mask"] if mask == "inp" else mask)
+
+
+def _apb_ref(inp, rows=None):
+    return ref.attention_pair_bias(inp["X"], inp["WQ"], inp["WK"], inp["WV"], inp["Z"], inp["W_ln"], inp["B_ln"],
+                                   inp["W_proj_z"], inp["B_proj_z"], inp["W_proj_g"], inp["B_proj_g"],
+                                   inp["W_proj_o"], inp["B_proj_o"], inp["H"], inp["D"], scale=inp["scale"], eps=1e-5,
+                                   mask=inp["mask"], rows=rows)
+
+
+@pytest.mark.parametrize("M", [40, 128, 200, 512])
+@pytest.mark.parametrize("mask", ["none", "pad", "random"])
+@pytest.mark.parametrize("biases", [False, True])
+def test_apb_matches_oracle(device, M, mask, biases):
+    inp = apb_inputs(M, seed=M, mask=mask, biases=biases)
+    _check(_apb_call(inp, device), _apb_ref(inp), torch.bfloat16, f"apb M={M} mask={mask} biases={biases}")
+
+
+def test_apb_fp16(device):
+    inp = apb_inputs(160, seed=6, mask="random", biases=True, dtype=torch.float16)
+    _check(_apb_call(inp, device), _apb_ref(inp), torch.float16, "apb fp16")
+
+
+def test_apb_precompute_forward_matches_oneshot(device):
+    inp = to_dev(apb_inputs(256, seed=2, mask="none"), device)
+    pre = tops.attn_pair_bias.precompute(inp["WQ"], inp["WK"], inp["WV"], inp["W_ln"], inp["B_ln"], inp["W_proj_z"],
+                                         inp["B_proj_z"], inp["H"], inp["D"])
+    a = tops.attn_pair_bias.forward(inp["X"], inp["Z"], pre, scale=1.0, W_proj_g=inp["W_proj_g"],
+                                    B_proj_g=inp["B_proj_g"], W_proj_o=inp["W_proj_o"], B_proj_o=inp["B_proj_o"])
+    b = tops.attention_pair_bias(inp["X"], inp["WQ"], inp["WK"], inp["WV"], inp["Z"], inp["W_ln"], inp["B_ln"],
+                                 inp["W_proj_z"], inp["B_proj_z"], inp["W_proj_g"], inp["B_proj_g"], inp["W_proj_o"],
+                                 inp["B_proj_o"], inp["H"], inp["D"], scale=1.0)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1024, 2048])
+def test_apb_config_sizes_sampled_rows(device, M):
+    inp = apb_inputs(M, seed=0, mask="pad")
+    out = _apb_call(inp, device)
+    rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
+    _check(out[rows].cpu(), _apb_ref(inp, rows=rows), torch.bfloat16, f"apb M={M}")

@@ -1,0 +1,121 @@
+"""ctypes binding of `libtriangleops_amd.so` (the C ABI declared in include/triangleops_amd.h).
+
+The library is loaded on first use.  There is no fallback: if it is missing or cannot be
+loaded, every op raises ImportError naming the build command.  Each call passes raw device
+pointers and torch's current HIP stream; a non-zero return code becomes RuntimeError with
+the library's message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtriangleops_amd.so")
+ABI_VERSION = 1
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+# name -> argtypes (all return int status codes except where noted)
+_SIGNATURES = {
+    "tops_tmu_input_phase": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _p],
+    "tops_tmu_einsum": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
+    "tops_tmu_output_phase": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
+    "tops_tri_ln_bias": [_p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p],
+    "tops_tri_attention": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
+    "tops_gate_out": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "tops_apb_forward": [
+        _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
+    ],
+}
+_OTHER = {
+    "tops_last_error": ([], ctypes.c_char_p),
+    "tops_abi_version": ([], ctypes.c_int),
+    "tops_apb_workspace_bytes": ([_i64, _i64, _i64], ctypes.c_int64),
+}
+
+EXPORTED = tuple(_SIGNATURES) + tuple(_OTHER)
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Loads the library (once) and declares the prototypes; raises ImportError if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(
+            f"triangleops_amd: HIP library not found at {path}; build it with "
+            "`python -m triangleops_amd._build` (hipcc, gfx950)"
+        )
+    try:
+        lib = ctypes.CDLL(path)
+    except OSError as e:
+        raise ImportError(f"triangleops_amd: cannot load {path}: {e}") from e
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    for name, (argtypes, restype) in _OTHER.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    if lib.tops_abi_version() != ABI_VERSION:
+        raise ImportError(f"triangleops_amd: ABI version mismatch ({lib.tops_abi_version()} != {ABI_VERSION})")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Calls C entry point `name`; raises RuntimeError with the library's message on failure."""
+    lib = _lib if _lib is not None else load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.tops_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (code {rc}): {msg}")
+
+
+def apb_workspace_bytes(M: int, H: int, D: int) -> int:
+    lib = _lib if _lib is not None else load()
+    return int(lib.tops_apb_workspace_bytes(M, H, D))
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on `t`'s device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def check_device(*tensors) -> None:
+    """All tensors must be on one GPU (the kernels dereference raw device pointers)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"triangleops_amd kernels need GPU tensors (got a tensor on {t.device})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"all tensors must be on one device (got {dev} and {t.device})")
+
+
+def mask_i8(mask: torch.Tensor | None) -> torch.Tensor | None:
+    """Mask as int8 storage without a copy for bool/int8/uint8 contiguous masks."""
+    if mask is None:
+        return None
+    m = mask if mask.is_contiguous() else mask.contiguous()
+    if m.dtype in (torch.bool, torch.uint8):
+        return m.view(torch.int8)
+    if m.dtype == torch.int8:
+        return m
+    return m.to(torch.int8)

@@ -1,0 +1,93 @@
+"""Public API of attention with pair bias on gfx950.
+
+Drop-in for `triangle_ops/attn_pair_bias/module.py` of the reference: same `precompute`,
+`forward` and one-shot signatures and precompute keys (W_QKV, W_combined, sum_W_combined,
+B_const), plus `wqkv_hm` (the head-major weight the kernel loads).  Two launches per call
+(three when the key range is split for parallelism): the fused QKV + LN(Z) bias + attention
+kernel, and the gate + W_o kernel.
+
+Additive extension: `forward(..., mask=None)` / `attention_pair_bias(..., mask=None)` take an
+optional (M,) key mask (masked keys -> -inf, as the reference's K-Fold variant does at
+`benchmarks/references.py:273-274`); without it the behaviour is the reference's.
+"""
+
+import torch
+
+from .._common.layouts import interleave_qkv, qkv_head_major
+from .._common.ln_absorption import absorb_ln_matmul
+from ..triangle_attn.kernel import gate_out_forward
+from .kernel import apb_forward
+
+
+def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
+    """One-time weight fusion.  Returns W_QKV (C, 3HD), W_combined (H, Cz) fp32, sum_W_combined (H,), B_const (H,)."""
+    W_QKV = interleave_qkv(WQ, WK, WV, H, D)
+    W_combined, sum_W_combined, B_const = absorb_ln_matmul(W_proj_z, W_ln, B_ln, weight_dtype=torch.float32)
+    W_combined = W_combined.t().contiguous()
+    if B_proj_z is not None:
+        B_const = B_const + B_proj_z.float()
+    return {
+        "W_QKV": W_QKV,
+        "W_combined": W_combined,
+        "sum_W_combined": sum_W_combined,
+        "B_const": B_const.contiguous(),
+        "wqkv_hm": qkv_head_major(WQ, WK, WV, H, D),
+    }
+
+
+def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, mask=None):
+    """Per-call forward.  X (M, C_s), Z (M, M, C_z) -> (M, C_out)."""
+    M = X.shape[0]
+    H = pre["sum_W_combined"].shape[0]
+    D = pre["W_QKV"].shape[1] // (3 * H)
+    Og = torch.empty(M, H * D, device=X.device, dtype=X.dtype)
+    apb_forward(
+        X,
+        pre["W_QKV"],
+        Z,
+        pre["W_combined"],
+        pre["sum_W_combined"],
+        pre["B_const"],
+        Og,
+        scale=scale,
+        eps=eps,
+        mask=mask,
+        wqkv_hm=pre.get("wqkv_hm"),
+    )
+    return gate_out_forward(Og.view(M, 1, H * D), X, W_proj_g, B_proj_g, W_proj_o, B_proj_o).view(M, -1)
+
+
+def attention_pair_bias(
+    X,
+    WQ,
+    WK,
+    WV,
+    Z,
+    W_ln,
+    B_ln,
+    W_proj_z,
+    B_proj_z,
+    W_proj_g,
+    B_proj_g,
+    W_proj_o,
+    B_proj_o,
+    H,
+    D,
+    scale=1.0,
+    eps=1e-5,
+    mask=None,
+):
+    """One-shot (precompute included).  For amortized latency call `precompute` once, then `forward`."""
+    pre = precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D)
+    return forward(
+        X,
+        Z,
+        pre,
+        scale=scale,
+        eps=eps,
+        W_proj_g=W_proj_g,
+        B_proj_g=B_proj_g,
+        W_proj_o=W_proj_o,
+        B_proj_o=B_proj_o,
+        mask=mask,
+    )
