@@ -1,0 +1,509 @@
+"""Benchmark of the triangleops_amd hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep FILE] [--no-cpu-baseline]
+
+Default workload (the configuration its metric is quoted on):
+triangle_multiplicative_update in bf16 at L = 1024, C = 128, B = 1, pad mask zeroing the last
+10% of rows/cols, random-init LayerNorm / projection weights.  One step = one outgoing call
+plus one incoming call (the two directions a Pairformer block runs).  Inputs are resident in
+HBM before timing; the precompute (weight folding) is outside the timed region.
+
+Prints ONE JSON line with the contract fields plus:
+  roofline      dominant kernel of the step (largest average launch time), its algorithmic
+                work per launch over its average HIP-event-timed duration, vs the MI355X peak
+                (bf16 dense MFMA 2.5 PFLOP/s, HBM 8 TB/s);
+  kernels       the same figures for each kernel of the step;
+  torch_path_ms the reference's pure-torch bf16 formulation on the same GPU;
+  cpu_baseline  the fp32 CPU oracle on this host (one full outgoing call at the same size).
+`--sweep FILE` additionally times all three ops at sizes 128..2048 (ours, the torch path and
+per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import triangleops_amd as tops  # noqa: E402
+from triangleops_amd.attn_pair_bias.kernel import apb_forward  # noqa: E402
+from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, ln_bias_forward  # noqa: E402
+from triangleops_amd.triangle_mul.kernel import input_phase, output_phase, triangle_einsum  # noqa: E402
+
+METRIC = "per-call ms + MFMA util % for each op at N/L/M=128–2048 (bf16, 1 GPU)"
+PEAK_MFMA_BF16 = 2500.0  # TFLOP/s, MI355X dense bf16
+PEAK_HBM = 8000.0  # GB/s
+C = 128
+H, D = 4, 32
+
+TMU_KEYS = ("norm_in_weight", "norm_in_bias", "p_in_weight", "g_in_weight", "norm_out_weight", "norm_out_bias",
+            "p_out_weight", "g_out_weight")
+
+
+# --------------------------------------------------------------------------- #
+# inputs (CPU generator, seed 0, fixed draw order; rounded to bf16 once)
+# --------------------------------------------------------------------------- #
+def _gen(seed=0):
+    return torch.Generator().manual_seed(seed)
+
+
+def pad_mask2(n, frac=10):
+    v = n - n // frac
+    i = torch.arange(n)
+    return (i[:, None] < v) & (i[None, :] < v)
+
+
+def tmu_inputs(L, seed=0):
+    g = _gen(seed)
+    x = torch.randn(1, L, L, C, generator=g).to(torch.bfloat16)
+    s = C**-0.5
+    w = {
+        "p_in_weight": torch.randn(2 * C, C, generator=g) * s,
+        "g_in_weight": torch.randn(2 * C, C, generator=g) * s,
+        "p_out_weight": torch.randn(C, C, generator=g) * s,
+        "g_out_weight": torch.randn(C, C, generator=g) * s,
+        "norm_in_weight": 1 + 0.1 * torch.randn(C, generator=g),
+        "norm_in_bias": 0.1 * torch.randn(C, generator=g),
+        "norm_out_weight": 1 + 0.1 * torch.randn(C, generator=g),
+        "norm_out_bias": 0.1 * torch.randn(C, generator=g),
+    }
+    w = {k: v.to(torch.bfloat16) for k, v in w.items()}
+    return x, pad_mask2(L).unsqueeze(0), w
+
+
+def tri_inputs(N, seed=0):
+    g = _gen(seed)
+    s = C**-0.5
+    d = dict(
+        X=torch.randn(N, N, C, generator=g),
+        W_ln=1 + 0.1 * torch.randn(C, generator=g),
+        B_ln=0.1 * torch.randn(C, generator=g),
+        WQ=torch.randn(C, H * D, generator=g) * s,
+        WK=torch.randn(C, H * D, generator=g) * s,
+        WV=torch.randn(C, H * D, generator=g) * s,
+        W_proj_z=torch.randn(C, H, generator=g) * s,
+        B_proj_z=torch.zeros(H),
+        W_proj_g=torch.randn(H * D, C, generator=g) * s,
+        W_proj_o=torch.randn(C, H * D, generator=g) * (H * D) ** -0.5,
+    )
+    d = {k: v.to(torch.bfloat16) for k, v in d.items()}
+    d["mask"] = pad_mask2(N)
+    return d
+
+
+def apb_inputs(M, seed=0):
+    g = _gen(seed)
+    s = C**-0.5
+    d = dict(
+        X=torch.randn(M, C, generator=g),
+        Z=torch.randn(M, M, C, generator=g),
+        WQ=torch.randn(C, H * D, generator=g) * s,
+        WK=torch.randn(C, H * D, generator=g) * s,
+        WV=torch.randn(C, H * D, generator=g) * s,
+        W_ln=1 + 0.1 * torch.randn(C, generator=g),
+        B_ln=0.1 * torch.randn(C, generator=g),
+        W_proj_z=torch.randn(C, H, generator=g) * s,
+        B_proj_z=torch.zeros(H),
+        W_proj_g=torch.randn(H * D, C, generator=g) * s,
+        B_proj_g=torch.zeros(H * D),
+        W_proj_o=torch.randn(C, H * D, generator=g) * (H * D) ** -0.5,
+        B_proj_o=torch.zeros(C),
+    )
+    d = {k: v.to(torch.bfloat16) for k, v in d.items()}
+    d["mask"] = torch.arange(M) < M - M // 20
+    return d
+
+
+def to_dev(d, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+
+
+# --------------------------------------------------------------------------- #
+# the reference's pure-torch bf16 path (benchmarks/references.py:143-221), restated.
+# Batched products use contiguous operands and matmul (no einsum over transposed views).
+# The tri_attn mask add is cast to the scores dtype (the reference's fp32 add fails in bf16).
+# --------------------------------------------------------------------------- #
+def torch_tmu(x, direction, mask, eps=1e-5, **w):
+    xln = F.layer_norm(x, (C,), w["norm_in_weight"], w["norm_in_bias"], eps=eps)
+    g = F.linear(xln, w["p_in_weight"]) * F.linear(xln, w["g_in_weight"]).sigmoid()
+    g = g * mask.unsqueeze(-1)
+    a, b = torch.chunk(g, 2, dim=-1)
+    if direction == "outgoing":
+        A = a.permute(0, 3, 1, 2).contiguous()  # b d i k
+        Bm = b.permute(0, 3, 2, 1).contiguous()  # b d k j
+    else:
+        A = a.permute(0, 3, 2, 1).contiguous()  # b d i k  (a[b,k,i,d])
+        Bm = b.permute(0, 3, 1, 2).contiguous()  # b d k j  (b[b,k,j,d])
+    y = torch.matmul(A, Bm).permute(0, 2, 3, 1)
+    yln = F.layer_norm(y, (C,), w["norm_out_weight"], w["norm_out_bias"], eps=eps)
+    return F.linear(yln, w["p_out_weight"]) * F.linear(xln, w["g_out_weight"]).sigmoid()
+
+
+def torch_tri(d, eps=1e-5):
+    X = d["X"]
+    N = X.shape[0]
+    xln = F.layer_norm(X, (C,), d["W_ln"], d["B_ln"], eps=eps)
+    q = (xln @ d["WQ"]).view(N, N, H, D).permute(0, 2, 1, 3)
+    k = (xln @ d["WK"]).view(N, N, H, D).permute(0, 2, 3, 1).contiguous()
+    v = (xln @ d["WV"]).view(N, N, H, D).permute(0, 2, 1, 3).contiguous()
+    bp = (xln @ d["W_proj_z"] + d["B_proj_z"]).permute(2, 0, 1).unsqueeze(0)
+    scores = torch.matmul((q * D**-0.5).contiguous(), k) + bp
+    scores = scores + torch.where(d["mask"][:, None, None, :], 0.0, -1e9).to(scores.dtype)
+    o = torch.matmul(torch.softmax(scores, -1), v).permute(0, 2, 1, 3).reshape(N, N, H * D)
+    g = torch.sigmoid(F.linear(xln, d["W_proj_g"]))
+    return F.linear(o * g, d["W_proj_o"])
+
+
+def torch_apb(d, eps=1e-5):
+    X, Z = d["X"], d["Z"]
+    M = X.shape[0]
+    q = (X @ d["WQ"]).reshape(M, H, D).permute(1, 0, 2)
+    k = (X @ d["WK"]).reshape(M, H, D).permute(1, 2, 0).contiguous()
+    v = (X @ d["WV"]).reshape(M, H, D).permute(1, 0, 2).contiguous()
+    bp = (F.layer_norm(Z, (C,), d["W_ln"], d["B_ln"], eps=eps) @ d["W_proj_z"] + d["B_proj_z"]).permute(2, 0, 1)
+    scores = torch.matmul((q * D**-0.5).contiguous(), k) + bp
+    scores = scores.masked_fill(~d["mask"][None, None, :], float("-inf"))
+    o = torch.matmul(torch.softmax(scores, -1), v).permute(1, 0, 2).reshape(M, H * D)
+    g = torch.sigmoid(F.linear(X, d["W_proj_g"], d["B_proj_g"]))
+    return F.linear(g * o, d["W_proj_o"], d["B_proj_o"])
+
+
+# --------------------------------------------------------------------------- #
+# timing helpers
+# --------------------------------------------------------------------------- #
+def time_ms(fn, iters, warmup):
+    """Median per-call ms via HIP events on the current stream; NaN on OOM."""
+    try:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e))
+        return statistics.median(ts)
+    except torch.OutOfMemoryError:
+        torch.cuda.empty_cache()
+        return float("nan")
+
+
+class PhaseTimer:
+    """Records HIP events between the launches of one call; averages each phase over calls."""
+
+    def __init__(self, names):
+        self.names = names
+        self.events = []
+
+    def run(self, phases):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)]
+        ev[0].record()
+        for i, ph in enumerate(phases):
+            ph()
+            ev[i + 1].record()
+        self.events.append(ev)
+
+    def averages(self):
+        torch.cuda.synchronize()
+        out = {}
+        for i, n in enumerate(self.names):
+            out[n] = statistics.fmean(ev[i].elapsed_time(ev[i + 1]) for ev in self.events)
+        return out
+
+
+def kernel_entry(name, ms, bound, work):
+    """Roofline figures of one kernel: work = algorithmic bytes (hbm) or flops (mfma) per launch."""
+    if bound == "mfma":
+        achieved = work / (ms * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_MFMA_BF16, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_MFMA_BF16, 4), "ms": round(ms, 4), "work": work}
+    achieved = work / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM, 4), "ms": round(ms, 4), "work": work}
+
+
+# --------------------------------------------------------------------------- #
+# per-op phase decompositions (exactly the launches forward() issues)
+# --------------------------------------------------------------------------- #
+def tmu_phases(x, m, pre, direction):
+    L = x.shape[1]
+    ld = max(64, (L + 63) // 64 * 64)
+    st = {}
+
+    def p_in():
+        st["ab"] = input_phase(x, m, pre["p_in_combined"], pre["g_in_combined"], pre["sum_W_p_in"],
+                               pre["sum_W_g_in"], pre["B_p_in_const"], pre["B_g_in_const"], 1e-5,
+                               transpose=direction == "incoming", ld=ld)
+
+    def p_ein():
+        st["y"] = triangle_einsum(st["ab"], L, ld, C, 1)
+
+    def p_out():
+        st["out"] = output_phase(st["y"], x, pre["p_out_combined"], pre["g_out_combined"], pre["sum_W_p_out"],
+                                 pre["sum_W_g_out"], pre["B_p_out_const"], pre["B_g_out_const"], 1e-5, ldy=ld)
+
+    return [p_in, p_ein, p_out]
+
+
+def tmu_work(L):
+    M = L * L
+    return {
+        "tmu_input_phase": ("hbm", 2 * M * C + M + 2 * M * 2 * C),
+        "tmu_einsum": ("mfma", 2 * C * L**3),
+        "tmu_output_phase": ("hbm", 3 * 2 * M * C),
+    }
+
+
+def tri_phases(d, pre):
+    st = {}
+    N = d["X"].shape[0]
+
+    def p_ln():
+        st["xln"], st["bias"] = ln_bias_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["WZ_c"], pre["BZ"])
+
+    def p_att():
+        st["o"] = torch.empty(N, N, H * D, device=d["X"].device, dtype=d["X"].dtype)
+        attention_core(st["xln"], pre["wqkv_hm"], st["bias"], st["o"], scale=D**-0.5, mask=d["mask"])
+
+    def p_gate():
+        st["out"] = gate_out_forward(st["o"], st["xln"], d["W_proj_g"], None, d["W_proj_o"], None)
+
+    return [p_ln, p_att, p_gate]
+
+
+def tri_work(N):
+    return {
+        "tri_ln_bias": ("hbm", 4 * N * N * C + 2 * H * N * N),
+        "tri_attention": ("mfma", 4 * N**3 * H * D + 6 * N * N * C * H * D),
+        "tri_gate_out": ("hbm", 6 * N * N * C),
+    }
+
+
+def apb_phases(d, pre):
+    st = {}
+    M = d["X"].shape[0]
+
+    def p_att():
+        st["og"] = torch.empty(M, H * D, device=d["X"].device, dtype=d["X"].dtype)
+        apb_forward(d["X"], pre["W_QKV"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"],
+                    st["og"], scale=D**-0.5, mask=d["mask"], wqkv_hm=pre["wqkv_hm"])
+
+    def p_gate():
+        st["out"] = gate_out_forward(st["og"].view(M, 1, H * D), d["X"], d["W_proj_g"], d["B_proj_g"],
+                                     d["W_proj_o"], d["B_proj_o"])
+
+    return [p_att, p_gate]
+
+
+def apb_work(M):
+    return {"apb_attention": ("hbm", 2 * M * M * C), "apb_gate_out": ("hbm", 3 * 2 * M * C)}
+
+
+def run_phases(phase_lists, names, iters, warmup):
+    """Times the phase lists (one list per call in a step); returns (avg ms per phase name)."""
+    for _ in range(warmup):
+        for pl in phase_lists:
+            for ph in pl:
+                ph()
+    torch.cuda.synchronize()
+    timers = [PhaseTimer(names) for _ in phase_lists]
+    for _ in range(iters):
+        for t, pl in zip(timers, phase_lists):
+            t.run(pl)
+    torch.cuda.synchronize()
+    avgs = [t.averages() for t in timers]
+    return {n: statistics.fmean(a[n] for a in avgs) for n in names}
+
+
+# --------------------------------------------------------------------------- #
+# CPU baseline (fp32 oracle on this host)
+# --------------------------------------------------------------------------- #
+def cpu_baseline_tmu(x, m, w, L, min_s=10.0):
+    from oracle import reference as oracle  # the checker, timed here as the CPU baseline
+
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(threads, 16))
+    torch.set_num_threads(threads)
+    calls, t0 = 0, time.perf_counter()
+    while True:  # repeat whole calls until at least min_s of CPU work has been timed
+        oracle.triangle_multiplicative_update(x, direction="outgoing", mask=m, **w)
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            break
+    return {"value": round(calls / dt, 5), "unit": "calls/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} full outgoing call(s) at L={L} (fp32 torch oracle), {dt:.1f} s"}
+
+
+# --------------------------------------------------------------------------- #
+def sweep(path, sizes, dev):
+    rows = []
+    with open(path, "w") as f:
+        for L in sizes:
+            torch.cuda.empty_cache()
+            x, m, w = tmu_inputs(L)
+            x, m, w = x.to(dev), m.to(dev), {k: v.to(dev) for k, v in w.items()}
+            pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+            it, wu = (20, 5) if L <= 1024 else (8, 3)
+            for direction in ("outgoing", "incoming"):
+                ms = time_ms(lambda: tops.triangle_mul.forward(x, pre, direction=direction, mask=m), it, wu)
+                tms = time_ms(lambda: torch_tmu(x, direction, m, **w), it, wu) if L <= 2048 else float("nan")
+                ph = run_phases([tmu_phases(x, m, pre, direction)], list(tmu_work(L)), it, wu)
+                kern = {n: kernel_entry(n, ph[n], *tmu_work(L)[n]) for n in ph}
+                r = {"op": "triangle_multiplicative_update", "direction": direction, "size": L, "ms": round(ms, 4),
+                     "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": kern}
+                f.write(json.dumps(r) + "\n")
+                f.flush()
+                rows.append(r)
+            del x, m, w, pre
+        for N in sizes:
+            torch.cuda.empty_cache()
+            d = to_dev(tri_inputs(N), dev)
+            pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                                d["B_proj_z"], H, D)
+            it, wu = (20, 5) if N <= 1024 else (6, 2)
+            fwd = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=D**-0.5,  # noqa: E731
+                                                     W_proj_g=d["W_proj_g"], B_proj_g=None,
+                                                     W_proj_o=d["W_proj_o"], B_proj_o=None)
+            ms = time_ms(fwd, it, wu)
+            ms_end = time_ms(lambda: tops.triangle_attn.forward(
+                d["X"].transpose(0, 1), pre, mask=d["mask"].T, scale=D**-0.5, W_proj_g=d["W_proj_g"],
+                B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None), it, wu)
+            tms = time_ms(lambda: torch_tri(d), max(3, it // 4), 1) if N <= 1024 else float("nan")
+            ph = run_phases([tri_phases(d, pre)], list(tri_work(N)), it, wu)
+            kern = {n: kernel_entry(n, ph[n], *tri_work(N)[n]) for n in ph}
+            r = {"op": "triangle_attention", "size": N, "ms": round(ms, 4), "ms_ending_node": round(ms_end, 4),
+                 "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": kern}
+            f.write(json.dumps(r) + "\n")
+            f.flush()
+            rows.append(r)
+            del d, pre
+        for M in sizes:
+            torch.cuda.empty_cache()
+            d = to_dev(apb_inputs(M), dev)
+            pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                                 d["B_proj_z"], H, D)
+            fwd = lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5,  # noqa: E731
+                                                      W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"],
+                                                      W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"], mask=d["mask"])
+            ms = time_ms(fwd, 20, 5)
+            tms = time_ms(lambda: torch_apb(d), 10, 2)
+            ph = run_phases([apb_phases(d, pre)], list(apb_work(M)), 20, 5)
+            kern = {n: kernel_entry(n, ph[n], *apb_work(M)[n]) for n in ph}
+            r = {"op": "attention_pair_bias", "size": M, "ms": round(ms, 4), "calls_per_s": round(1e3 / ms, 1),
+                 "torch_path_ms": round(tms, 4), "kernels": kern}
+            f.write(json.dumps(r) + "\n")
+            f.flush()
+            rows.append(r)
+            del d, pre
+    return rows
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--size", type=int, default=1024, help="L of the headline workload")
+    ap.add_argument("--sweep", default=None, help="also sweep all ops/sizes; JSON lines to this file")
+    ap.add_argument("--sweep-sizes", default="128,256,512,1024,2048")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-torch", action="store_true", help="skip the torch-path reference timing")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the ops are "
+              "single-GPU kernels and no multi-GPU path is part of it", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    L = args.size
+
+    x_c, m_c, w_c = tmu_inputs(L)
+    x, m = x_c.to(dev), m_c.to(dev)
+    w = {k: v.to(dev) for k, v in w_c.items()}
+    pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+    steps = [tmu_phases(x, m, pre, "outgoing"), tmu_phases(x, m, pre, "incoming")]
+    names = list(tmu_work(L))
+
+    # warmup
+    for _ in range(args.warmup):
+        for pl in steps:
+            for ph in pl:
+                ph()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps (outgoing + incoming), per-launch HIP events inside
+    timers = [PhaseTimer(names) for _ in steps]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        for t, pl in zip(timers, steps):
+            t.run(pl)
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    per_dir = [t.averages() for t in timers]
+    ph = {n: statistics.fmean(a[n] for a in per_dir) for n in names}
+    work = tmu_work(L)
+    kernels = {n: kernel_entry(n, ph[n], *work[n]) for n in names}
+    dominant = max(names, key=lambda n: ph[n])
+    kd = kernels[dominant]
+    roofline = {"kernel": dominant, "bound": kd["bound"], "achieved": kd["achieved"], "peak": kd["peak"],
+                "unit": kd["unit"], "frac": kd["frac"], "traffic": None}
+
+    torch_ms = {} if args.no_torch else {d: time_ms(lambda: torch_tmu(x, d, m, **w), 5, 2)
+                                          for d in ("outgoing", "incoming")}
+
+    out = {
+        "metric": METRIC,
+        "value": round(2 * args.steps / (total_ms * 1e-3), 2),
+        "unit": "calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_call": round(ms_per_step / 2, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, random-init weights)",
+        "config": {"workload": f"triangle_multiplicative_update bf16 outgoing+incoming, L={L}, C={C}, B=1, "
+                               "pad mask (last 10% rows/cols), one step = one call per direction",
+                   "L": L, "C": C, "B": 1},
+        "roofline": roofline,
+        "kernels": kernels,
+        "torch_path_ms": {k: round(v, 4) for k, v in torch_ms.items()},
+        "device": torch.cuda.get_device_name(dev),
+    }
+    del x, m, w, pre, steps, timers
+    torch.cuda.empty_cache()
+    if args.sweep:
+        sweep(args.sweep, [int(s) for s in args.sweep_sizes.split(",")], dev)
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

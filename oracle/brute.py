@@ -14,6 +14,7 @@ Python lists of floats.
 from __future__ import annotations
 
 import math
+import struct
 
 
 def _l(t):
@@ -36,6 +37,16 @@ def _lin(v, W, bias=None):
 def _matvec_in_out(v, W):
     """v (in,) @ W (in, out)."""
     return [sum(v[c] * W[c][o] for c in range(len(v))) for o in range(len(W[0]))]
+
+
+def _f32(v):
+    """Round a Python float to the nearest float32 value."""
+    return struct.unpack("f", struct.pack("f", v))[0]
+
+
+def _masked_score(s):
+    """The reference adds -1e9 to a masked score in fp32 (triangle_attn/kernel.py:230-237)."""
+    return _f32(_f32(s) + _f32(-1e9))
 
 
 def _sig(z):
@@ -107,7 +118,7 @@ def triangle_attention(X, W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, W_proj_g, 
                 for k in range(N):
                     s = sum(qv[q][h * D + d] * scale * kv[k][h * D + d] for d in range(D)) + bias[h][q][k]
                     if mask is not None and not mask[i][k]:
-                        s += -1e9
+                        s = _masked_score(s)
                     sc.append(s)
                 p = _softmax_weights(sc)
                 o.extend(sum(p[k] * vv[k][h * D + d] for k in range(N)) for d in range(D))

@@ -145,7 +145,7 @@ def tri_attention_core(xln, WQ, WK, WV, bias, H, D, scale=1.0, mask=None, dtype=
 
     xln (N, N, C), bias (H, N, N), mask (N, N) (nonzero = valid key) ->
     O (R, N, H*D) for rows i in `rows` (all rows by default), before gating.
-    Masked keys get -1e9 added to their scores (fp32), as the reference kernel does.
+    Masked keys get -1e9 added to their scores in fp32, as the reference kernel does.
     """
     xln, bias = _f(xln, dtype), _f(bias, dtype)
     WQ, WK, WV = _f(WQ, dtype), _f(WK, dtype), _f(WV, dtype)
@@ -161,8 +161,11 @@ def tri_attention_core(xln, WQ, WK, WV, bias, H, D, scale=1.0, mask=None, dtype=
         v = (xr @ WV).view(R, N, H, D).permute(0, 2, 1, 3)
         scores = torch.matmul(q * scale, k.transpose(-1, -2)) + bias.unsqueeze(0)
         if mask is not None:
-            valid = _f(mask, dtype)[r] != 0  # (R, N) over keys
-            scores = scores + torch.where(valid, 0.0, -1e9).to(dtype)[:, None, None, :]
+            # -1e9 is added in fp32, as the reference does, also when checking in float64:
+            # a row without valid keys then has all scores == -1e9 (uniform weights).
+            valid = (_f(mask, dtype)[r] != 0)[:, None, None, :]  # (R, 1, 1, N) over keys
+            masked = (scores.float() + torch.tensor(-1e9, dtype=torch.float32)).to(dtype)
+            scores = torch.where(valid, scores, masked)
         o = torch.matmul(torch.softmax(scores, -1), v)  # (R, H, N, D)
         outs.append(o.permute(0, 2, 1, 3).reshape(R, N, H * D))
     return torch.cat(outs, 0)

@@ -265,3 +265,47 @@ def test_apb_config_sizes_sampled_rows(device, M):
     out = _apb_call(inp, device)
     rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
     _check(out[rows].cpu(), _apb_ref(inp, rows=rows), torch.bfloat16, f"apb M={M}")
+
+
+# --------------------------------------------------------------------------- #
+# golden fixtures (brute-force float64 expected outputs, tests/golden)
+# --------------------------------------------------------------------------- #
+def _golden(name):
+    import os
+
+    import numpy as np
+
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name), allow_pickle=False)
+    inp = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("in_")}
+    meta = {k[5:]: z[k] for k in z.files if k.startswith("meta_")}
+    return inp, torch.from_numpy(z["expected"]), meta
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_golden_tmu_gpu(device, direction):
+    inp, expected, meta = _golden(f"tmu_{direction}.npz")
+    d = {k: v.to(torch.bfloat16).to(device) for k, v in inp.items() if k not in ("mask",)}
+    x = d.pop("x")
+    out = tops.triangle_multiplicative_update(x, direction=direction, mask=inp["mask"].to(device).bool(),
+                                              eps=float(meta["eps"]), **d)
+    _check(out, expected, torch.bfloat16, f"golden tmu {direction}")
+
+
+def test_golden_tri_gpu(device):
+    inp, expected, meta = _golden("tri_attn.npz")
+    d = {k: v.to(torch.bfloat16).to(device) for k, v in inp.items()}
+    out = tops.triangle_attention(d["X"], d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                  d["B_proj_z"], d["W_proj_g"], None, d["W_proj_o"], None, 4, 32,
+                                  scale=float(meta["scale"]), eps=float(meta["eps"]),
+                                  mask=inp["mask"].to(device).bool())
+    _check(out, expected, torch.bfloat16, "golden tri")
+
+
+def test_golden_apb_gpu(device):
+    inp, expected, meta = _golden("apb.npz")
+    d = {k: v.to(torch.bfloat16).to(device) for k, v in inp.items()}
+    out = tops.attention_pair_bias(d["X"], d["WQ"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                   d["B_proj_z"], d["W_proj_g"], d["B_proj_g"], d["W_proj_o"], d["B_proj_o"], 4, 32,
+                                   scale=float(meta["scale"]), eps=float(meta["eps"]),
+                                   mask=inp["mask"].to(device).bool())
+    _check(out, expected, torch.bfloat16, "golden apb")

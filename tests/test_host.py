@@ -1,0 +1,194 @@
+"""Host-side checks (CPU only): drop-in API surface, precompute contents, error behaviour,
+and that the C-ABI library exports every entry point the header declares."""
+
+import ctypes
+import inspect
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+import triangleops_amd as tops
+from triangleops_amd import _native
+from triangleops_amd._common import tl_io_dtype
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "triangleops_amd.h")
+
+# Public signatures of the reference API (triangle_ops/*/module.py and kernel.py), as
+# (parameter name, default or None, keyword-only) lists; the drop-in must accept the same calls.
+REF_SIGNATURES = {
+    "triangle_mul.triangle_multiplicative_update": "x, *, direction, mask=None, eps=1e-05, norm_in_weight, "
+    "norm_in_bias, p_in_weight, g_in_weight, norm_out_weight, norm_out_bias, p_out_weight, g_out_weight",
+    "triangle_mul.precompute": "norm_in_weight, norm_in_bias, p_in_weight, g_in_weight, norm_out_weight, "
+    "norm_out_bias, p_out_weight, g_out_weight",
+    "triangle_mul.forward": "x, pre, *, direction, mask=None, eps=1e-05",
+    "triangle_mul.input_phase": "x, mask, p_in_combined, g_in_combined, sum_W_p_in, sum_W_g_in, B_p_in_const, "
+    "B_g_in_const, eps",
+    "triangle_mul.output_phase": "y_t, x, p_out_combined, g_out_combined, sum_W_p_out, sum_W_g_out, B_p_out_const, "
+    "B_g_out_const, eps",
+    "triangle_attn.triangle_attention": "X, W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, W_proj_g, B_proj_g, W_proj_o, "
+    "B_proj_o, H, D, scale=1.0, eps=1e-05, mask=None",
+    "triangle_attn.precompute": "W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, H, D",
+    "triangle_attn.forward": "X, pre, *, mask=None, scale=1.0, eps=1e-05, W_proj_g, B_proj_g, W_proj_o, B_proj_o, "
+    "pad_to=32",
+    "triangle_attn.triangle_attn_forward": "X_ln, WQ_c, WKV_c, WZ_c, BZ, out, scale=1.0, mask=None, Bias_buf=None, *, "
+    "WK_c=None, WV_c=None",
+    "triangle_attn.fused_gate_forward": "o_attn, qx_ln, WG, WO",
+    "attn_pair_bias.attention_pair_bias": "X, WQ, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj_g, B_proj_g, "
+    "W_proj_o, B_proj_o, H, D, scale=1.0, eps=1e-05",
+    "attn_pair_bias.precompute": "WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D",
+    "attn_pair_bias.forward": "X, Z, pre, *, scale=1.0, eps=1e-05, W_proj_g, B_proj_g, W_proj_o, B_proj_o",
+    "attn_pair_bias.apb_forward": "X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0, eps=1e-05",
+}
+
+
+def _parse(spec):
+    out, kwonly = [], False
+    for p in [s.strip() for s in spec.split(",")]:
+        if p == "*":
+            kwonly = True
+            continue
+        name, _, default = p.partition("=")
+        out.append((name, default or None, kwonly))
+    return out
+
+
+@pytest.mark.parametrize("qual", sorted(REF_SIGNATURES))
+def test_reference_signature_accepted(qual):
+    """Every reference parameter exists with the same kind and default (extra optional ones allowed)."""
+    mod, fn = qual.split(".")
+    sig = inspect.signature(getattr(getattr(tops, mod), fn))
+    params = list(sig.parameters.values())
+    ref = _parse(REF_SIGNATURES[qual])
+    pos = [p for p in params if p.kind in (p.POSITIONAL_ONLY, p.POSITIONAL_OR_KEYWORD)]
+    ref_pos = [r for r in ref if not r[2]]
+    assert [p.name for p in pos[: len(ref_pos)]] == [r[0] for r in ref_pos], qual
+    for name, default, kwonly in ref:
+        p = sig.parameters[name]
+        assert (p.kind == p.KEYWORD_ONLY) == kwonly or not kwonly, (qual, name)
+        if default is not None:
+            assert repr(p.default) == default or str(p.default) == default, (qual, name, p.default)
+        else:
+            assert p.default is inspect.Parameter.empty, (qual, name)
+    for p in params[len(ref):]:
+        if p.name not in dict((r[0], r) for r in ref):
+            assert p.default is not inspect.Parameter.empty, f"{qual}: extra parameter {p.name} must be optional"
+
+
+def test_package_exports_match_reference():
+    assert set(tops.__all__) == {"attn_pair_bias", "triangle_attn", "triangle_mul", "attention_pair_bias",
+                                 "triangle_attention", "triangle_multiplicative_update"}
+    assert tops.triangle_multiplicative_update is tops.triangle_mul.triangle_multiplicative_update
+    assert tops.triangle_attention is tops.triangle_attn.triangle_attention
+    assert tops.attention_pair_bias is tops.attn_pair_bias.attention_pair_bias
+
+
+def test_triangle_ops_alias_package():
+    import triangle_ops
+
+    assert triangle_ops.triangle_multiplicative_update is tops.triangle_multiplicative_update
+    assert triangle_ops.triangle_mul.forward is tops.triangle_mul.forward
+    from triangle_ops.triangle_attn import triangle_attn_forward  # noqa: F401
+    from triangle_ops._common import absorb_ln  # noqa: F401
+
+
+def _w(C=128, dt=torch.bfloat16):
+    g = torch.Generator().manual_seed(0)
+    r = lambda *s: torch.randn(*s, generator=g).to(dt)  # noqa: E731
+    return r
+
+
+def test_precompute_dicts_cpu():
+    r = _w()
+    C, H, D = 128, 4, 32
+    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    assert set(pre) == {"p_in_combined", "g_in_combined", "p_out_combined", "g_out_combined", "sum_W_p_in",
+                        "sum_W_g_in", "sum_W_p_out", "sum_W_g_out", "B_p_in_const", "B_g_in_const", "B_p_out_const",
+                        "B_g_out_const"}
+    assert pre["p_in_combined"].dtype == torch.bfloat16 and pre["sum_W_p_in"].dtype == torch.float32
+    WQ, WK, WV, Wz = r(C, H * D), r(C, H * D), r(C, H * D), r(C, H)
+    pre = tops.triangle_attn.precompute(r(C), r(C), WQ, WK, WV, Wz, None, H, D)
+    for k in ("WQ_c", "WKV_c", "WK_c", "WV_c", "WZ_c", "BZ", "W_ln", "B_ln"):
+        assert k in pre
+    assert pre["WK_c"] is None and pre["WZ_c"].shape == (H, C) and torch.equal(pre["BZ"], torch.zeros(H))
+    pre16 = tops.triangle_attn.precompute(r(64), r(64), r(64, 64), r(64, 64), r(64, 64), r(64, 4), r(4), 4, 16)
+    assert pre16["WK_c"].data_ptr() != pre16["WKV_c"].data_ptr()
+    pre = tops.attn_pair_bias.precompute(WQ, WK, WV, r(C), r(C), Wz, r(H), H, D)
+    for k in ("W_QKV", "W_combined", "sum_W_combined", "B_const"):
+        assert k in pre
+    assert pre["W_QKV"].shape == (C, 3 * H * D)
+    assert pre["W_combined"].shape == (H, C) and pre["W_combined"].dtype == torch.float32
+
+
+def test_dtype_codes_and_errors():
+    assert tl_io_dtype(torch.bfloat16) == 2 and tl_io_dtype(torch.float16) == 1 and tl_io_dtype(torch.float32) == 3
+    with pytest.raises(ValueError):
+        tl_io_dtype(torch.int32)
+
+
+def test_bad_direction_and_bias_asserts():
+    r = _w()
+    C = 128
+    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    with pytest.raises(ValueError, match="unknown direction"):
+        tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="sideways")
+    with pytest.raises(AssertionError):
+        tops.triangle_attn.forward(r(4, 4, C), {}, W_proj_g=r(C, C), B_proj_g=r(C), W_proj_o=r(C, C), B_proj_o=None)
+
+
+def test_cpu_tensors_rejected():
+    r = _w()
+    C = 128
+    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    with pytest.raises(ValueError, match="GPU tensors"):
+        tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
+
+
+def test_fp32_io_rejected_clearly():
+    C = 128
+    r = _w(dt=torch.float32)
+    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    with pytest.raises(ValueError, match="not supported by the gfx950 kernels"):
+        tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
+
+
+def test_missing_library_fresh_process(tmp_path):
+    code = ("import triangleops_amd._native as n\n"
+            "try:\n    n.load('/nonexistent/libtriangleops_amd.so')\n"
+            "except ImportError as e:\n    print('IMPORTERROR', e)\n")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True, text=True, timeout=120)
+    assert "IMPORTERROR" in r.stdout and "python -m triangleops_amd._build" in r.stdout
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(tops_[a-z_0-9]+)\s*\(([^;]*?)\)\s*;", text, re.M)
+    return {name: [a.strip() for a in args.split(",") if a.strip() and a.strip() != "void"] for name, args in decls}
+
+
+def test_header_declares_all_bound_symbols():
+    decl = _header_functions()
+    assert set(decl) == set(_native.EXPORTED), set(decl) ^ set(_native.EXPORTED)
+    for name, args in decl.items():
+        n_bound = len(_native._SIGNATURES[name]) if name in _native._SIGNATURES else len(_native._OTHER[name][0])
+        assert len(args) == n_bound, f"{name}: header has {len(args)} args, binding has {n_bound}"
+
+
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+    lib.tops_abi_version.restype = ctypes.c_int
+    assert lib.tops_abi_version() == _native.ABI_VERSION
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], cwd=ROOT,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode != 0 and "one GPU" in r.stderr
