@@ -38,7 +38,7 @@ if ROOT not in sys.path:
 
 import triangleops_amd as tops  # noqa: E402
 from triangleops_amd.attn_pair_bias.kernel import apb_forward  # noqa: E402
-from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, ln_bias_forward  # noqa: E402
+from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, prep_forward  # noqa: E402
 from triangleops_amd.triangle_mul.kernel import input_phase, output_phase, triangle_einsum  # noqa: E402
 
 METRIC = "per-call ms + MFMA util % for each op at N/L/M=128–2048 (bf16, 1 GPU)"
@@ -272,22 +272,24 @@ def tri_phases(d, pre):
     st = {}
     N = d["X"].shape[0]
 
-    def p_ln():
-        st["xln"], st["bias"] = ln_bias_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["WZ_c"], pre["BZ"])
+    def p_prep():
+        st["qp"], st["kv"], st["bias"], st["ldn"] = prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"],
+                                                                 pre["WZ_c"], pre["BZ"], scale=D**-0.5)
 
     def p_att():
         st["o"] = torch.empty(N, N, H * D, device=d["X"].device, dtype=d["X"].dtype)
-        attention_core(st["xln"], pre["wqkv_hm"], st["bias"], st["o"], scale=D**-0.5, mask=d["mask"])
+        attention_core(st["qp"], st["kv"], st["bias"], st["o"], N=N, ldn=st["ldn"], mask=d["mask"])
 
     def p_gate():
-        st["out"] = gate_out_forward(st["o"], st["xln"], d["W_proj_g"], None, d["W_proj_o"], None)
+        st["out"] = gate_out_forward(st["o"], d["X"], d["W_proj_g"], None, d["W_proj_o"], None,
+                                     ln=(pre["W_ln"], pre["B_ln"], 1e-5))
 
-    return [p_ln, p_att, p_gate]
+    return [p_prep, p_att, p_gate]
 
 
 def tri_work(N):
     return {
-        "tri_ln_bias": ("hbm", 4 * N * N * C + 2 * H * N * N),
+        "tri_prep": ("hbm", 2 * N * N * C + 6 * N * N * H * D + 2 * H * N * N),
         "tri_attention": ("mfma", 4 * N**3 * H * D + 6 * N * N * C * H * D),
         "tri_gate_out": ("hbm", 6 * N * N * C),
     }

@@ -68,51 +68,59 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
                           int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype, void* stream);
 
 /*
- * triangle_attention: LayerNorm + row-shared pair-bias projection in one pass.
- * Replaces F.layer_norm (triangle_attn/module.py:77-83) and `bias_proj_kernel`
- * (triangle_attn/kernel.py:36-98, launched at :303-322).
- *   x      io   element (q, k, c) at x[q*sx0 + k*sx1 + c], c < C (channel stride 1)
- *   w_ln, b_ln  io (C,) LayerNorm affine (b_ln may be NULL); ignored when apply_ln == 0
+ * triangle_attention pre-pass: LayerNorm, row-shared pair bias and the Q/K/V projections of all
+ * heads in one pass over x.  Replaces F.layer_norm (triangle_attn/module.py:77-83),
+ * `bias_proj_kernel` (triangle_attn/kernel.py:36-98) and the Q/K/V projections inside
+ * `triangle_attn_kernel` (triangle_attn/kernel.py:181-219).
+ *   x      io   element (i, k, c) at x[i*sx0 + k*sx1 + c], c < C (channel stride 1); read as
+ *               already normalized when apply_ln == 0 (w_ln, b_ln ignored)
+ *   w_ln, b_ln  io (C,) LayerNorm affine (b_ln may be NULL)
+ *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T
  *   WZ     io   (H, C);  BZ fp32 (H,) or NULL
- *   x_ln   io   (N, N, C) contiguous LN(x), or NULL (not written); must be NULL when apply_ln == 0
- *   bias   io   (H, N, N) contiguous: bias[h,q,k] = x_ln[q,k,:] . WZ[h,:] + BZ[h]
- * With apply_ln == 0 the input is taken as already normalized (the reference's bias kernel).
+ *   ldn         N rounded up to a multiple of 64
+ *   Qp     io   (N, H, ldn, D): scale * log2(e) * Q, d permuted within each 32 as
+ *               [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]
+ *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x D, d permuted) then
+ *               V^T (D x 64 keys, keys permuted the same way within each 32)
+ *   bias   io   (H, N, ldn): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]), zeros for k >= N
+ * C == 128, H == 4, D == 32.
  */
-int tops_tri_ln_bias(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
-                     const void* WZ, const float* BZ, void* x_ln, void* bias, int64_t N, int64_t C, int64_t H,
-                     float eps, int dtype, void* stream);
+int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
+                  const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
+                  int64_t ldn, int64_t C, int64_t H, int64_t D, float eps, float scale, int dtype, void* stream);
 
 /*
- * triangle_attention core (starting node).  Replaces `triangle_attn_kernel`
- * (triangle_attn/kernel.py:110-253, launched at :335-373).
- *   x_ln   io   (N, N, C) contiguous, C == 128
- *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T (feature-major)
- *   bias   io   (H, N, N) from tops_tri_ln_bias
+ * triangle_attention core (starting node) over the pre-pass outputs.  Replaces the attention
+ * of `triangle_attn_kernel` (triangle_attn/kernel.py:197-253, launched at :335-373).
  *   mask   int8 (N, N) with strides (sm0, sm1), nonzero = valid key, or NULL
  *   out    io   O[i, q, h*D + d] at out[i*so0 + q*so1 + h*D + d]
- * out[i,q,h] = softmax_k(scale * Q.K + bias[h,q,k] - 1e9 * (mask[i,k] == 0)) V, D == 32.
+ * out[i,q,h] = softmax_k(scale * Q.K + bias[h,q,k] - 1e9 * (mask[i,k] == 0)) V; a row with no
+ * valid key is the uniform average of V over all N keys (what the -1e9 add gives).  D == 32.
  */
-int tops_tri_attention(const void* x_ln, const void* wqkv, const void* bias, const void* mask, int64_t sm0,
-                       int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t C, int64_t H, int64_t D,
-                       float scale, int dtype, void* stream);
+int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0, int64_t sm1,
+                       void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H, int64_t D, int dtype,
+                       void* stream);
 
 /*
  * Gate + output projection over M1*M2 tokens.  Replaces `fused_gate_forward` /
  * `fused_gate_kernel` (triangle_attn/kernel.py:387-470) and the apb epilogue
  * (attn_pair_bias/module.py:69-70):
- *   out[t] = ((o[t] * sigmoid(gin[t] Wg^T + bg)) -> io) Wo^T + bo
+ *   out[t] = ((o[t] * sigmoid(g[t] Wg^T + bg)) -> io) Wo^T + bo,  g = LN(gin) if apply_ln else gin
  *   o      io   token (m1, m2) at o[m1*so0 + m2*so1 + c], c < C
- *   gin    io   (M1*M2, C) contiguous;  Wg, Wo io (C, C) in (out, in) layout;  bg, bo io (C,) or NULL
+ *   gin    io   token (m1, m2) at gin[m1*sg0 + m2*sg1 + c];  w_ln, b_ln io (C,), ln_eps
+ *   Wg, Wo io   (C, C) in (out, in) layout;  bg, bo io (C,) or NULL
  *   out    io   (M1*M2, C) contiguous.  C == 128.
  */
-int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, const void* Wg, const void* bg,
+int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
+                  const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg, const void* bg,
                   const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2, int64_t C, int dtype,
                   void* stream);
 
 /*
  * attention_pair_bias core.  Replaces `apb_forward` + `_apb_kernel`
  * (attn_pair_bias/kernel.py:205-257, :24-202).
- *   X      io   (M, C) contiguous, C == 128;  W_QKV io (C, 3*H*D) per-head [Q_h | K_h | V_h]
+ *   X      io   (M, C) contiguous, C == 128
+ *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T (feature-major)
  *   Z      io   element (q, k, c) at Z[q*sz0 + k*sz1 + c], c < Cz, Cz == 128
  *   Wc     fp32 (H, Cz) LN-folded bias weight;  sWc, Bc fp32 (H,)
  *   mask   int8 (M,) key mask (nonzero = valid) or NULL; masked keys get -inf
@@ -120,7 +128,7 @@ int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, cons
  *   work   device scratch of tops_apb_workspace_bytes(M, H, D) bytes (caller-owned)
  */
 int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D);
-int tops_apb_forward(const void* X, const void* W_QKV, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
+int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
                      const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M, int64_t C,
                      int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
 

@@ -26,9 +26,13 @@ _SIGNATURES = {
     "tops_tmu_input_phase": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _p],
     "tops_tmu_einsum": [_p, _p, _i64, _i64, _i64, _i64, _i32, _p],
     "tops_tmu_output_phase": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
-    "tops_tri_ln_bias": [_p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p],
-    "tops_tri_attention": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
-    "tops_gate_out": [_p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
+    "tops_tri_prep": [
+        _p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
+    ],
+    "tops_tri_attention": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "tops_gate_out": [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p,
+    ],
     "tops_apb_forward": [
         _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],

@@ -63,16 +63,35 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)); saturates cleanly to 0 / 1.
 __device__ inline float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-x * kLog2e)); }
 
-// Sum over groups of `W` adjacent lanes (W = 2, 4, 8, ...) via xor shuffles.
+// Lane permutation through DPP (a VALU operand modifier, no LDS traffic).
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of `W` adjacent lanes (W = 1, 2, 4, 8, 16), result in every lane of
+// the group: quad permutations (xor 1, xor 2), then half-row and row mirrors, which pair each
+// lane with one in the other half of its 8- / 16-lane group.
 template <int W>
 __device__ inline float group_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < W; m <<= 1) v += __shfl_xor(v, m);
+  static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16, "group width");
+  if constexpr (W >= 2) v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp<0x141>(v);  // row_half_mirror
+  if constexpr (W >= 16) v += dpp<0x140>(v); // row_mirror
   return v;
 }
 
 // max / sum of the values held by lanes l and l ^ 32, returned in both lanes.
-__device__ inline float halves_max(float v) { return fmaxf(v, __shfl_xor(v, 32)); }
-__device__ inline float halves_sum(float v) { return v + __shfl_xor(v, 32); }
+// v_permlane32_swap exchanges the upper half of its first operand with the lower half of
+// its second; with both operands = v the two results hold (lo, lo) and (hi, hi).
+__device__ inline float halves_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float halves_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 }  // namespace tops

@@ -1,13 +1,23 @@
-// triangle_attention (starting node) on gfx950.
+// triangle_attention (starting node) on gfx950: two launches before the gate.
 //
-//   tri_ln_bias_kernel   one pass over x: x_ln = LN(x) (written once, shared by the attention
-//                        and the gate epilogue) and the row-shared pair bias
-//                        bias[h,q,k] = x_ln[q,k,:] . WZ[h,:] + BZ[h]   (fp32 dot, io store).
-//   tri_attn_kernel      one block per (row i, head h, query chunk): projects K/V of row i
-//                        once per 64-key block into LDS, each wave streams its queries over
-//                        them with an online softmax.  S^T = K . Q^T is accumulated on top of
-//                        the bias tile (MFMA C operand), and the D registers of S^T are the
-//                        B operand of O^T = V^T . P^T, so scores never leave registers.
+//   tri_prep_kernel   one pass over x per (row i, 64 positions): LN(x), the row-shared pair bias
+//                     (fp32 dot), and Q, K, V of all heads as one K = 128 MFMA GEMM.  Outputs
+//                     are written in the order the attention kernel consumes them:
+//                       Qp  [i][h][q][32]    Q * scale * log2(e), d permuted (below)
+//                       KV  [i][h][kb][4096] per 64-key block: K [64 keys][32 d permuted] then
+//                                            V^T [32 d][64 keys permuted]
+//                       bias[h][q][ldn]      log2(e) * bias, rows padded with zeros to ldn
+//   tri_attn_kernel   4 waves per (row i, head h, query chunk): the KV block of each 64 keys is
+//                     copied into LDS (double-buffered, one barrier per block), each wave
+//                     streams its query tiles over it with an online softmax in the exp2
+//                     domain.  No projection and no x_ln reads, so blocks are small enough for
+//                     two to share a CU and hide each other's barriers.
+//
+// Element permutation within each group of 32 (d for Q/K, keys for V^T):
+//   [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]
+// i.e. position 16 j + 8 hl + e (j = 0, 1; hl = lane / 32; e < 8) holds the element that the
+// MFMA D register v = 8 j + e of lane half hl holds (8 (v / 4) + 4 hl + v % 4), so every MFMA
+// operand of the attention kernel is one 16-byte load.
 //
 // Reference: triangle_attn/module.py:57-125 (forward), triangle_attn/kernel.py:36-98 (bias),
 // :110-253 (attention), :230-238 and :369 (additive -1e9 pair mask, -inf outside the row).
@@ -16,118 +26,191 @@
 
 namespace tops {
 
-// ---------------------------------------------------------------------------------------------
-// LayerNorm + bias.  8 threads per token (16 channels each), 32 tokens per 256-thread block.
-// ---------------------------------------------------------------------------------------------
-template <typename T, int C, int H>
-__global__ __launch_bounds__(256) void tri_ln_bias_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
-                                                         const T* __restrict__ w_ln, const T* __restrict__ b_ln,
-                                                         int apply_ln, const T* __restrict__ WZ,
-                                                         const float* __restrict__ BZ, T* __restrict__ x_ln,
-                                                         T* __restrict__ bias, int64_t N, float eps) {
-  constexpr int TPT = 8, CPT = C / TPT;  // 16 channels per thread
-  using V8 = vec<T, 8>;
-  const int tid = threadIdx.x;
-  const int part = tid % TPT;
-  const int64_t t = (int64_t)blockIdx.x * (256 / TPT) + tid / TPT;
-  const int64_t NN = N * N;
-  const bool valid = t < NN;
-  const int64_t q = valid ? t / N : 0, k = valid ? t % N : 0;
+constexpr int kKVBlock = 4096;  // elements per (row, head, 64-key) KV block: 64x32 K + 32x64 V^T
 
-  float v[CPT];
+// ---------------------------------------------------------------------------------------------
+// Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 256 threads: the LN mapping is
+// 4 threads per position (32 channels each); the GEMM mapping is wave w = head w with its
+// WQ^T / WK^T / WV^T rows in registers and the normalized tile read from LDS as MFMA operands.
+// Positions >= N are processed from zeros (finite values, masked by the attention kernel).
+// ---------------------------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
+                                                         const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                         int apply_ln, const T* __restrict__ wqkv,
+                                                         const T* __restrict__ WZ, const float* __restrict__ BZ,
+                                                         T* __restrict__ Qp, T* __restrict__ KV, T* __restrict__ bias,
+                                                         int64_t N, int64_t ldn, float eps, float qscale,
+                                                         float bias_scale, int64_t ntiles) {
+  constexpr int C = 128, D = 32, ROW = C * 2;
+  static_assert(H == 4, "one wave per head");
+  using V8 = vec<T, 8>;
+  __shared__ __attribute__((aligned(16))) char xs[64 * ROW];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int h = wave;
+  const int64_t nkb = ldn / 64;
+
+  V8 wq[8], wk[8], wv[8];
   {
-    const T* src = x + q * sx0 + k * sx1 + part * CPT;
+    const T* wh = wqkv + (int64_t)h * 3 * D * C + (int64_t)col * C + 8 * hl;
 #pragma unroll
-    for (int e = 0; e < CPT / 8; ++e) {
-      V8 a = valid ? ldg<V8>(src + 8 * e) : V8{};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[8 * e + j] = (float)a[j];
+    for (int s = 0; s < 8; ++s) {
+      wq[s] = ldg<V8>(wh + 16 * s);
+      wk[s] = ldg<V8>(wh + D * C + 16 * s);
+      wv[s] = ldg<V8>(wh + 2 * D * C + 16 * s);
     }
   }
-  if (apply_ln) {
-    float s = 0.f;
+  const int tok = tid >> 2, part = tid & 3;  // LN mapping
+
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t i = tile / nkb, kb = tile % nkb;
+    const int64_t p = kb * 64 + tok;  // position of this thread's token
+    // ---- LN + bias (fp32), normalized tile -> LDS ----
+    {
+      float v[32];
+      if (p < N) {
+        const T* src = x + i * sx0 + p * sx1 + 32 * part;
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) s += v[j];
-    const float mean = group_sum<TPT>(s) * (1.0f / C);
-    float sq = 0.f;
+        for (int e = 0; e < 4; ++e) {
+          const V8 a = ldg<V8>(src + 8 * e);
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) sq += (v[j] - mean) * (v[j] - mean);
-    const float rstd = rsqrtf(group_sum<TPT>(sq) * (1.0f / C) + eps);
+          for (int j = 0; j < 8; ++j) v[8 * e + j] = (float)a[j];
+        }
+      } else {
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-      const int c = part * CPT + j;
-      v[j] = (v[j] - mean) * rstd * (float)w_ln[c] + (b_ln ? (float)b_ln[c] : 0.f);
-    }
-    if (x_ln && valid) {
-      T* dst = x_ln + t * C + part * CPT;
+        for (int e = 0; e < 32; ++e) v[e] = 0.f;
+      }
+      if (apply_ln) {
+        float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < CPT / 8; ++e) {
+        for (int e = 0; e < 32; ++e) s += v[e];
+        const float mean = group_sum<4>(s) * (1.0f / C);
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) q += (v[e] - mean) * (v[e] - mean);
+        const float rstd = rsqrtf(group_sum<4>(q) * (1.0f / C) + eps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const V8 w8 = ldg<V8>(w_ln + 32 * part + 8 * e);
+          const V8 b8 = b_ln ? ldg<V8>(b_ln + 32 * part + 8 * e) : V8{};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[8 * e + j] = (v[8 * e + j] - mean) * rstd * (float)w8[j] + (float)b8[j];
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < H; ++hh) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const V8 w8 = ldg<V8>(WZ + hh * C + 32 * part + 8 * e);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) d += v[8 * e + j] * (float)w8[j];
+        }
+        d = group_sum<4>(d);
+        if (part == 0)
+          bias[((int64_t)hh * N + i) * ldn + p] = p < N ? (T)((d + (BZ ? BZ[hh] : 0.f)) * bias_scale) : (T)0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
         V8 o;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] = (T)v[8 * e + j];
-        stg<V8>(dst + 8 * e, o);
+        const int chunk = 4 * part + e;
+        *reinterpret_cast<V8*>(&xs[tok * ROW + ((chunk ^ (tok & 7)) << 4)]) = o;
       }
     }
-  }
+    __syncthreads();
+    // ---- Q, K, V of head h for the 64 positions ----
+    T* qdst = Qp + ((i * H + h) * ldn + kb * 64) * D;
+    T* kvdst = KV + ((i * H + h) * nkb + kb) * kKVBlock;
 #pragma unroll
-  for (int h = 0; h < H; ++h) {
-    float d = 0.f;
+    for (int sub = 0; sub < 2; ++sub) {
+      const int t = sub * 32 + col;
+      f32x16 aq = {}, ak = {}, av = {};
 #pragma unroll
-    for (int j = 0; j < CPT; ++j) d += v[j] * (float)WZ[h * C + part * CPT + j];
-    d = group_sum<TPT>(d);
-    if (part == 0 && valid) bias[h * NN + t] = (T)(d + (BZ ? BZ[h] : 0.f));
+      for (int s = 0; s < 8; ++s) {
+        const V8 xb = *reinterpret_cast<const V8*>(&xs[t * ROW + (((2 * s + hl) ^ (t & 7)) << 4)]);
+        aq = Mma<T>::m32(wq[s], xb, aq);  // Q^T: lane -> position t, d rows
+        ak = Mma<T>::m32(wk[s], xb, ak);  // K^T: lane -> key t, d rows
+        av = Mma<T>::m32(xb, wv[s], av);  // V:   lane -> d = col, key rows
+      }
+      V8 q0, q1, k0, k1, v0, v1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        q0[e] = (T)(aq[e] * qscale);
+        q1[e] = (T)(aq[8 + e] * qscale);
+        k0[e] = (T)ak[e];
+        k1[e] = (T)ak[8 + e];
+        v0[e] = (T)av[e];
+        v1[e] = (T)av[8 + e];
+      }
+      stg<V8>(qdst + t * D + 8 * hl, q0);
+      stg<V8>(qdst + t * D + 16 + 8 * hl, q1);
+      stg<V8>(kvdst + t * D + 8 * hl, k0);
+      stg<V8>(kvdst + t * D + 16 + 8 * hl, k1);
+      stg<V8>(kvdst + 64 * D + col * 64 + sub * 32 + 8 * hl, v0);
+      stg<V8>(kvdst + 64 * D + col * 64 + sub * 32 + 16 + 8 * hl, v1);
+    }
+    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention core.  C = 128, D = 32, 8 waves, 64-key blocks, QT query tiles (32 queries each)
-// per wave.  wqkv is (H, 3, D, C): rows of WQ^T, WK^T, WV^T for each head.
+// Attention core.  4 waves, QT query tiles (32 queries) per wave, 64-key blocks.
 //
-// Per 64-key block:
-//   projection: wave w computes a 16-key x 32-d slice of K (w < 4) or V (w >= 4) with
-//     16x16x32 MFMAs straight from x_ln rows in HBM/L2, storing K as [key][d] and V as
-//     V^T [d][key] in LDS (rows padded to keep the operand reads bank-conflict free);
-//   attention: per 32-key tile and query tile, S^T = bias + K . Q^T (2 MFMAs), masked and
-//     folded into the running max / sum, then O^T += V^T . P^T (2 MFMAs).
-// Masked keys get probability exactly 0 (exp(-1e9 - m) underflows to 0 in fp32 whenever the
-// row has a valid key).  A row without valid keys reproduces the reference's uniform
-// average: every score is -1e9 there, so all N keys get weight 1/N.
+// Per (32-key tile, query tile) a wave runs
+//     S^T  = C0 + I . bias^T          2 MFMAs, A = identity, B = 16 bias bytes per lane
+//          + K . Q^T                  2 MFMAs, K from LDS, Q^T in registers
+//     P    = exp2(S^T), l += rowsum   16 v_exp per lane, no max / subtract per element
+//     O^T += V^T . P^T                2 MFMAs, V^T from LDS, P^T = S^T's D registers
+// where C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m
+// is exact after the first tile and is only raised when a tile's probabilities could exceed
+// 2^64 (then O and l are rescaled and the tile recomputed), so the common path needs neither
+// a max nor a subtraction per score.  Masked keys get probability exactly 0 (equal to the
+// reference's exp(-1e9 - m) in fp32 whenever the row has a valid key); a row without valid
+// keys takes the uniform average of V over all N keys, as the reference's -1e9 add gives.
+// The identity MFMA multiplies every bias element of the tile by 0 or 1, so the bias padding
+// must be finite (the pre-pass writes zeros there).
 // ---------------------------------------------------------------------------------------------
-constexpr int kTriKRow = 36;  // K  LDS row: 32 d + 4 pad (elements)
-constexpr int kTriVRow = 68;  // V^T LDS row: 64 keys + 4 pad (elements)
+constexpr int kKPad = 40;  // LDS row of K: 32 d + 8 pad (conflict-free 16-byte operand reads)
+constexpr int kVPad = 72;  // LDS row of V^T: 64 keys + 8 pad
+constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
+constexpr float kOverflow = 18446744073709551616.0f;  // 2^64
 
 template <typename T, int QT>
-__global__ __launch_bounds__(512) void tri_attn_kernel(const T* __restrict__ xln, const T* __restrict__ wqkv,
-                                                      const T* __restrict__ bias, const int8_t* __restrict__ mask,
-                                                      int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
-                                                      int64_t so1, int64_t N, int H, int nqc, float scale) {
-  constexpr int C = 128, D = 32;
+__global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
+                                                         const T* __restrict__ bias, const int8_t* __restrict__ mask,
+                                                         int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
+                                                         int64_t so1, int64_t N, int64_t ldn, int H, int nqc) {
+  constexpr int D = 32, NW = 4;
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
 
-  __shared__ __attribute__((aligned(16))) T Ks[64 * kTriKRow];
-  __shared__ __attribute__((aligned(16))) T Vs[D * kTriVRow];
-  __shared__ unsigned long long kvalid[64];  // N <= 4096 -> at most 64 key blocks
-  __shared__ int row_any;
+  __shared__ __attribute__((aligned(16))) T kvs[2][kKVLds];
+  __shared__ unsigned long long kvalid[64];  // per 64-key block (N <= 4096)
+  __shared__ short vblk[64];                 // indices of blocks with a valid key
+  __shared__ int nvblk, row_any;
 
-  // ---- block -> (row i, head h, query chunk); XCD-aware: consecutive rows of one head
-  // ---- share an XCD so that head's bias stays in that XCD's L2.
+  // ---- block -> (row i, head h, query chunk); XCD-aware: an XCD works on one head and a
+  // ---- contiguous range of query chunks for all rows, so that head's bias stays in its L2.
   const int64_t total = N * H * nqc;
   int64_t id = blockIdx.x;
   if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
   const int64_t i = id % N;
   const int hq = (int)(id / N);
-  const int h = hq % H;
-  const int qc = hq / H;
+  const int qc = hq % nqc;
+  const int h = hq / nqc;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
-  const int nkb = (int)((N + 63) / 64);
+  const int nkb = (int)(ldn / 64);
 
-  // ---- key validity per 64-key block ----
+  // ---- key validity per 64-key block; compact list of blocks to visit ----
   if (tid == 0) row_any = 0;
   __syncthreads();
-  for (int kb = wave; kb < nkb; kb += 8) {
+  for (int kb = wave; kb < nkb; kb += NW) {
     const int64_t k = (int64_t)kb * 64 + lane;
     bool ok = k < N;
     if (ok && mask) ok = mask[i * sm0 + k * sm1] != 0;
@@ -138,176 +221,176 @@ __global__ __launch_bounds__(512) void tri_attn_kernel(const T* __restrict__ xln
     }
   }
   __syncthreads();
-  const bool uniform = row_any == 0;  // no valid key in this row: every score is -1e9
-  if (uniform) {
-    for (int kb = wave; kb < nkb; kb += 8) {
-      const int64_t k = (int64_t)kb * 64 + lane;
-      const unsigned long long bits = __ballot(k < N);
-      if (lane == 0) kvalid[kb] = bits;
+  const bool uniform = row_any == 0;  // no valid key: every score is -1e9, weights 1/N
+  if (tid == 0) {
+    int n = 0;
+    for (int kb = 0; kb < nkb; ++kb) {
+      if (uniform) kvalid[kb] = (N - 64LL * kb >= 64) ? ~0ull : ((1ull << (N - 64LL * kb)) - 1ull);
+      if (kvalid[kb]) vblk[n++] = (short)kb;
     }
-    __syncthreads();
+    nvblk = n;
   }
+  __syncthreads();
+  const int nv = nvblk;
 
-  const T* xrow = xln + i * N * C;
-  const T* wh = wqkv + (int64_t)h * 3 * D * C;
+  const T* kvrow = KV + ((int64_t)i * H + h) * nkb * kKVBlock;
+  const T* brow0 = bias + (int64_t)h * N * ldn;
 
-  // ---- Q^T tiles for this wave's queries: B operand of S^T = K . Q^T ----
-  const int64_t qbase = (int64_t)qc * (8 * 32 * QT) + (int64_t)wave * 32 * QT;
+  // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) ----
+  const int64_t qbase = (int64_t)qc * (NW * 32 * QT) + (int64_t)wave * 32 * QT;
   V8 qop[QT][2];
-  {
-    V8 wq[8];
+  const T* bq[QT];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) wq[s] = ldg<V8>(wh + (int64_t)col * C + 16 * s + 8 * hl);
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      int64_t q = qbase + 32 * t + col;
-      q = q < N ? q : N - 1;
-      f32x16 acc = {};
-#pragma unroll
-      for (int s = 0; s < 8; ++s) acc = Mma<T>::m32(wq[s], ldg<V8>(xrow + q * C + 16 * s + 8 * hl), acc);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qop[t][0][e] = (T)(acc[e] * scale);
-        qop[t][1][e] = (T)(acc[8 + e] * scale);
-      }
-    }
+  for (int t = 0; t < QT; ++t) {
+    int64_t q = qbase + 32 * t + col;
+    q = q < N ? q : N - 1;
+    const T* qr = Qp + (((int64_t)i * H + h) * ldn + q) * D + 8 * hl;
+    qop[t][0] = ldg<V8>(qr);
+    qop[t][1] = ldg<V8>(qr + 16);
+    bq[t] = brow0 + q * ldn + 8 * hl;
   }
-
-  // ---- projection role: rows of WK^T (waves 0-3) or WV^T (waves 4-7), 16x16x32 layout ----
-  const bool is_v = wave >= 4;
-  const int kq = wave & 3;  // 16-key quarter of the block
-  V8 wr[2][4];
-  {
-    const T* wsrc = wh + (is_v ? 2 : 1) * D * C;
+  // ---- identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j ----
+  V8 ident[2];
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        wr[dt][s] = ldg<V8>(wsrc + (int64_t)(16 * dt + (lane & 15)) * C + 32 * s + 8 * (lane >> 4));
-  }
+    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
 
-  f32x16 o[QT];
-  float m[QT], l[QT];
+  // KV block copy: thread t moves elements [16 t, 16 t + 16) (K rows, then V^T rows)
+  auto kv_load = [&](int kb, V8* r) {
+    const T* src = kvrow + (int64_t)kb * kKVBlock + 16 * tid;
+    r[0] = ldg<V8>(src);
+    r[1] = ldg<V8>(src + 8);
+  };
+  auto kv_store = [&](int buf, const V8* r) {
+    const int e = 16 * tid;
+    T* dst;
+    if (e < 64 * D)
+      dst = &kvs[buf][(e / D) * kKPad + (e % D)];
+    else
+      dst = &kvs[buf][64 * kKPad + ((e - 64 * D) / 64) * kVPad + ((e - 64 * D) % 64)];
+    *reinterpret_cast<V8*>(dst) = r[0];
+    *reinterpret_cast<V8*>(dst + 8) = r[1];
+  };
+  // bias B operands of one 32-key tile of a block: [query tile t][half j], 16 bytes per lane
+  auto load_bias = [&](int kb, int kt, V8 (*bb)[2]) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bb[t][j] = uniform ? V8{} : ldg<V8>(bq[t] + kb * 64 + 32 * kt + 16 * j);
+  };
+
+  f32x16 o[QT], cinit[QT];
+  float l[QT];
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     o[t] = f32x16{};
-    m[t] = -INFINITY;
+    cinit[t] = f32x16{};
     l[t] = 0.f;
   }
-  const bool bias_vec = (N % 4) == 0;
 
-  for (int kb = 0; kb < nkb; ++kb) {
-    const unsigned long long kbits = kvalid[kb];
-    if (kbits == 0) continue;  // block-uniform
-    // ---- projection of this block's K / V into LDS ----
+  bool first = true;
+  auto tile = [&](int buf, int kt, unsigned int tbits, V8 (*bb)[2]) {
+    const bool full = tbits == 0xffffffffu;
+    V8 kop[2], vop[2];
     {
-      int64_t key = (int64_t)kb * 64 + 16 * kq + (lane & 15);
-      key = key < N ? key : N - 1;
-      V8 xa[4];
+      const T* kr = &kvs[buf][(32 * kt + col) * kKPad + 8 * hl];
+      kop[0] = *reinterpret_cast<const V8*>(kr);
+      kop[1] = *reinterpret_cast<const V8*>(kr + 16);
+      const T* vr = &kvs[buf][64 * kKPad + col * kVPad + 32 * kt + 8 * hl];
+      vop[0] = *reinterpret_cast<const V8*>(vr);
+      vop[1] = *reinterpret_cast<const V8*>(vr + 16);
+    }
+    // all score tiles first, so their MFMAs overlap the exponentials of the previous one
+    f32x16 s[QT];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xa[s] = ldg<V8>(xrow + key * C + 32 * s + 8 * (lane >> 4));
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        f32x4 acc = {};
-        if (!is_v) {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) acc = Mma<T>::m16(wr[dt][s], xa[s], acc);
-          // D = K^T tile: lane -> key (lane & 15), d = 16 dt + 4 (lane >> 4) + v
-          V4 kv = {(T)acc[0], (T)acc[1], (T)acc[2], (T)acc[3]};
-          *reinterpret_cast<V4*>(&Ks[(16 * kq + (lane & 15)) * kTriKRow + 16 * dt + 4 * (lane >> 4)]) = kv;
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) acc = Mma<T>::m16(xa[s], wr[dt][s], acc);
-          // D = V tile: lane -> d = 16 dt + (lane & 15), keys 4 (lane >> 4) + v
-          V4 vv = {(T)acc[0], (T)acc[1], (T)acc[2], (T)acc[3]};
-          *reinterpret_cast<V4*>(&Vs[(16 * dt + (lane & 15)) * kTriVRow + 16 * kq + 4 * (lane >> 4)]) = vv;
-        }
+    for (int t = 0; t < QT; ++t) {
+      s[t] = cinit[t];
+      if (!uniform) {
+        s[t] = Mma<T>::m32(ident[0], bb[t][0], s[t]);
+        s[t] = Mma<T>::m32(ident[1], bb[t][1], s[t]);
+        s[t] = Mma<T>::m32(kop[0], qop[t][0], s[t]);
+        s[t] = Mma<T>::m32(kop[1], qop[t][1], s[t]);
       }
     }
-    __syncthreads();
-
-    // ---- attention over the two 32-key tiles ----
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const unsigned int tbits = (unsigned int)(kbits >> (32 * kt));
-      if (tbits == 0) continue;
-      const bool full = tbits == 0xffffffffu;
-      V8 kop[2], vop[2];
-      {
-        const T* kr = &Ks[(32 * kt + col) * kTriKRow];
-        const V4 a0 = *reinterpret_cast<const V4*>(kr + 4 * hl);
-        const V4 a1 = *reinterpret_cast<const V4*>(kr + 8 + 4 * hl);
-        const V4 a2 = *reinterpret_cast<const V4*>(kr + 16 + 4 * hl);
-        const V4 a3 = *reinterpret_cast<const V4*>(kr + 24 + 4 * hl);
-        kop[0] = V8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        kop[1] = V8{a2[0], a2[1], a2[2], a2[3], a3[0], a3[1], a3[2], a3[3]};
-        const T* vr = &Vs[col * kTriVRow + 32 * kt];
-        const V4 b0 = *reinterpret_cast<const V4*>(vr + 4 * hl);
-        const V4 b1 = *reinterpret_cast<const V4*>(vr + 8 + 4 * hl);
-        const V4 b2 = *reinterpret_cast<const V4*>(vr + 16 + 4 * hl);
-        const V4 b3 = *reinterpret_cast<const V4*>(vr + 24 + 4 * hl);
-        vop[0] = V8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-        vop[1] = V8{b2[0], b2[1], b2[2], b2[3], b3[0], b3[1], b3[2], b3[3]};
-      }
-      const int64_t k0 = (int64_t)kb * 64 + 32 * kt;
-#pragma unroll
-      for (int t = 0; t < QT; ++t) {
-        int64_t q = qbase + 32 * t + col;
-        q = q < N ? q : N - 1;
-        f32x16 s;
-        if (uniform) {
-          s = f32x16{};
-        } else {
-          const T* brow = bias + ((int64_t)h * N + q) * N + k0;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int kk = 8 * g + 4 * hl;
-            if (bias_vec && k0 + kk + 3 < N) {
-              const V4 b = ldg<V4>(brow + kk);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) s[4 * g + e] = (float)b[e];
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) s[4 * g + e] = (k0 + kk + e < N) ? (float)brow[kk + e] : 0.f;
-            }
-          }
-          s = Mma<T>::m32(kop[0], qop[t][0], s);
-          s = Mma<T>::m32(kop[1], qop[t][1], s);
-        }
-        if (!full) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int kk = 8 * (v / 4) + 4 * hl + (v % 4);
-            if (!((tbits >> kk) & 1u)) s[v] = -INFINITY;
-          }
-        }
-        float mt = s[0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, s[v]);
-        mt = halves_max(mt);
-        const float mnew = fmaxf(m[t], mt);
-        const float muse = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = fast_exp2((m[t] - muse) * kLog2e);
-        const float nb = -muse * kLog2e;
-        float ps = 0.f;
-        V8 pop0, pop1;
+    for (int t = 0; t < QT; ++t) {
+      if (!full) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float p = fast_exp2(fmaf(s[v], kLog2e, nb));
-          ps += p;
-          if (v < 8)
-            pop0[v] = (T)p;
-          else
-            pop1[v - 8] = (T)p;
+          const int kk = 8 * (v / 4) + 4 * hl + (v % 4);
+          if (!((tbits >> kk) & 1u)) s[t][v] = -INFINITY;
         }
-        l[t] = l[t] * alpha + ps;
-        m[t] = mnew;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
-        o[t] = Mma<T>::m32(vop[0], pop0, o[t]);
-        o[t] = Mma<T>::m32(vop[1], pop1, o[t]);
       }
+      if (first) {  // exact running max from the first visited tile (wave-uniform)
+        float mt = s[t][0];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, s[t][v]);
+        mt = halves_max(mt);  // finite: the tile has a valid key
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[t][v] -= mt;
+        cinit[t] -= mt;
+      }
+      float p[16], ps = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        p[v] = fast_exp2(s[t][v]);
+        ps += p[v];
+      }
+      if (__ballot(!(ps <= kOverflow)) != 0) {  // rare: raise the running max of this tile
+        float mt = s[t][0];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, s[t][v]);
+        mt = fmaxf(halves_max(mt), 0.f);
+        const float alpha = fast_exp2(-mt);
+        ps = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          p[v] = fast_exp2(s[t][v] - mt);
+          ps += p[v];
+          o[t][v] *= alpha;
+        }
+        l[t] *= alpha;
+        cinit[t] -= mt;
+      }
+      l[t] += ps;
+      V8 p0, p1;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        p0[v] = (T)p[v];
+        p1[v] = (T)p[8 + v];
+      }
+      o[t] = Mma<T>::m32(vop[0], p0, o[t]);
+      o[t] = Mma<T>::m32(vop[1], p1, o[t]);
     }
+    first = false;
+  };
+
+  // Pipeline per visited block j: the next KV block and this block's tile-1 bias are loaded
+  // while tile 0 runs, the next block's tile-0 bias while tile 1 runs; the next KV block goes
+  // to the other LDS buffer before the single barrier.
+  V8 kvr[2];
+  V8 bt0[QT][2], bt1[QT][2];
+  if (nv > 0) {
+    kv_load(vblk[0], kvr);
+    load_bias(vblk[0], 0, bt0);
+    kv_store(0, kvr);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nv; ++j) {
+    const int kb = vblk[j];
+    const int buf = j & 1;
+    const bool more = j + 1 < nv;
+    const int kbn = more ? vblk[j + 1] : kb;
+    const unsigned long long kbits = kvalid[kb];
+    const unsigned int tb0 = (unsigned int)kbits, tb1 = (unsigned int)(kbits >> 32);
+    if (more) kv_load(kbn, kvr);
+    load_bias(kb, 1, bt1);
+    if (tb0) tile(buf, 0, tb0, bt0);  // wave-uniform
+    if (more) load_bias(kbn, 0, bt0);
+    if (tb1) tile(buf, 1, tb1, bt1);
+    if (more) kv_store(buf ^ 1, kvr);
     __syncthreads();
   }
 
@@ -329,45 +412,35 @@ __global__ __launch_bounds__(512) void tri_attn_kernel(const T* __restrict__ xln
 }
 
 template <typename T>
-static int tri_ln_bias_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
-                         const void* WZ, const float* BZ, void* x_ln, void* bias, int64_t N, int64_t H, float eps,
-                         hipStream_t st) {
-  const int64_t NN = N * N;
-  const int64_t grid = (NN + 31) / 32;
-  if (grid == 0) return TOPS_OK;
-#define TOPS_LNB(HH)                                                                                          \
-  hipLaunchKernelGGL((tri_ln_bias_kernel<T, 128, HH>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)x, sx0, \
-                     sx1, (const T*)w_ln, (const T*)b_ln, apply_ln, (const T*)WZ, BZ, (T*)x_ln, (T*)bias, N, eps)
-  switch (H) {
-    case 1: TOPS_LNB(1); break;
-    case 2: TOPS_LNB(2); break;
-    case 4: TOPS_LNB(4); break;
-    case 8: TOPS_LNB(8); break;
-    default: return fail(TOPS_EUNSUPPORTED, "tops_tri_ln_bias: H must be 1, 2, 4 or 8 (got %lld)", (long long)H);
-  }
-#undef TOPS_LNB
-  return launched("tops_tri_ln_bias");
+static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
+                      const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
+                      int64_t ldn, float eps, float qscale, hipStream_t st) {
+  const int64_t ntiles = N * (ldn / 64);
+  if (ntiles == 0) return TOPS_OK;
+  const int64_t grid = ntiles < 2LL * num_cus() ? ntiles : 2LL * num_cus();
+  hipLaunchKernelGGL((tri_prep_kernel<T, 4>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)x, sx0, sx1,
+                     (const T*)w_ln, (const T*)b_ln, apply_ln, (const T*)wqkv, (const T*)WZ, BZ, (T*)Qp, (T*)KV,
+                     (T*)bias, N, ldn, eps, qscale, kLog2e, ntiles);
+  return launched("tops_tri_prep");
 }
 
 template <typename T>
-static int tri_attention_t(const void* xln, const void* wqkv, const void* bias, const void* mask, int64_t sm0,
-                           int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t H, float scale,
+static int tri_attention_t(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
+                           int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
                            hipStream_t st) {
-  const int qt = N <= 256 ? 1 : (N <= 512 ? 2 : 4);
-  const int64_t per_block = 8 * 32 * qt;
+  const int qt = N <= 128 ? 1 : 2;
+  const int64_t per_block = 4 * 32 * qt;
   const int nqc = (int)((N + per_block - 1) / per_block);
   const int64_t grid = N * H * nqc;
   if (grid == 0) return TOPS_OK;
-#define TOPS_TRI(QTV)                                                                                        \
-  hipLaunchKernelGGL((tri_attn_kernel<T, QTV>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)xln,        \
-                     (const T*)wqkv, (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, (int)H, \
-                     nqc, scale)
+#define TOPS_TRI(QTV)                                                                                     \
+  hipLaunchKernelGGL((tri_attn_kernel<T, QTV>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Qp,      \
+                     (const T*)KV, (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, ldn, \
+                     (int)H, nqc)
   if (qt == 1)
     TOPS_TRI(1);
-  else if (qt == 2)
-    TOPS_TRI(2);
   else
-    TOPS_TRI(4);
+    TOPS_TRI(2);
 #undef TOPS_TRI
   return launched("tops_tri_attention");
 }
@@ -376,34 +449,39 @@ static int tri_attention_t(const void* xln, const void* wqkv, const void* bias, 
 
 using namespace tops;
 
-extern "C" int tops_tri_ln_bias(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln,
-                                int apply_ln, const void* WZ, const float* BZ, void* x_ln, void* bias, int64_t N,
-                                int64_t C, int64_t H, float eps, int dtype, void* stream) {
-  TOPS_REQUIRE(x && WZ && bias, "tops_tri_ln_bias: null pointer argument");
-  TOPS_REQUIRE(!apply_ln || w_ln, "tops_tri_ln_bias: w_ln is required when apply_ln != 0");
-  TOPS_REQUIRE(apply_ln || !x_ln, "tops_tri_ln_bias: x_ln must be NULL when apply_ln == 0");
-  TOPS_REQUIRE(C == 128, "tops_tri_ln_bias: C must be 128 (got %lld)", (long long)C);
-  TOPS_REQUIRE(N >= 0, "tops_tri_ln_bias: bad N");
+extern "C" int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln,
+                             int apply_ln, const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV,
+                             void* bias, int64_t N, int64_t ldn, int64_t C, int64_t H, int64_t D, float eps,
+                             float scale, int dtype, void* stream) {
+  TOPS_REQUIRE(x && wqkv && WZ && Qp && KV && bias, "tops_tri_prep: null pointer argument");
+  TOPS_REQUIRE(!apply_ln || w_ln, "tops_tri_prep: w_ln is required when apply_ln != 0");
+  TOPS_REQUIRE(C == 128 && H == 4 && D == 32,
+               "tops_tri_prep: supports C == 128, H == 4, D == 32 (got %lld, %lld, %lld)", (long long)C,
+               (long long)H, (long long)D);
+  TOPS_REQUIRE(N >= 0 && N <= 4096 && ldn >= N && ldn % 64 == 0, "tops_tri_prep: bad N / ldn");
+  TOPS_REQUIRE(sx0 % 8 == 0 && sx1 % 8 == 0, "tops_tri_prep: x token strides must be multiples of 8");
   hipStream_t st = (hipStream_t)stream;
+  const float qscale = scale * kLog2e;
   if (dtype == TOPS_DTYPE_BF16)
-    return tri_ln_bias_t<__bf16>(x, sx0, sx1, w_ln, b_ln, apply_ln, WZ, BZ, x_ln, bias, N, H, eps, st);
+    return tri_prep_t<__bf16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, eps, qscale, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tri_ln_bias_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, WZ, BZ, x_ln, bias, N, H, eps, st);
-  return fail(TOPS_EUNSUPPORTED, "tops_tri_ln_bias: unsupported dtype code %d", dtype);
+    return tri_prep_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, eps, qscale,
+                                st);
+  return fail(TOPS_EUNSUPPORTED, "tops_tri_prep: unsupported dtype code %d", dtype);
 }
 
-extern "C" int tops_tri_attention(const void* x_ln, const void* wqkv, const void* bias, const void* mask, int64_t sm0,
-                                  int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t C, int64_t H,
-                                  int64_t D, float scale, int dtype, void* stream) {
-  TOPS_REQUIRE(x_ln && wqkv && bias && out, "tops_tri_attention: null pointer argument");
-  TOPS_REQUIRE(C == 128 && D == 32, "tops_tri_attention: supports C == 128, D == 32 (got C=%lld D=%lld)",
-               (long long)C, (long long)D);
-  TOPS_REQUIRE(N >= 0 && N <= 4096, "tops_tri_attention: N must be in [0, 4096] (got %lld)", (long long)N);
-  TOPS_REQUIRE(H >= 1 && H <= 64, "tops_tri_attention: bad H %lld", (long long)H);
+extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
+                                  int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
+                                  int64_t D, int dtype, void* stream) {
+  TOPS_REQUIRE(Qp && KV && bias && out, "tops_tri_attention: null pointer argument");
+  TOPS_REQUIRE(D == 32 && H >= 1 && H <= 64, "tops_tri_attention: supports D == 32 (got D=%lld H=%lld)", (long long)D,
+               (long long)H);
+  TOPS_REQUIRE(N >= 0 && N <= 4096 && ldn >= N && ldn % 64 == 0, "tops_tri_attention: bad N / ldn");
+  TOPS_REQUIRE(so0 % 4 == 0 && so1 % 4 == 0, "tops_tri_attention: out strides must be multiples of 4");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return tri_attention_t<__bf16>(x_ln, wqkv, bias, mask, sm0, sm1, out, so0, so1, N, H, scale, st);
+    return tri_attention_t<__bf16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tri_attention_t<_Float16>(x_ln, wqkv, bias, mask, sm0, sm1, out, so0, so1, N, H, scale, st);
+    return tri_attention_t<_Float16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_attention: unsupported dtype code %d", dtype);
 }

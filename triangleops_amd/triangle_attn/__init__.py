@@ -1,4 +1,4 @@
-from .kernel import fused_gate_forward, ln_bias_forward, triangle_attn_forward
+from .kernel import attention_core, fused_gate_forward, gate_out_forward, prep_forward, triangle_attn_forward
 from .module import forward, precompute, triangle_attention
 
 __all__ = [
@@ -7,5 +7,7 @@ __all__ = [
     "forward",
     "triangle_attn_forward",
     "fused_gate_forward",
-    "ln_bias_forward",
+    "prep_forward",
+    "attention_core",
+    "gate_out_forward",
 ]

@@ -1,9 +1,11 @@
 """Low-level launchers of the gfx950 triangle-attention kernels.
 
 Same names and arguments as the reference's launchers (`triangle_attn/kernel.py:256-374`
-`triangle_attn_forward`, `:438-470` `fused_gate_forward`), plus `ln_bias_forward`, the one
-pass that produces x_ln = LN(x) and the row-shared bias together (the reference runs
-F.layer_norm and then a separate bias kernel).
+`triangle_attn_forward`, `:438-470` `fused_gate_forward`), plus the pieces `forward` uses:
+
+    prep_forward      LN(x), the row-shared bias and Q/K/V of all heads in one pass over x
+    attention_core    flash attention over the pre-pass outputs
+    gate_out_forward  sigmoid gate (optionally on LN of its input) and output projection
 """
 
 import torch
@@ -18,8 +20,13 @@ def _as(x, t):
     return t if (t.dtype == x.dtype and t.is_contiguous()) else t.to(x.dtype).contiguous()
 
 
+def row_stride(N):
+    """Padded key count of the pre-pass buffers: N rounded up to a multiple of 64."""
+    return max(64, (N + 63) // 64 * 64)
+
+
 def wqkv_from_layouts(WQ_c, WKV_c, H, D, WK_c=None, WV_c=None):
-    """(H, 3, D, C) head-major weight the attention kernel loads, from the reference layouts."""
+    """(H, 3, D, C) head-major weight the kernels load, from the reference layouts."""
     C = WQ_c.shape[0]
     if WK_c is not None and WV_c is not None:
         WK, WV = WK_c.reshape(C, H, D), WV_c.reshape(C, H, D)
@@ -30,52 +37,55 @@ def wqkv_from_layouts(WQ_c, WKV_c, H, D, WK_c=None, WV_c=None):
     return w.permute(2, 0, 3, 1).contiguous()
 
 
-def ln_bias_forward(X, W_ln, B_ln, WZ_c, BZ, *, eps=1e-5, apply_ln=True, X_ln=None, Bias_buf=None):
-    """x_ln = LN(X) (if apply_ln) and bias[h, q, k] = x_ln[q, k] . WZ_c[h] + BZ[h] in one pass.
+def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln=True):
+    """One pass over X (N, N, C): returns (Qp, KV, bias, ldn) in the attention kernel's layouts.
 
     X may be any (N, N, C) view with unit channel stride (e.g. the transposed view of the
-    ending node).  Returns (x_ln or None, bias (H, N, N)).
+    ending node).  With apply_ln=False, X is taken as already normalized.
     """
     N, N2, C = X.shape
     assert N == N2, "X must be (N, N, C)"
-    H = WZ_c.shape[0]
+    H, _, D, _ = wqkv.shape
     code = io_dtype_code(X.dtype)
-    _native.check_device(X, WZ_c, W_ln, B_ln)
+    _native.check_device(X, wqkv, WZ_c, W_ln)
     if X.stride(2) != 1 or X.stride(0) % 8 or X.stride(1) % 8:
         X = X.contiguous()
-    if apply_ln and X_ln is None:
-        X_ln = torch.empty(N, N, C, device=X.device, dtype=X.dtype)
-    if Bias_buf is None:
-        Bias_buf = torch.empty(H, N, N, device=X.device, dtype=X.dtype)
-    WZ = _as(X, WZ_c)
+    ldn = row_stride(N)
+    Qp = torch.empty(N, H, ldn, D, device=X.device, dtype=X.dtype)
+    KV = torch.empty(N, H, ldn // 64, 4096, device=X.device, dtype=X.dtype)
+    bias = torch.empty(H, N, ldn, device=X.device, dtype=X.dtype)
     BZf = None if BZ is None else BZ.float().contiguous()
     _native.call(
-        "tops_tri_ln_bias",
+        "tops_tri_prep",
         X.data_ptr(),
         X.stride(0),
         X.stride(1),
         _native.ptr(_as(X, W_ln)) if apply_ln else None,
         _native.ptr(_as(X, B_ln)) if apply_ln else None,
         1 if apply_ln else 0,
-        WZ.data_ptr(),
+        _as(X, wqkv).data_ptr(),
+        _as(X, WZ_c).data_ptr(),
         _native.ptr(BZf),
-        _native.ptr(X_ln) if apply_ln else None,
-        Bias_buf.data_ptr(),
+        Qp.data_ptr(),
+        KV.data_ptr(),
+        bias.data_ptr(),
         N,
+        ldn,
         C,
         H,
+        D,
         float(eps),
+        float(scale),
         code,
         _native.stream_of(X),
     )
-    return (X_ln if apply_ln else None), Bias_buf
+    return Qp, KV, bias, ldn
 
 
-def attention_core(X_ln, wqkv, bias, out, *, scale=1.0, mask=None):
+def attention_core(Qp, KV, bias, out, *, N, ldn, mask=None):
     """O[i, q, h*D:(h+1)*D] = softmax_k(scale Q.K + bias - 1e9 [mask[i,k] == 0]) V, written into `out`."""
-    N, _, C = X_ln.shape
-    H, _, D, _ = wqkv.shape
-    _native.check_device(X_ln, wqkv, bias, out, mask)
+    _, H, _, D = Qp.shape
+    _native.check_device(Qp, KV, bias, out, mask)
     assert out.shape == (N, N, H * D) and out.stride(2) == 1, "out must be (N, N, H*D) with unit last stride"
     m8 = None
     sm0 = sm1 = 0
@@ -84,8 +94,8 @@ def attention_core(X_ln, wqkv, bias, out, *, scale=1.0, mask=None):
         sm0, sm1 = m8.stride()
     _native.call(
         "tops_tri_attention",
-        X_ln.data_ptr(),
-        wqkv.data_ptr(),
+        Qp.data_ptr(),
+        KV.data_ptr(),
         bias.data_ptr(),
         _native.ptr(m8),
         sm0,
@@ -94,12 +104,11 @@ def attention_core(X_ln, wqkv, bias, out, *, scale=1.0, mask=None):
         out.stride(0),
         out.stride(1),
         N,
-        C,
+        ldn,
         H,
         D,
-        float(scale),
-        io_dtype_code(X_ln.dtype),
-        _native.stream_of(X_ln),
+        io_dtype_code(Qp.dtype),
+        _native.stream_of(Qp),
     )
     return out
 
@@ -118,27 +127,40 @@ def triangle_attn_forward(
     WK_c=None,
     WV_c=None,
 ):
-    """Bias projection + attention over a pre-normalized X_ln (N, N, C), written into out (N, N, H*D)."""
+    """Bias projection + attention over a pre-normalized X_ln (N, N, C), written into out (N, N, H*D).
+
+    `Bias_buf` (optional (H, N, N) scratch) receives log2(e) * bias, the form the kernel uses.
+    """
     N, N2, C = X_ln.shape
     assert N == N2
     H = WZ_c.shape[0]
     D = WQ_c.shape[1] // H
     assert WKV_c.shape == (C, 2 * H * D)
     assert out.shape == (N, N, H * D)
-    X_ln = X_ln if X_ln.is_contiguous() else X_ln.contiguous()
-    _, Bias_buf = ln_bias_forward(X_ln, None, None, WZ_c, BZ, apply_ln=False, Bias_buf=Bias_buf)
     wqkv = wqkv_from_layouts(_as(X_ln, WQ_c), _as(X_ln, WKV_c), H, D, _as(X_ln, WK_c), _as(X_ln, WV_c))
-    return attention_core(X_ln, wqkv, Bias_buf, out, scale=scale, mask=mask)
+    Qp, KV, bias, ldn = prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, scale=scale, apply_ln=False)
+    if Bias_buf is not None:
+        Bias_buf.copy_(bias[:, :, :N])
+    return attention_core(Qp, KV, bias, out, N=N, ldn=ldn, mask=mask)
 
 
-def gate_out_forward(o, gin, W_g, b_g, W_o, b_o):
-    """out = ((o * sigmoid(gin W_g^T + b_g)) -> io) W_o^T + b_o over (N1, N2, C) tokens."""
+def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
+    """out = ((o * sigmoid(g W_g^T + b_g)) -> io) W_o^T + b_o over (N1, N2, C) tokens.
+
+    g = gin, or LN(gin) with ln = (w_ln, b_ln, eps).  o and gin may be strided views with unit
+    channel stride.
+    """
     N1, N2, C = o.shape
     _native.check_device(o, gin, W_g, W_o)
     if o.stride(2) != 1 or o.stride(0) % 4 or o.stride(1) % 4:
         o = o.contiguous()
-    gin = gin if gin.is_contiguous() else gin.contiguous()
-    assert gin.numel() == N1 * N2 * C
+    gin = gin.reshape(N1, N2, C) if gin.dim() != 3 else gin
+    if gin.stride(2) != 1 or gin.stride(0) % 8 or gin.stride(1) % 8:
+        gin = gin.contiguous()
+    w_ln = b_ln = None
+    eps = 1e-5
+    if ln is not None:
+        w_ln, b_ln, eps = ln
     out = torch.empty(N1, N2, C, device=o.device, dtype=o.dtype)
     _native.call(
         "tops_gate_out",
@@ -146,6 +168,12 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o):
         o.stride(0),
         o.stride(1),
         gin.data_ptr(),
+        gin.stride(0),
+        gin.stride(1),
+        _native.ptr(_as(o, w_ln)),
+        _native.ptr(_as(o, b_ln)),
+        float(eps),
+        1 if ln is not None else 0,
         _as(o, W_g).data_ptr(),
         _native.ptr(_as(o, b_g)),
         _as(o, W_o).data_ptr(),

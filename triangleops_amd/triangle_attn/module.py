@@ -2,22 +2,22 @@
 
 Drop-in for `triangle_ops/triangle_attn/module.py` of the reference: same `precompute`,
 `forward` and one-shot signatures and precompute keys (WQ_c, WKV_c, WK_c, WV_c, WZ_c, BZ,
-W_ln, B_ln), plus `wqkv_hm`, the head-major weight the attention kernel loads.  Three
-launches per call:
+W_ln, B_ln), plus `wqkv_hm`, the head-major weight the kernels load.  Three launches per
+call:
 
-    ln_bias     x_ln = LN(x) and the row-shared bias (H, N, N) in one pass over x
-    attention   per (row, head, query chunk): K/V projection + flash attention over keys
-    gate_out    sigmoid(x_ln W_g^T) gate and W_o projection
+    prep        LN(x), the row-shared bias and Q/K/V of all heads in one pass over x
+    attention   per (row, head, query chunk): flash attention over the row's keys
+    gate_out    sigmoid(LN(x) W_g^T) gate (LN recomputed from x) and W_o projection
 
-The ending node is the same op on X.transpose(0, 1) (and mask.T): the LN pass reads the
-transposed view in place, so no transpose copy is made.  Any N is handled natively:
+The ending node is the same op on X.transpose(0, 1) (and mask.T): the pre-pass and the gate
+read the transposed view in place, so no transpose copy is made.  Any N is handled natively:
 `pad_to` is accepted for signature compatibility and ignored.
 """
 
 import torch
 
 from .._common.layouts import interleave_kv, qkv_head_major
-from .kernel import attention_core, gate_out_forward, ln_bias_forward
+from .kernel import attention_core, gate_out_forward, prep_forward
 
 
 def precompute(W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, H, D):
@@ -54,10 +54,11 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
     if wqkv.dtype != X.dtype:
         wqkv = wqkv.to(X.dtype)
     H, _, D, _ = wqkv.shape
-    X_ln, bias = ln_bias_forward(X, pre["W_ln"], pre["B_ln"], pre["WZ_c"], pre["BZ"], eps=eps)
+    Qp, KV, bias, ldn = prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], scale=scale, eps=eps)
     O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
-    attention_core(X_ln, wqkv, bias, O, scale=scale, mask=mask)
-    return gate_out_forward(O, X_ln, W_proj_g, None, W_proj_o, None)
+    attention_core(Qp, KV, bias, O, N=N, ldn=ldn, mask=mask)
+    # the gate reads LN(X); it is recomputed from X inside the gate kernel
+    return gate_out_forward(O, X, W_proj_g, None, W_proj_o, None, ln=(pre["W_ln"], pre["B_ln"], eps))
 
 
 def triangle_attention(
