@@ -82,7 +82,9 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
  *               [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]
  *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x D, d permuted) then
  *               V^T (D x 64 keys, keys permuted the same way within each 32)
- *   bias   io   (H, N, ldn): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]), zeros for k >= N
+ *   bias   io   (H, ceil(N/32), ldn/32, 1024): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]) per
+ *               32 x 32 (query, key) tile; (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e) at
+ *               element (64 j + 32 hl + c) * 8 + e of tile (qt, kt); zeros for k >= N
  * C == 128, H == 4, D == 32.
  */
 int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,

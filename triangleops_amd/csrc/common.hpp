@@ -36,6 +36,11 @@ struct Mma<__bf16> {
   __device__ static inline f32x4 m16(vec<__bf16, 8> a, vec<__bf16, 8> b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // c + a.x * b.x + a.y * b.y with fp32 products and sum (v_dot2c_f32_bf16)
+  __device__ static inline float dot2(vec<__bf16, 2> a, vec<__bf16, 2> b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+  static constexpr float kMaxP = 18446744073709551616.0f;  // 2^64: bf16 keeps fp32's range
 };
 
 template <>
@@ -46,7 +51,27 @@ struct Mma<_Float16> {
   __device__ static inline f32x4 m16(vec<_Float16, 8> a, vec<_Float16, 8> b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
+  __device__ static inline float dot2(vec<_Float16, 2> a, vec<_Float16, 2> b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+  }
+  static constexpr float kMaxP = 32768.0f;  // 2^15: below fp16's largest finite value 65504
 };
+
+// acc + the sum of the 8 elements of `a`, in fp32 (4 packed-pair dot products against 1.0).
+template <typename T>
+__device__ inline float sum8(vec<T, 8> a, float acc) {
+  const vec<T, 2> one = {(T)1.0f, (T)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = Mma<T>::dot2(vec<T, 2>{a[e], a[e + 1]}, one, acc);
+  return acc;
+}
+
+// Pins `v` in registers at this point of the program: the compiler must compute it here and
+// may not sink its computation into a later branch.
+template <typename V>
+__device__ inline void pin(V& v) {
+  asm volatile("" : "+v"(v));
+}
 
 template <typename V>
 __device__ inline V ldg(const void* p) {

@@ -6,7 +6,9 @@
 //                       Qp  [i][h][q][32]    Q * scale * log2(e), d permuted (below)
 //                       KV  [i][h][kb][4096] per 64-key block: K [64 keys][32 d permuted] then
 //                                            V^T [32 d][64 keys permuted]
-//                       bias[h][q][ldn]      log2(e) * bias, rows padded with zeros to ldn
+//                       bias[h][qt][kt][1024] log2(e) * bias per 32 x 32 (query, key) tile, in
+//                                            the order of the MFMA B operand (below); keys
+//                                            >= N hold zeros
 //   tri_attn_kernel   4 waves per (row i, head h, query chunk): the KV block of each 64 keys is
 //                     copied into LDS (double-buffered, one barrier per block), each wave
 //                     streams its query tiles over it with an online softmax in the exp2
@@ -18,6 +20,9 @@
 // i.e. position 16 j + 8 hl + e (j = 0, 1; hl = lane / 32; e < 8) holds the element that the
 // MFMA D register v = 8 j + e of lane half hl holds (8 (v / 4) + 4 hl + v % 4), so every MFMA
 // operand of the attention kernel is one 16-byte load.
+// Bias tile (query tile qt, key tile kt): element (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e)
+// sits at (64 j + 32 hl + c) * 8 + e, so the B operand of half j for lane (c, hl) is 16 bytes
+// and one load instruction of a wave reads 1 KB contiguous.
 //
 // Reference: triangle_attn/module.py:57-125 (forward), triangle_attn/kernel.py:36-98 (bias),
 // :110-253 (attention), :230-238 and :369 (additive -1e9 pair mask, -inf outside the row).
@@ -50,7 +55,7 @@ __global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
   const int h = wave;
-  const int64_t nkb = ldn / 64;
+  const int64_t nkb = ldn / 64, nkt = ldn / 32, nqt = (N + 31) / 32;
 
   V8 wq[8], wk[8], wv[8];
   {
@@ -109,8 +114,11 @@ __global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ 
           for (int j = 0; j < 8; ++j) d += v[8 * e + j] * (float)w8[j];
         }
         d = group_sum<4>(d);
-        if (part == 0)
-          bias[((int64_t)hh * N + i) * ldn + p] = p < N ? (T)((d + (BZ ? BZ[hh] : 0.f)) * bias_scale) : (T)0.f;
+        if (part == 0) {
+          const int64_t off = (((int64_t)hh * nqt + i / 32) * nkt + p / 32) * 1024 +
+                              ((((p % 32) / 16) * 64 + ((p % 16) / 8) * 32 + i % 32) * 8 + p % 8);
+          bias[off] = p < N ? (T)((d + (BZ ? BZ[hh] : 0.f)) * bias_scale) : (T)0.f;
+        }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -158,7 +166,8 @@ __global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention core.  4 waves, QT query tiles (32 queries) per wave, 64-key blocks.
+// Attention core.  4 waves, QT query tiles (32 queries) per wave, 64-key blocks of two 32-key
+// tiles.
 //
 // Per (32-key tile, query tile) a wave runs
 //     S^T  = C0 + I . bias^T          2 MFMAs, A = identity, B = 16 bias bytes per lane
@@ -166,18 +175,25 @@ __global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ 
 //     P    = exp2(S^T), l += rowsum   16 v_exp per lane, no max / subtract per element
 //     O^T += V^T . P^T                2 MFMAs, V^T from LDS, P^T = S^T's D registers
 // where C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m
-// is exact after the first tile and is only raised when a tile's probabilities could exceed
-// 2^64 (then O and l are rescaled and the tile recomputed), so the common path needs neither
-// a max nor a subtraction per score.  Masked keys get probability exactly 0 (equal to the
-// reference's exp(-1e9 - m) in fp32 whenever the row has a valid key); a row without valid
-// keys takes the uniform average of V over all N keys, as the reference's -1e9 add gives.
-// The identity MFMA multiplies every bias element of the tile by 0 or 1, so the bias padding
-// must be finite (the pre-pass writes zeros there).
+// is exact from the first tile with a valid key on and is only raised when a tile's
+// probabilities could overflow the I/O type (then O and l are rescaled and the tile
+// recomputed), so the common path needs neither a max nor a subtraction per score.  Masked
+// keys get probability exactly 0 (equal to the reference's exp(-1e9 - m) in fp32 whenever the
+// row has a valid key); a row without valid keys takes the uniform average of V over all N
+// keys, as the reference's -1e9 add gives.  The identity MFMA multiplies every bias element
+// of the tile by 0 or 1, so the bias padding must be finite (the pre-pass writes zeros).
+//
+// Each tile is one straight-line phase in which the score MFMAs of the NEXT tile are
+// interleaved (sched_group_barrier) with the exponentials of the current one, so the matrix
+// cores and the VALU of one wave work at the same time; the rare paths (partial tile, first
+// max, overflow) branch around the phase.
 // ---------------------------------------------------------------------------------------------
 constexpr int kKPad = 40;  // LDS row of K: 32 d + 8 pad (conflict-free 16-byte operand reads)
 constexpr int kVPad = 72;  // LDS row of V^T: 64 keys + 8 pad
 constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
-constexpr float kOverflow = 18446744073709551616.0f;  // 2^64
+
+// scheduling-group masks of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
 template <typename T, int QT>
 __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
@@ -188,20 +204,21 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
 
-  __shared__ __attribute__((aligned(16))) T kvs[2][kKVLds];
+  __shared__ __attribute__((aligned(16))) T kvs[3][kKVLds];
   __shared__ unsigned long long kvalid[64];  // per 64-key block (N <= 4096)
   __shared__ short vblk[64];                 // indices of blocks with a valid key
   __shared__ int nvblk, row_any;
 
-  // ---- block -> (row i, head h, query chunk); XCD-aware: an XCD works on one head and a
-  // ---- contiguous range of query chunks for all rows, so that head's bias stays in its L2.
+  // ---- block -> (row i, head h, query chunk); XCD-aware: an XCD works through a contiguous
+  // ---- range of rows of one head, all query chunks of a row at once, so each KV block is read
+  // ---- from HBM once and shared in that XCD's L2, as is the head's bias across rows.
   const int64_t total = N * H * nqc;
   int64_t id = blockIdx.x;
   if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
-  const int64_t i = id % N;
-  const int hq = (int)(id / N);
-  const int qc = hq % nqc;
-  const int h = hq / nqc;
+  const int qc = (int)(id % nqc);
+  const int64_t ih = id / nqc;
+  const int64_t i = ih % N;
+  const int h = (int)(ih / N);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
@@ -231,12 +248,13 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     nvblk = n;
   }
   __syncthreads();
-  const int nv = nvblk;
+  const int nv = nvblk;  // >= 1 whenever N >= 1
 
   const T* kvrow = KV + ((int64_t)i * H + h) * nkb * kKVBlock;
-  const T* brow0 = bias + (int64_t)h * N * ldn;
+  const int64_t nqt = (N + 31) / 32;
 
-  // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) ----
+  // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) and bias pointers.
+  // ---- A row without valid keys zeroes Q and the identity, so its scores are all C0. ----
   const int64_t qbase = (int64_t)qc * (NW * 32 * QT) + (int64_t)wave * 32 * QT;
   V8 qop[QT][2];
   const T* bq[QT];
@@ -245,41 +263,35 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     int64_t q = qbase + 32 * t + col;
     q = q < N ? q : N - 1;
     const T* qr = Qp + (((int64_t)i * H + h) * ldn + q) * D + 8 * hl;
-    qop[t][0] = ldg<V8>(qr);
-    qop[t][1] = ldg<V8>(qr + 16);
-    bq[t] = brow0 + q * ldn + 8 * hl;
+    qop[t][0] = uniform ? V8{} : ldg<V8>(qr);
+    qop[t][1] = uniform ? V8{} : ldg<V8>(qr + 16);
+    bq[t] = bias + ((int64_t)h * nqt + q / 32) * (2 * nkb) * 1024 + (32 * hl + q % 32) * 8;
   }
-  // ---- identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j ----
+  // identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j
   V8 ident[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
+    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((!uniform && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
 
-  // KV block copy: thread t moves elements [16 t, 16 t + 16) (K rows, then V^T rows)
+  // KV block copy: thread t moves 16-byte chunks t (K: row t / 4) and 256 + t (V^T: row t / 8);
+  // each load instruction of a wave reads 1 KB contiguous.
   auto kv_load = [&](int kb, V8* r) {
-    const T* src = kvrow + (int64_t)kb * kKVBlock + 16 * tid;
+    const T* src = kvrow + (int64_t)kb * kKVBlock + 8 * tid;
     r[0] = ldg<V8>(src);
-    r[1] = ldg<V8>(src + 8);
+    r[1] = ldg<V8>(src + 64 * D);
   };
   auto kv_store = [&](int buf, const V8* r) {
-    const int e = 16 * tid;
-    T* dst;
-    if (e < 64 * D)
-      dst = &kvs[buf][(e / D) * kKPad + (e % D)];
-    else
-      dst = &kvs[buf][64 * kKPad + ((e - 64 * D) / 64) * kVPad + ((e - 64 * D) % 64)];
-    *reinterpret_cast<V8*>(dst) = r[0];
-    *reinterpret_cast<V8*>(dst + 8) = r[1];
+    *reinterpret_cast<V8*>(&kvs[buf][(tid / 4) * kKPad + 8 * (tid % 4)]) = r[0];
+    *reinterpret_cast<V8*>(&kvs[buf][64 * kKPad + (tid / 8) * kVPad + 8 * (tid % 8)]) = r[1];
   };
-  // bias B operands of one 32-key tile of a block: [query tile t][half j], 16 bytes per lane
+  // bias B operands of one 32-key tile: [query tile t][half j], 16 bytes per lane
   auto load_bias = [&](int kb, int kt, V8 (*bb)[2]) {
 #pragma unroll
     for (int t = 0; t < QT; ++t)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bb[t][j] = uniform ? V8{} : ldg<V8>(bq[t] + kb * 64 + 32 * kt + 16 * j);
+      for (int j = 0; j < 2; ++j) bb[t][j] = ldg<V8>(bq[t] + (int64_t)(2 * kb + kt) * 1024 + 512 * j);
   };
-
   f32x16 o[QT], cinit[QT];
   float l[QT];
 #pragma unroll
@@ -288,110 +300,145 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     cinit[t] = f32x16{};
     l[t] = 0.f;
   }
-
   bool first = true;
-  auto tile = [&](int buf, int kt, unsigned int tbits, V8 (*bb)[2]) {
-    const bool full = tbits == 0xffffffffu;
+
+  // scores of one 32-key tile for all query tiles
+  auto scores = [&](const V8* kop, V8 (*bb)[2], f32x16* s) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      s[t] = Mma<T>::m32(ident[0], bb[t][0], cinit[t]);
+      s[t] = Mma<T>::m32(ident[1], bb[t][1], s[t]);
+      s[t] = Mma<T>::m32(kop[0], qop[t][0], s[t]);
+      s[t] = Mma<T>::m32(kop[1], qop[t][1], s[t]);
+    }
+  };
+
+  // One tile.  buf / kt / tb: its LDS buffer, tile within the block and valid-key bits; s: its
+  // scores.  nbuf / nkt / bn / snext: the next tile's buffer, tile, bias operands and score
+  // registers.  (rkb, rkt): the bias tile loaded into bn once the score MFMAs have read it.
+  auto phase = [&](int buf, int kt, unsigned int tb, f32x16* s, int nbuf, int nkt, V8 (*bn)[2], f32x16* snext,
+                   int rkb, int rkt) {
+    if (tb != 0xffffffffu) {  // partial tile (wave-uniform): masked keys get probability 0
+      const unsigned int lb = tb >> (4 * hl);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const bool ok = (lb >> (8 * (v / 4) + (v % 4))) & 1u;
+#pragma unroll
+        for (int t = 0; t < QT; ++t) s[t][v] = ok ? s[t][v] : -INFINITY;
+      }
+    }
+    // ---- straight line: next tile's score MFMAs interleaved with this tile's exponentials ----
     V8 kop[2], vop[2];
     {
-      const T* kr = &kvs[buf][(32 * kt + col) * kKPad + 8 * hl];
+      const T* kr = &kvs[nbuf][(32 * nkt + col) * kKPad + 8 * hl];
       kop[0] = *reinterpret_cast<const V8*>(kr);
       kop[1] = *reinterpret_cast<const V8*>(kr + 16);
       const T* vr = &kvs[buf][64 * kKPad + col * kVPad + 32 * kt + 8 * hl];
       vop[0] = *reinterpret_cast<const V8*>(vr);
       vop[1] = *reinterpret_cast<const V8*>(vr + 16);
     }
-    // all score tiles first, so their MFMAs overlap the exponentials of the previous one
-    f32x16 s[QT];
+    scores(kop, bn, snext);
+    load_bias(rkb, rkt, bn);
+    V8 p[QT][2];
+    float ps[QT];
+    bool over = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      s[t] = cinit[t];
-      if (!uniform) {
-        s[t] = Mma<T>::m32(ident[0], bb[t][0], s[t]);
-        s[t] = Mma<T>::m32(ident[1], bb[t][1], s[t]);
-        s[t] = Mma<T>::m32(kop[0], qop[t][0], s[t]);
-        s[t] = Mma<T>::m32(kop[1], qop[t][1], s[t]);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      if (!full) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int kk = 8 * (v / 4) + 4 * hl + (v % 4);
-          if (!((tbits >> kk) & 1u)) s[t][v] = -INFINITY;
-        }
-      }
-      if (first) {  // exact running max from the first visited tile (wave-uniform)
-        float mt = s[t][0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, s[t][v]);
-        mt = halves_max(mt);  // finite: the tile has a valid key
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s[t][v] -= mt;
-        cinit[t] -= mt;
-      }
-      float p[16], ps = 0.f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        p[v] = fast_exp2(s[t][v]);
-        ps += p[v];
-      }
-      if (__ballot(!(ps <= kOverflow)) != 0) {  // rare: raise the running max of this tile
-        float mt = s[t][0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mt = fmaxf(mt, s[t][v]);
-        mt = fmaxf(halves_max(mt), 0.f);
-        const float alpha = fast_exp2(-mt);
-        ps = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          p[v] = fast_exp2(s[t][v] - mt);
-          ps += p[v];
-          o[t][v] *= alpha;
-        }
-        l[t] *= alpha;
-        cinit[t] -= mt;
-      }
-      l[t] += ps;
-      V8 p0, p1;
 #pragma unroll
       for (int v = 0; v < 8; ++v) {
-        p0[v] = (T)p[v];
-        p1[v] = (T)p[8 + v];
+        p[t][0][v] = (T)fast_exp2(s[t][v]);
+        p[t][1][v] = (T)fast_exp2(s[t][8 + v]);
       }
-      o[t] = Mma<T>::m32(vop[0], p0, o[t]);
-      o[t] = Mma<T>::m32(vop[1], p1, o[t]);
+      // row sum of the rounded weights the PV product uses (packed dot products)
+      ps[t] = sum8<T>(p[t][0], 0.f) + sum8<T>(p[t][1], 0.f);
+      over |= !(ps[t] <= Mma<T>::kMaxP);
+      pin(p[t][0]);
+      pin(p[t][1]);
     }
-    first = false;
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+    for (int m = 0; m < 2 * QT; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 9, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 2 * QT, 0);
+#pragma unroll
+    for (int m = 0; m < 2 * QT; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 9, 0);
+    }
+    // ---- rare: the first tile with a valid key sets the exact max; later tiles raise it only
+    // ---- when a probability could overflow the I/O type ----
+    const bool rare = (__ballot(over) != 0) | (first & (tb != 0));
+    if (rare) {
+#pragma unroll
+      for (int t = 0; t < QT; ++t) {
+        float mr = s[t][0];
+#pragma unroll
+        for (int v = 1; v < 16; ++v) mr = fmaxf(mr, s[t][v]);
+        mr = halves_max(mr);
+        const float mt = first ? mr : fmaxf(mr, 0.f);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          p[t][0][v] = (T)fast_exp2(s[t][v] - mt);
+          p[t][1][v] = (T)fast_exp2(s[t][8 + v] - mt);
+        }
+        ps[t] = sum8<T>(p[t][0], 0.f) + sum8<T>(p[t][1], 0.f);
+        if (!first) {  // O and l are still zero before the first valid tile
+          const float alpha = fast_exp2(-mt);
+          o[t] *= alpha;
+          l[t] *= alpha;
+        }
+        cinit[t] -= mt;
+        snext[t] -= mt;
+      }
+      first = false;
+    }
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      l[t] += ps[t];
+      o[t] = Mma<T>::m32(vop[0], p[t][0], o[t]);
+      o[t] = Mma<T>::m32(vop[1], p[t][1], o[t]);
+    }
   };
 
-  // Pipeline per visited block j: the next KV block and this block's tile-1 bias are loaded
-  // while tile 0 runs, the next block's tile-0 bias while tile 1 runs; the next KV block goes
-  // to the other LDS buffer before the single barrier.
-  V8 kvr[2];
-  V8 bt0[QT][2], bt1[QT][2];
-  if (nv > 0) {
-    kv_load(vblk[0], kvr);
-    load_bias(vblk[0], 0, bt0);
-    kv_store(0, kvr);
-  }
+  // Tiles (j, 0), (j, 1) of the visited blocks j in order.  Scores of tile (j, 0) live in sA,
+  // of (j, 1) in sB, their bias operands in bA / bB, each loaded two tiles ahead.  KV blocks
+  // rotate through three LDS buffers (the buffer written at block j was last read before the
+  // previous barrier) and are loaded into registers two blocks ahead.  One barrier per block.
+  // Past the last block the pipeline recomputes a tile of the last block (results unused).
+  f32x16 sA[QT], sB[QT];
+  V8 bA[QT][2], bB[QT][2];
+  V8 kvA[2], kvB[2];
+  auto blk = [&](int j) { return (int)vblk[j < nv ? j : nv - 1]; };
+  kv_load(blk(0), kvA);
+  load_bias(blk(0), 0, bA);
+  load_bias(blk(0), 1, bB);
+  if (nv > 1) kv_load(blk(1), kvB);
+  kv_store(0, kvA);
   __syncthreads();
-
-  for (int j = 0; j < nv; ++j) {
-    const int kb = vblk[j];
-    const int buf = j & 1;
+  {
+    V8 kop[2];
+    const T* kr = &kvs[0][col * kKPad + 8 * hl];
+    kop[0] = *reinterpret_cast<const V8*>(kr);
+    kop[1] = *reinterpret_cast<const V8*>(kr + 16);
+    scores(kop, bA, sA);
+    load_bias(blk(1), 0, bA);
+  }
+  auto block = [&](int j, V8* kload, const V8* kstore) {
+    const int buf = j % 3, nbuf = (j + 1) % 3;
     const bool more = j + 1 < nv;
-    const int kbn = more ? vblk[j + 1] : kb;
-    const unsigned long long kbits = kvalid[kb];
-    const unsigned int tb0 = (unsigned int)kbits, tb1 = (unsigned int)(kbits >> 32);
-    if (more) kv_load(kbn, kvr);
-    load_bias(kb, 1, bt1);
-    if (tb0) tile(buf, 0, tb0, bt0);  // wave-uniform
-    if (more) load_bias(kbn, 0, bt0);
-    if (tb1) tile(buf, 1, tb1, bt1);
-    if (more) kv_store(buf ^ 1, kvr);
+    const unsigned long long kbits = kvalid[vblk[j]];
+    const int kb1 = blk(j + 1), kb2 = blk(j + 2);
+    if (j + 2 < nv) kv_load(kb2, kload);
+    phase(buf, 0, (unsigned int)kbits, sA, buf, 1, bB, sB, kb1, 1);
+    if (more) kv_store(nbuf, kstore);
     __syncthreads();
+    phase(buf, 1, (unsigned int)(kbits >> 32), sB, more ? nbuf : buf, 0, bA, sA, kb2, 0);
+  };
+  for (int j = 0; j < nv; j += 2) {
+    block(j, kvA, kvB);
+    if (j + 1 < nv) block(j + 1, kvB, kvA);
   }
 
   // ---- normalise and store O[i, q, h*D + d] ----
@@ -410,7 +457,6 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     }
   }
 }
-
 template <typename T>
 static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                       const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,

@@ -53,7 +53,7 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
     ldn = row_stride(N)
     Qp = torch.empty(N, H, ldn, D, device=X.device, dtype=X.dtype)
     KV = torch.empty(N, H, ldn // 64, 4096, device=X.device, dtype=X.dtype)
-    bias = torch.empty(H, N, ldn, device=X.device, dtype=X.dtype)
+    bias = torch.empty(H, (N + 31) // 32, ldn // 32, 1024, device=X.device, dtype=X.dtype)
     BZf = None if BZ is None else BZ.float().contiguous()
     _native.call(
         "tops_tri_prep",
@@ -80,6 +80,13 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
         _native.stream_of(X),
     )
     return Qp, KV, bias, ldn
+
+
+def untile_bias(bias, N):
+    """(H, N, N) view-copy of the pre-pass bias tiles (log2(e)-scaled, see tops_tri_prep)."""
+    H, nqt, nkt, _ = bias.shape
+    t = bias.view(H, nqt, nkt, 2, 2, 32, 8).permute(0, 1, 5, 2, 3, 4, 6)  # h, qt, c, kt, j, hl, e
+    return t.reshape(H, nqt * 32, nkt * 32)[:, :N, :N]
 
 
 def attention_core(Qp, KV, bias, out, *, N, ldn, mask=None):
@@ -140,7 +147,7 @@ def triangle_attn_forward(
     wqkv = wqkv_from_layouts(_as(X_ln, WQ_c), _as(X_ln, WKV_c), H, D, _as(X_ln, WK_c), _as(X_ln, WV_c))
     Qp, KV, bias, ldn = prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, scale=scale, apply_ln=False)
     if Bias_buf is not None:
-        Bias_buf.copy_(bias[:, :, :N])
+        Bias_buf.copy_(untile_bias(bias, N))
     return attention_core(Qp, KV, bias, out, N=N, ldn=ldn, mask=mask)
 
 
