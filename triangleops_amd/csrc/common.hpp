@@ -66,6 +66,25 @@ __device__ inline float sum8(vec<T, 8> a, float acc) {
   return acc;
 }
 
+// Division by a runtime constant d >= 1 of 32-bit unsigned n (Granlund-Montgomery): a multiply-
+// high, an add and a shift, all scalar when n is wave-uniform.
+struct FastDiv {
+  uint32_t d, m, s;
+  __host__ __device__ FastDiv() : d(1), m(1), s(0) {}
+  __host__ explicit FastDiv(uint32_t div) : d(div), m(0), s(0) {
+    while ((1ull << s) < div) ++s;
+    m = (uint32_t)(((1ull << 32) * ((1ull << s) - div)) / div + 1);
+  }
+  __host__ __device__ uint32_t div(uint32_t n) const {
+#ifdef __HIP_DEVICE_COMPILE__
+    const uint32_t hi = __umulhi(n, m);
+#else
+    const uint32_t hi = (uint32_t)(((uint64_t)n * m) >> 32);
+#endif
+    return (uint32_t)(((uint64_t)hi + n) >> s);
+  }
+};
+
 // Pins `v` in registers at this point of the program: the compiler must compute it here and
 // may not sink its computation into a later branch.
 template <typename V>

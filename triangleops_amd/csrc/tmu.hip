@@ -30,134 +30,192 @@ __device__ inline GridTile grid_tile(int64_t t, int64_t L, int tiles_per_row) {
   return g;
 }
 
+// Tile coordinates with scalar divisions (tile indices are wave-uniform).
+__device__ inline GridTile grid_tile_fast(uint32_t t, const FastDiv& tpr, const FastDiv& Ld) {
+  GridTile g;
+  const uint32_t rr = tpr.div(t);
+  g.c0 = (int64_t)(t - rr * tpr.d) * 64;
+  const uint32_t b = Ld.div(rr);
+  g.r = rr - b * Ld.d;
+  g.b = b;
+  return g;
+}
+
 // ---------------------------------------------------------------------------------------------
-// Input phase.  NW waves; wave w owns output features [32w, 32w + 32) of both P and G, keeping
-// its weight rows in registers (A operand).  A block processes 64-token tiles in a grid-stride
-// loop: the x tile is staged once in LDS (XOR-swizzled 16-byte chunks) and read by all waves
-// as the B operand.  D = W . x^T lands with one token per lane column, so the per-token LN
-// statistics are a per-lane scalar in the epilogue.
+// Input phase.  NW waves; wave w owns output features f = 32w + lane%32 of both P and G, with
+// its weight rows in registers as the MFMA B operand.  A block walks 64-token tiles in a
+// grid-stride loop, with two roles: waves [0, NW/2) fetch x (three tiles ahead, in a ring of
+// register stages) and waves [NW/2, NW) write the results, so neither role ever has loads and
+// stores outstanding together and the in-order memory counter waits only for the stage being
+// consumed.  The loaders normalise each token with its LayerNorm statistics (one pass, fp32,
+// packed dot products) on the way into LDS, so the GEMM yields LN(x) . Wc^T directly and the
+// epilogue is a bias add and the gate.  The A operand reads tokens in a permuted order so
+// that D = x . W^T leaves 16 consecutive tokens of one feature in each lane; the gated result
+// goes through a feature-major LDS tile and every store instruction writes whole 128-byte
+// rows (8 features x 64 tokens) of the channel-major output.
 // ---------------------------------------------------------------------------------------------
 template <typename T, int C, int NW>
 __global__ __launch_bounds__(NW * 64) void tmu_in_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
                                                         const T* __restrict__ Wp, const T* __restrict__ Wg,
-                                                        const float* __restrict__ sWp, const float* __restrict__ sWg,
                                                         const float* __restrict__ Bp, const float* __restrict__ Bg,
                                                         T* __restrict__ ab, int64_t L, int64_t ld, int64_t fstride,
-                                                        int transpose, float eps, int64_t ntiles, int tiles_per_row) {
+                                                        int transpose, float eps, uint32_t ntiles, FastDiv tpr,
+                                                        FastDiv Ld) {
   constexpr int NT = NW * 64;
-  constexpr int TPT = NT / 64;           // threads per token
-  constexpr int CPT = (C / 8) / TPT;     // 16-byte chunks per thread
-  constexpr int ROW = C * 2;             // LDS bytes per token row
-  constexpr int KS = C / 16;             // MFMA k-steps
+  constexpr int NL = NT / 2;          // loader threads
+  constexpr int TPT = NL / 64;        // loader threads per token
+  constexpr int CPT = (C / 8) / TPT;  // 16-byte chunks per loader thread
+  constexpr int ROW = C * 2;          // LDS bytes per token row
+  constexpr int KS = C / 16;          // MFMA k-steps
+  constexpr int PD = 3;               // register stages in flight
   static_assert(CPT * TPT * 8 == C, "channel split");
   using V8 = vec<T, 8>;
+  using V2 = vec<T, 2>;
 
-  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];
-  __shared__ float st_mean[2][64], st_rstd[2][64], st_mask[2][64];
+  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x tile
+  __shared__ __attribute__((aligned(16))) float smask[2][64];
+  __shared__ __attribute__((aligned(16))) T os[NW * 32 * 64];  // gated tile, [feature][token]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
+  const int f = wave * 32 + col;
 
   V8 wp[KS], wg[KS];
-  {
-    const int64_t frow = (int64_t)(wave * 32 + col) * C;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      wp[s] = ldg<V8>(Wp + frow + 16 * s + 8 * hl);
-      wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+  for (int s = 0; s < KS; ++s) {
+    wp[s] = ldg<V8>(Wp + (int64_t)f * C + 16 * s + 8 * hl);
+    wg[s] = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
+  }
+  const float cbp = Bp[f], cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
+
+  // token of MFMA row r: 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3), so D slot v of lane
+  // half hl is token 16 hl + v of the 32-token sub-tile
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+  // GEMMs + gate of one staged tile -> feature-major LDS tile (all waves)
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int tok = sub * 32 + prow;
+      f32x16 accP = {}, accG = {};
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const V8 xa = *reinterpret_cast<const V8*>(&xs[buf][tok * ROW + (((2 * k + hl) ^ (tok & 7)) << 4)]);
+        accP = Mma<T>::m32(xa, wp[k], accP);
+        accG = Mma<T>::m32(xa, wg[k], accG);
+      }
+      const int tb = sub * 32 + 16 * hl;  // first of this lane's 16 tokens
+      V8 o[2];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 rm = *reinterpret_cast<const f32x4*>(&smask[buf][tb + 4 * gq]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int v = 4 * gq + j;
+          const float P = accP[v] + cbp;
+          const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+          o[v / 8][v % 8] = (T)(P * gate * rm[j]);
+        }
+      }
+      // 16-byte chunks c = tb / 8 + {0, 1} of feature row f, XOR-swizzled by (f >> 1) & 7
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = tb / 8 + h;
+        *reinterpret_cast<V8*>(&os[f * 64 + ((c ^ ((f >> 1) & 7)) << 3)]) = o[h];
+      }
     }
-  }
-  float csp[16], cbp[16], csg[16], cbg[16];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int f = wave * 32 + 8 * (v / 4) + 4 * hl + (v % 4);
-    csp[v] = sWp[f];
-    cbp[v] = Bp[f];
-    csg[v] = sWg[f];
-    cbg[v] = Bg[f];
-  }
+  };
 
-  const int my_tok = tid / TPT, my_part = tid % TPT;
-  V8 xr[CPT];
-  float mval = 0.f;
-
-  auto load_tile = [&](int64_t t) {
-    const GridTile g = grid_tile(t, L, tiles_per_row);
-    const int64_t c = g.c0 + my_tok;
-    if (c < L) {
+  const uint32_t G = gridDim.x;
+  uint32_t t = blockIdx.x;
+  if (wave < NW / 2) {
+    // ================= loaders =================
+    const int my_tok = tid / TPT, my_part = tid % TPT;
+    struct Stage {
+      V8 x[CPT];
+      int mb;   // raw mask byte and position flag, combined when the stage is consumed so
+      bool ok;  // the fetch itself never waits for its loads
+    };
+    // Every fetch issues the same loads (past the end it reloads the last tile; positions
+    // c >= L read token L - 1 and get mask 0), keeping the memory-counter accounting exact.
+    auto fetch = [&](uint32_t tt, Stage& sg) {
+      tt = tt < ntiles ? tt : ntiles - 1;
+      const GridTile g = grid_tile_fast(tt, tpr, Ld);
+      int64_t c = g.c0 + my_tok;
+      const bool ok = c < L;
+      c = ok ? c : L - 1;
       const int64_t i = transpose ? c : g.r, j = transpose ? g.r : c;
       const int64_t tok = (g.b * L + i) * L + j;
       const T* src = x + tok * C + my_part * CPT * 8;
 #pragma unroll
-      for (int e = 0; e < CPT; ++e) xr[e] = ldg<V8>(src + 8 * e);
-      mval = mask ? (float)mask[tok] : 1.f;
-    } else {
+      for (int e = 0; e < CPT; ++e) sg.x[e] = ldg<V8>(src + 8 * e);
+      sg.mb = *(mask ? mask + tok : reinterpret_cast<const int8_t*>(x));
+      sg.ok = ok;
+    };
+    auto step = [&](uint32_t tt, int buf, Stage& sg) {
+      // LayerNorm of this thread's token (sum and sum of squares in fp32) -> LDS
+      float s1 = 0.f, s2 = 0.f;
+      const V2 one = {(T)1.f, (T)1.f};
 #pragma unroll
-      for (int e = 0; e < CPT; ++e) xr[e] = V8{};
-      mval = 0.f;
-    }
-  };
-
-  int64_t tile = blockIdx.x;
-  if (tile >= ntiles) return;
-  load_tile(tile);
-  int buf = 0;
-  for (; tile < ntiles; tile += gridDim.x) {
-    // LayerNorm statistics of this thread's token (two-pass, fp32).
-    float s = 0.f;
+      for (int e = 0; e < CPT; ++e)
 #pragma unroll
-    for (int e = 0; e < CPT; ++e)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) s += (float)xr[e][k];
-    const float mean = group_sum<TPT>(s) * (1.0f / C);
-    float q = 0.f;
-#pragma unroll
-    for (int e = 0; e < CPT; ++e)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float d = (float)xr[e][k] - mean;
-        q += d * d;
-      }
-    const float rstd = rsqrtf(group_sum<TPT>(q) * (1.0f / C) + eps);
-
-#pragma unroll
-    for (int e = 0; e < CPT; ++e) {
-      const int chunk = my_part * CPT + e;
-      *reinterpret_cast<V8*>(&xs[buf][my_tok * ROW + ((chunk ^ (my_tok & 7)) << 4)]) = xr[e];
-    }
-    if (my_part == 0) {
-      st_mean[buf][my_tok] = mean;
-      st_rstd[buf][my_tok] = rstd;
-      st_mask[buf][my_tok] = mval;
-    }
-    __syncthreads();
-
-    if (tile + gridDim.x < ntiles) load_tile(tile + gridDim.x);
-
-    const GridTile g = grid_tile(tile, L, tiles_per_row);
-    T* dst = ab + (g.b * L + g.r) * ld + g.c0;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int tok = sub * 32 + col;
-      f32x16 accP = {}, accG = {};
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const V8 xb = *reinterpret_cast<const V8*>(&xs[buf][tok * ROW + (((2 * k + hl) ^ (tok & 7)) << 4)]);
-        accP = Mma<T>::m32(wp[k], xb, accP);
-        accG = Mma<T>::m32(wg[k], xb, accG);
-      }
-      const float mu = st_mean[buf][tok], rs = st_rstd[buf][tok], mk = st_mask[buf][tok];
-      if (g.c0 + tok < ld) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float P = rs * (accP[v] - mu * csp[v]) + cbp[v];
-          const float G = rs * (accG[v] - mu * csg[v]) + cbg[v];
-          const int f = wave * 32 + 8 * (v / 4) + 4 * hl + (v % 4);
-          dst[f * fstride + tok] = (T)(P * sigmoid(G) * mk);
+        for (int k = 0; k < 8; k += 2) {
+          const V2 pr = {sg.x[e][k], sg.x[e][k + 1]};
+          s1 = Mma<T>::dot2(pr, one, s1);
+          s2 = Mma<T>::dot2(pr, pr, s2);
         }
+      const float mean = group_sum<TPT>(s1) * (1.0f / C);
+      const float var = fmaxf(group_sum<TPT>(s2) * (1.0f / C) - mean * mean, 0.f);
+      const float rstd = rsqrtf(var + eps), shift = -mean * rstd;
+#pragma unroll
+      for (int e = 0; e < CPT; ++e) {
+        V8 h;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) h[k] = (T)((float)sg.x[e][k] * rstd + shift);
+        const int chunk = my_part * CPT + e;
+        *reinterpret_cast<V8*>(&xs[buf][my_tok * ROW + ((chunk ^ (my_tok & 7)) << 4)]) = h;
       }
+      // every thread of the token stores the same value: no divergent branch in the loop (it
+      // would make the compiler wait for all outstanding loads at the loop head)
+      smask[buf][my_tok] = sg.ok ? (mask ? (float)sg.mb : 1.f) : 0.f;
+      __syncthreads();
+      fetch(tt + PD * G, sg);  // refill this stage
+      compute(buf);
+      __syncthreads();
+    };
+    int buf = 0;
+    Stage s0, s1, s2;
+    fetch(t, s0);
+    fetch(t + G, s1);
+    fetch(t + 2 * G, s2);
+    for (; t < ntiles; t += 3 * G) {  // block-uniform trip count: barriers match the writers
+      step(t, buf, s0);
+      buf ^= 1;
+      if (t + G >= ntiles) break;
+      step(t + G, buf, s1);
+      buf ^= 1;
+      if (t + 2 * G >= ntiles) break;
+      step(t + 2 * G, buf, s2);
+      buf ^= 1;
     }
-    buf ^= 1;
+  } else {
+    // ================= writers =================
+    const int wt = tid - NL;
+    int buf = 0;
+    for (; t < ntiles; t += G) {
+      __syncthreads();  // tile staged by the loaders
+      compute(buf);
+      __syncthreads();  // feature-major tile complete
+      const GridTile g = grid_tile_fast(t, tpr, Ld);
+      const int64_t rowoff = (g.b * L + g.r) * ld + g.c0;
+#pragma unroll
+      for (int k = 0; k < NW * 32 * 8 / NL; ++k) {
+        const int ci = k * NL + wt;  // chunk index: feature ci / 8, chunk ci % 8
+        const int ff = ci >> 3, c = ci & 7;
+        const V8 v = *reinterpret_cast<const V8*>(&os[ff * 64 + ((c ^ ((ff >> 1) & 7)) << 3)]);
+        stg<V8>(ab + (int64_t)ff * fstride + rowoff + 8 * c, v);
+      }
+      buf ^= 1;
+    }
   }
 }
 
@@ -437,22 +495,23 @@ __global__ __launch_bounds__(256) void tmu_out_kernel(const T* __restrict__ y, c
 }
 
 template <typename T>
-static int tmu_input_phase_t(const void* x, const void* mask, const void* Wp, const void* Wg, const float* sWp,
-                             const float* sWg, const float* Bp, const float* Bg, void* ab, int64_t B, int64_t L,
-                             int64_t C_out, int64_t ld, int transpose, float eps, hipStream_t st) {
-  const int tpr = (int)((ld + 63) / 64);
+static int tmu_input_phase_t(const void* x, const void* mask, const void* Wp, const void* Wg, const float* Bp,
+                             const float* Bg, void* ab, int64_t B, int64_t L, int64_t C_out, int64_t ld, int transpose,
+                             float eps, hipStream_t st) {
+  const int64_t tpr = ld / 64;
   const int64_t ntiles = B * L * tpr;
   if (ntiles == 0) return TOPS_OK;
   const int64_t fstride = B * L * ld;
-  const int64_t grid = ntiles < 4LL * num_cus() ? ntiles : 4LL * num_cus();
+  const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
+  const FastDiv tdiv((uint32_t)tpr), ldiv((uint32_t)L);
   if (C_out == 256) {
     hipLaunchKernelGGL((tmu_in_kernel<T, 128, 8>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)x,
-                       (const int8_t*)mask, (const T*)Wp, (const T*)Wg, sWp, sWg, Bp, Bg, (T*)ab, L, ld, fstride,
-                       transpose, eps, ntiles, tpr);
+                       (const int8_t*)mask, (const T*)Wp, (const T*)Wg, Bp, Bg, (T*)ab, L, ld, fstride, transpose, eps,
+                       (uint32_t)ntiles, tdiv, ldiv);
   } else {
     hipLaunchKernelGGL((tmu_in_kernel<T, 128, 4>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)x,
-                       (const int8_t*)mask, (const T*)Wp, (const T*)Wg, sWp, sWg, Bp, Bg, (T*)ab, L, ld, fstride,
-                       transpose, eps, ntiles, tpr);
+                       (const int8_t*)mask, (const T*)Wp, (const T*)Wg, Bp, Bg, (T*)ab, L, ld, fstride, transpose, eps,
+                       (uint32_t)ntiles, tdiv, ldiv);
   }
   return launched("tops_tmu_input_phase");
 }
@@ -501,13 +560,17 @@ extern "C" int tops_tmu_input_phase(const void* x, const void* mask, const void*
   TOPS_REQUIRE(C == 128, "tops_tmu_input_phase: C must be 128 (got %lld)", (long long)C);
   TOPS_REQUIRE(C_out == 128 || C_out == 256, "tops_tmu_input_phase: C_out must be 128 or 256 (got %lld)",
                (long long)C_out);
-  TOPS_REQUIRE(B >= 0 && L >= 0 && ld >= L, "tops_tmu_input_phase: bad sizes B=%lld L=%lld ld=%lld", (long long)B,
+  TOPS_REQUIRE(B >= 0 && L >= 0 && ld >= L && ld % 64 == 0,
+               "tops_tmu_input_phase: bad sizes B=%lld L=%lld ld=%lld (ld must be a multiple of 64)", (long long)B,
                (long long)L, (long long)ld);
+  TOPS_REQUIRE(B * L * (ld / 64) < (1LL << 31), "tops_tmu_input_phase: too many tokens");
+  (void)sWp;  // the kernel normalises x before the GEMM: the column sums of the folded weights
+  (void)sWg;  // are part of the ABI (reference layout) but not needed
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return tmu_input_phase_t<__bf16>(x, mask, Wp, Wg, sWp, sWg, Bp, Bg, ab, B, L, C_out, ld, transpose, eps, st);
+    return tmu_input_phase_t<__bf16>(x, mask, Wp, Wg, Bp, Bg, ab, B, L, C_out, ld, transpose, eps, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tmu_input_phase_t<_Float16>(x, mask, Wp, Wg, sWp, sWg, Bp, Bg, ab, B, L, C_out, ld, transpose, eps, st);
+    return tmu_input_phase_t<_Float16>(x, mask, Wp, Wg, Bp, Bg, ab, B, L, C_out, ld, transpose, eps, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_input_phase: unsupported dtype code %d", dtype);
 }
 

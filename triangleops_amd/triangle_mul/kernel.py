@@ -38,13 +38,14 @@ def input_phase(
     """LN_in + p_in * sigmoid(g_in) * mask -> ab, channel-major (2C, B, L, ld).
 
     With `transpose=True` each channel's L x L token grid is stored transposed (the layout
-    the incoming einsum consumes).  Columns [L, ld) are zero.  With the defaults the result
-    is the reference's (2C, B, L, L) tensor.
+    the incoming einsum consumes).  `ld` must be a multiple of 64; columns [L, ld) are zero.
+    With the defaults the result is the reference's contiguous (2C, B, L, L) tensor.
     """
     B, L, L2, C = x.shape
     assert L == L2, "x must be (B, L, L, C)"
     C_out = p_in_combined.shape[0]
-    ld = L if ld is None else int(ld)
+    trim = ld is None and L % 64 != 0
+    ld = max(64, (L + 63) // 64 * 64) if ld is None else int(ld)
     code = io_dtype_code(x.dtype)
     _native.check_device(x, p_in_combined, g_in_combined, mask)
     x = x if x.is_contiguous() else x.contiguous()
@@ -75,7 +76,7 @@ def input_phase(
         code,
         _native.stream_of(x),
     )
-    return out
+    return out[..., :L].contiguous() if trim else out
 
 
 def triangle_einsum(ab, L, ld, C, B):
