@@ -290,7 +290,7 @@ def tri_phases(d, pre):
 def tri_work(N):
     return {
         "tri_prep": ("hbm", 2 * N * N * C + 6 * N * N * H * D + 2 * H * N * N),
-        "tri_attention": ("mfma", 4 * N**3 * H * D + 6 * N * N * C * H * D),
+        "tri_attention": ("mfma", 4 * N**3 * H * D),
         "tri_gate_out": ("hbm", 6 * N * N * C),
     }
 

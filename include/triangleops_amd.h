@@ -35,7 +35,7 @@ int tops_abi_version(void);
  *   x      io   (B, L, L, C) contiguous, C == 128
  *   mask   int8 (B, L, L) contiguous (bool storage is accepted: 0/1), or NULL; multiplies the output
  *   Wp, Wg io   (C_out, C) LN-folded weights (out, in);  sWp, sWg, Bp, Bg fp32 (C_out,)
- *   ab     io   out[f * B*L*ld + (b*L + r)*ld + c] for f < C_out, r < L, c < ld (ld >= L)
+ *   ab     io   out[f * B*L*ld + (b*L + r)*ld + c] for f < C_out, r < L, c < ld (ld >= L, ld % 64 == 0)
  *               = sigmoid(G) * P * mask of token (b, i, j) with (i, j) = (r, c), or (c, r) when
  *               transpose != 0; positions c >= L are written as 0.
  * C_out must be 128 or 256.
@@ -48,9 +48,10 @@ int tops_tmu_input_phase(const void* x, const void* mask, const void* Wp, const 
  * triangle_multiplicative_update, triangle einsum (replaces the torch.einsum calls at
  * triangle_mul/module.py:80-84).  For every channel-batch slab s < nslab:
  *   y[s*L*ldy + i*ldy + j] = sum_{k < ld} a[s*L*ld + i*ld + k] * b[s*L*ld + j*ld + k]
- * with a = ab, b = ab + nslab*L*ld, for i, j < L.  ld must be a multiple of 64 and the
- * columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them).  Outgoing feeds
- * the natural token grid, incoming the transposed one (transpose=1 above).
+ * with a = ab, b = ab + nslab*L*ld, for i, j < L.  ld and ldy must be multiples of 64 and
+ * the columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them); columns
+ * [L, ldy) of y receive unspecified finite values.  Outgoing feeds the natural token grid,
+ * incoming the transposed one (transpose=1 above).
  */
 int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
                     void* stream);
@@ -58,7 +59,7 @@ int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t l
 /*
  * triangle_multiplicative_update, output phase.
  * Replaces `output_phase` + its Triton kernel (triangle_mul/kernel.py:282-326).
- *   y      io   channel-major: y[c * B*L*ldy + (b*L + i)*ldy + j], c < C
+ *   y      io   channel-major: y[c * B*L*ldy + (b*L + i)*ldy + j], c < C (ldy >= L, ldy % 64 == 0)
  *   x      io   (B, L, L, C) contiguous
  *   Wp, Wg io   (C_out, C);  sWp, sWg, Bp, Bg fp32 (C_out,)
  *   out    io   (B, L, L, C_out) contiguous = p_out(LN_out(y)) * sigmoid(g_out(LN_in(x)))

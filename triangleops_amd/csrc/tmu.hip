@@ -16,6 +16,9 @@
 
 namespace tops {
 
+// scheduling-group masks of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
+
 // Token tiles: 64 consecutive positions c of one row r of the (B, L, ld) store grid.
 struct GridTile {
   int64_t b, r, c0;
@@ -221,18 +224,26 @@ __global__ __launch_bounds__(NW * 64) void tmu_in_kernel(const T* __restrict__ x
 
 // ---------------------------------------------------------------------------------------------
 // Einsum: per slab s, Y = A . B^T with A, B (L x ld) row-major (k contiguous), ld % 64 == 0.
-// Block tile BM x BN, k-tile 64, 4 waves in a 2 x 2 arrangement, double-buffered LDS with the
-// 16-byte chunks of each 128-byte row XOR-swizzled by (row & 7) so the MFMA operand reads
-// (8 lanes = 8 rows, same chunk) are bank-conflict free.
+// Block tile BM (i) x BN (j), k-tile 64, NW waves in a 2 x (NW / 2) arrangement (two waves per
+// SIMD with NW = 8, so one wave's MFMAs cover the other's LDS reads), double-buffered LDS with
+// one barrier per k-tile: the next k-tile goes from registers into the other buffer while the
+// last k-steps of this one run.  The MFMA computes D = B_tile . A_tile^T (rows j, columns i)
+// with the B-tile rows read in a permuted order, so each lane ends up with 16 consecutive j of
+// one row i of Y and writes them as two 16-byte stores.  LDS rows (128 bytes = 8 chunks of
+// 16 bytes) are XOR-swizzled by (row >> 1) & 7: 16 consecutive rows read at one chunk column
+// hit all 64 banks once.
 // ---------------------------------------------------------------------------------------------
-template <typename T, int BM, int BN>
-__global__ __launch_bounds__(256) void tmu_einsum_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
-                                                        T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
-                                                        int64_t nslab, int tiles_m, int tiles_n) {
+template <typename T, int BM, int BN, int NW>
+__global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+                                                            T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
+                                                            int64_t nslab, int tiles_m, int tiles_n) {
+  constexpr int NT = NW * 64;
   constexpr int BK = 64;
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MI = WM / 32, NI = WN / 32;
-  constexpr int ACH = BM * 8 / 256, BCH = BN * 8 / 256;  // 16-byte chunks per thread per tile
+  constexpr int WM = BM / 2, WN = BN / (NW / 2);
+  constexpr int MI = WM / 32, NJ = WN / 32;
+  constexpr int RPP = NT / 8;                   // rows per load pass (8 threads per 128-byte row)
+  constexpr int ACH = BM / RPP, BCH = BN / RPP;  // 16-byte chunks per thread per k-tile
+  static_assert(ACH * RPP == BM && BCH * RPP == BN, "tile / block shape");
   using V8 = vec<T, 8>;
 
   __shared__ __attribute__((aligned(16))) T As[2][BM * BK];
@@ -254,20 +265,23 @@ __global__ __launch_bounds__(256) void tmu_einsum_kernel(const T* __restrict__ A
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave % 2, wn = wave / 2;
+  // B-tile row read by MFMA row r = col: D slot v of lane half hl is then j = 16 hl + v
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
 
+  auto swz = [](int row, int chunk) { return (chunk ^ ((row >> 1) & 7)) << 3; };
   const int lc = tid & 7, lr = tid >> 3;  // loader: chunk within the 128-byte row, base row
   V8 ra[ACH], rb[BCH];
   auto gload = [&](int kt) {
 #pragma unroll
     for (int j = 0; j < ACH; ++j) {
-      int64_t row = (int64_t)tm * BM + lr + 32 * j;
+      int64_t row = (int64_t)tm * BM + lr + RPP * j;
       row = row < L ? row : L - 1;
       ra[j] = ldg<V8>(Ab + row * ld + kt * BK + lc * 8);
     }
 #pragma unroll
     for (int j = 0; j < BCH; ++j) {
-      int64_t row = (int64_t)tn * BN + lr + 32 * j;
+      int64_t row = (int64_t)tn * BN + lr + RPP * j;
       row = row < L ? row : L - 1;
       rb[j] = ldg<V8>(Bb + row * ld + kt * BK + lc * 8);
     }
@@ -275,222 +289,285 @@ __global__ __launch_bounds__(256) void tmu_einsum_kernel(const T* __restrict__ A
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < ACH; ++j) {
-      const int row = lr + 32 * j;
-      *reinterpret_cast<V8*>(&As[buf][row * BK + ((lc ^ (row & 7)) << 3)]) = ra[j];
+      const int row = lr + RPP * j;
+      *reinterpret_cast<V8*>(&As[buf][row * BK + swz(row, lc)]) = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < BCH; ++j) {
-      const int row = lr + 32 * j;
-      *reinterpret_cast<V8*>(&Bs[buf][row * BK + ((lc ^ (row & 7)) << 3)]) = rb[j];
+      const int row = lr + RPP * j;
+      *reinterpret_cast<V8*>(&Bs[buf][row * BK + swz(row, lc)]) = rb[j];
     }
   };
 
-  f32x16 acc[MI][NI];
+  f32x16 acc[NJ][MI];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+    for (int i = 0; i < MI; ++i) acc[j][i] = f32x16{};
 
+  auto frags = [&](int buf, int ks, V8* fa, V8* fb) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int row = wm * WM + i * 32 + col;
+      fa[i] = *reinterpret_cast<const V8*>(&As[buf][row * BK + swz(row, 2 * ks + hl)]);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int row = wn * WN + j * 32 + prow;
+      fb[j] = *reinterpret_cast<const V8*>(&Bs[buf][row * BK + swz(row, 2 * ks + hl)]);
+    }
+  };
+
+  // Branch-free k-tile body (the last k-tile reloads itself into the unused buffer), scheduled
+  // explicitly: fragments of k-step ks + 1 are read from LDS before the MFMAs of ks issue.
   const int nk = (int)(ld / BK);
   gload(0);
   sstore(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
+    gload(kt + 1 < nk ? kt + 1 : kt);
+    V8 fa[2][MI], fb[2][NJ];
+    frags(buf, 0, fa[0], fb[0]);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      V8 a[MI], b[NI];
+      if (ks + 1 < BK / 16) frags(buf, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int row = wm * WM + i * 32 + col;
-        a[i] = *reinterpret_cast<const V8*>(&As[buf][row * BK + (((2 * ks + hl) ^ (row & 7)) << 3)]);
-      }
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        const int row = wn * WN + j * 32 + col;
-        b[j] = *reinterpret_cast<const V8*>(&Bs[buf][row * BK + (((2 * ks + hl) ^ (row & 7)) << 3)]);
-      }
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = Mma<T>::m32(a[i], b[j], acc[i][j]);
+        for (int i = 0; i < MI; ++i) acc[j][i] = Mma<T>::m32(fb[ks & 1][j], fa[ks & 1][i], acc[j][i]);
+      if (ks == BK / 16 - 2) sstore(buf ^ 1);  // that buffer was last read before the barrier
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+    // schedule: global loads, fragments of step 0, then per step [next fragments | MFMAs]
+    __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, ACH + BCH, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, MI + NJ, 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      if (ks + 1 < BK / 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, MI + NJ, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, MI * NJ, 0);
+      if (ks == BK / 16 - 2) __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, ACH + BCH, 0);
+    }
     __syncthreads();
   }
 
+  // ---- Y[i][j0 .. j0 + 15] per lane: two 16-byte stores (columns [L, ldy) get finite filler) ----
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < MI; ++i) {
+    const int64_t ii = (int64_t)tm * BM + wm * WM + i * 32 + col;
+    if (ii < L) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int64_t cc = (int64_t)tn * BN + wn * WN + j * 32 + col;
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t j0 = (int64_t)tn * BN + wn * WN + j * 32 + 16 * hl;
+        if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
+        V8 o0, o1;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t rr = (int64_t)tm * BM + wm * WM + i * 32 + 8 * (v / 4) + 4 * hl + (v % 4);
-        if (rr < L && cc < L) Yb[rr * ldy + cc] = (T)acc[i][j][v];
+        for (int e = 0; e < 8; ++e) {
+          o0[e] = (T)acc[j][i][e];
+          o1[e] = (T)acc[j][i][8 + e];
+        }
+        stg<V8>(Yb + ii * ldy + j0, o0);
+        stg<V8>(Yb + ii * ldy + j0 + 8, o1);
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Output phase.  4 waves x 32 output features (C_out = 128).  Per 64-token tile the y tile
-// (channel-major in HBM) is transposed into a token-major LDS tile, x is staged beside it,
-// LN statistics for both are computed from LDS, then each wave runs the two K = C GEMMs
-// (P from y, G from x) with its weight rows in registers.
+// Output phase (C = C_out = 128).  8 waves; wave w computes features [32 (w & 3), +32) for the
+// 32 tokens [32 (w >> 2), +32) of a 64-token tile with its Wp / Wg rows in registers (rows
+// permuted so each lane ends up with 16 consecutive features of one token).  Roles as in the
+// input phase: waves 0-3 fetch y and x two tiles ahead, waves 4-7 write the output.
+//   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
+//   registers (4 channels x 8 tokens per thread) into a token-major LDS tile; its LN
+//   statistics are taken from LDS by the waves that use them and applied in the epilogue.
+//   x (token-major) is normalised on the way into LDS.
+//   The gated result goes through a token-major LDS tile: whole 256-byte output rows per store.
 // ---------------------------------------------------------------------------------------------
 template <typename T, int C, int COUT>
-__global__ __launch_bounds__(256) void tmu_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
+__global__ __launch_bounds__(512) void tmu_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
                                                      const T* __restrict__ Wp, const T* __restrict__ Wg,
-                                                     const float* __restrict__ sWp, const float* __restrict__ sWg,
-                                                     const float* __restrict__ Bp, const float* __restrict__ Bg,
-                                                     T* __restrict__ out, int64_t L, int64_t ldy, int64_t cstride,
-                                                     float eps, int64_t ntiles, int tiles_per_row) {
+                                                     const float* __restrict__ sWp, const float* __restrict__ Bp,
+                                                     const float* __restrict__ Bg, T* __restrict__ out, int64_t L,
+                                                     int64_t ldy, int64_t cstride, float eps, uint32_t ntiles,
+                                                     FastDiv tpr, FastDiv Ld) {
   static_assert(C == 128 && COUT == 128, "tmu_out_kernel is specialised for C = C_out = 128");
-  constexpr int ROW = C * 2;
+  constexpr int ROW = C * 2;  // LDS bytes per token row (16 chunks of 16 bytes)
   constexpr int KS = C / 16;
+  constexpr int NL = 256;  // loader threads (waves 0-3); writers are waves 4-7
+  constexpr int PD = 2;    // register stages in flight
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
+  using V2 = vec<T, 2>;
 
-  __shared__ __attribute__((aligned(16))) char ys[64 * ROW];
-  __shared__ __attribute__((aligned(16))) char xs[64 * ROW];
-  __shared__ float st[4][64];  // mean_y, rstd_y, mean_x, rstd_x
+  __shared__ __attribute__((aligned(16))) char ys[2][64 * ROW];  // raw y, token-major
+  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x
+  __shared__ __attribute__((aligned(16))) T os[64 * COUT];       // gated output, token-major
+  __shared__ __attribute__((aligned(16))) float cst[3][COUT];    // sum(Wp_c), Bp, -log2(e) Bg
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
+  const int fset = wave & 3, sub = wave >> 2;
 
+  for (int i = tid; i < COUT; i += 512) {
+    cst[0][i] = sWp[i];
+    cst[1][i] = Bp[i];
+    cst[2][i] = -kLog2e * Bg[i];
+  }
+  // A operand row r = col holds feature 32 fset + prow: D slot v of lane half hl is then
+  // feature 32 fset + 16 hl + v
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
   V8 wp[KS], wg[KS];
   {
-    const int64_t frow = (int64_t)(wave * 32 + col) * C;
+    const int64_t frow = (int64_t)(32 * fset + prow) * C;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       wp[s] = ldg<V8>(Wp + frow + 16 * s + 8 * hl);
       wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
     }
   }
-  float csp[16], cbp[16], csg[16], cbg[16];
+  __syncthreads();  // cst
+
+  auto yswz = [](int t) { return (t ^ (t >> 3)) & 7; };
+  // GEMMs, y statistics and gate of one staged tile -> token-major LDS output tile (all waves)
+  auto compute = [&](int buf) {
+    const int tok = 32 * sub + col;
+    const char* yrow = &ys[buf][tok * ROW];
+    const char* xrow = &xs[buf][tok * ROW];
+    f32x16 accP = {}, accG = {};
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int f = wave * 32 + 8 * (v / 4) + 4 * hl + (v % 4);
-    csp[v] = sWp[f];
-    cbp[v] = Bp[f];
-    csg[v] = sWg[f];
-    cbg[v] = Bg[f];
-  }
-
-  const bool vec_y = (ldy % 8) == 0;
-  // y loader: channels 4*cq .. 4*cq+3, tokens 8*tg .. 8*tg+7 of the tile
-  const int cq = tid & 31, tg = tid >> 5;
-  // x loader / stats: token tid/4, channels [32*(tid%4), +32)
-  const int xt = tid >> 2, xq = tid & 3;
-
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const GridTile g = grid_tile(tile, L, tiles_per_row);
-    const int64_t rowbase = g.b * L + g.r;  // token row (b, i=r); tokens j = c0 + t
-    const int nvalid = (int)((L - g.c0) < 64 ? (L - g.c0) : 64);
-
-    // ---- y tile -> LDS (token-major, swizzled) ----
+    for (int k = 0; k < KS; ++k) {
+      accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
+      accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(xrow + (((2 * k + hl) ^ (tok & 7)) << 4)), accG);
+    }
+    // LN statistics of y for this token: this lane sums chunks [8 hl, 8 hl + 8), its partner the rest
+    float s1 = 0.f, s2 = 0.f;
     {
-      T yv[4][8];
+      const V2 one = {(T)1.f, (T)1.f};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const V8 v = *reinterpret_cast<const V8*>(yrow + (((8 * hl + c) ^ yswz(tok)) << 4));
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+          const V2 pr = {v[k], v[k + 1]};
+          s1 = Mma<T>::dot2(pr, one, s1);
+          s2 = Mma<T>::dot2(pr, pr, s2);
+        }
+      }
+    }
+    const float mean = halves_sum(s1) * (1.0f / C);
+    const float var = fmaxf(halves_sum(s2) * (1.0f / C) - mean * mean, 0.f);
+    const float ra = rsqrtf(var + eps), rb = -mean * ra;
+    const int f0 = 32 * fset + 16 * hl;
+    V8 o[2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 cs = *reinterpret_cast<const f32x4*>(&cst[0][f0 + 4 * q]);
+      const f32x4 cb = *reinterpret_cast<const f32x4*>(&cst[1][f0 + 4 * q]);
+      const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int v = 4 * q + j;
+        const float P = fmaf(accP[v], ra, fmaf(rb, cs[j], cb[j]));
+        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cg[j])));
+        o[v / 8][v % 8] = (T)(P * gate);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = f0 / 8 + h;
+      *reinterpret_cast<V8*>(&os[tok * COUT + ((c ^ (tok & 15)) << 3)]) = o[h];
+    }
+  };
+
+  const uint32_t G = gridDim.x;
+  uint32_t t = blockIdx.x;
+  if (wave < 4) {
+    // ================= loaders =================
+    const int cq = tid >> 3, tg = tid & 7;  // y: channels 4 cq .. 4 cq + 3, tokens 8 tg .. 8 tg + 7
+    struct Stage {
+      V8 y[4], x[4];
+    };
+    // same loads on every call (past the end: the last tile; tokens >= L read token L - 1)
+    auto fetch = [&](uint32_t tt, Stage& sg) {
+      tt = tt < ntiles ? tt : ntiles - 1;
+      const GridTile g = grid_tile_fast(tt, tpr, Ld);
+      const int64_t rowbase = g.b * L + g.r;
       const T* ysrc = y + rowbase * ldy + g.c0 + 8 * tg;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const T* p = ysrc + (int64_t)(4 * cq + r) * cstride;
-        if (vec_y && 8 * tg + 8 <= nvalid) {
-          const V8 v = ldg<V8>(p);
+      for (int r = 0; r < 4; ++r) sg.y[r] = ldg<V8>(ysrc + (int64_t)(4 * cq + r) * cstride);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) yv[r][e] = v[e];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) yv[r][e] = (8 * tg + e < nvalid) ? p[e] : (T)0.f;
-        }
+      for (int k = 0; k < 4; ++k) {
+        const int ci = k * NL + tid;  // token ci / 16, chunk ci % 16
+        int64_t j = g.c0 + (ci >> 4);
+        j = j < L ? j : L - 1;
+        sg.x[k] = ldg<V8>(x + (rowbase * L + j) * C + 8 * (ci & 15));
       }
+    };
+    auto step = [&](uint32_t tt, int buf, Stage& sg) {
+      // x: normalise (16 lanes per token) -> LDS
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int ci = k * NL + tid, xt = ci >> 4, ch = ci & 15;
+        float s1 = 0.f, s2 = 0.f;
+        const V2 one = {(T)1.f, (T)1.f};
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const V2 pr = {sg.x[k][e], sg.x[k][e + 1]};
+          s1 = Mma<T>::dot2(pr, one, s1);
+          s2 = Mma<T>::dot2(pr, pr, s2);
+        }
+        const float mean = group_sum<16>(s1) * (1.0f / C);
+        const float var = fmaxf(group_sum<16>(s2) * (1.0f / C) - mean * mean, 0.f);
+        const float rstd = rsqrtf(var + eps), shift = -mean * rstd;
+        V8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (T)((float)sg.x[k][e] * rstd + shift);
+        *reinterpret_cast<V8*>(&xs[buf][xt * ROW + ((ch ^ (xt & 7)) << 4)]) = h;
+      }
+      // y: 4 x 8 register transpose -> token-major rows (8 bytes = 4 channels per write)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int t = 8 * tg + e;
-        V4 q4 = {yv[0][e], yv[1][e], yv[2][e], yv[3][e]};
-        const int chunk = cq >> 1;
-        *reinterpret_cast<V4*>(&ys[t * ROW + ((chunk ^ (t & 7)) << 4) + ((cq & 1) << 3)]) = q4;
+        const int tk = 8 * tg + e;
+        const V4 q4 = {sg.y[0][e], sg.y[1][e], sg.y[2][e], sg.y[3][e]};
+        *reinterpret_cast<V4*>(&ys[buf][tk * ROW + (((cq >> 1) ^ yswz(tk)) << 4) + ((cq & 1) << 3)]) = q4;
       }
+      __syncthreads();
+      fetch(tt + PD * G, sg);  // refill this stage
+      compute(buf);
+      __syncthreads();
+    };
+    int buf = 0;
+    Stage s0, s1;
+    fetch(t, s0);
+    fetch(t + G, s1);
+    for (; t < ntiles; t += 2 * G) {  // block-uniform trip count: barriers match the writers
+      step(t, buf, s0);
+      buf ^= 1;
+      if (t + G >= ntiles) break;
+      step(t + G, buf, s1);
+      buf ^= 1;
     }
-    // ---- x tile -> LDS ----
-    {
-      const int64_t tok = rowbase * L + g.c0 + xt;
+  } else {
+    // ================= writers =================
+    const int wt = tid - NL;
+    int buf = 0;
+    for (; t < ntiles; t += G) {
+      __syncthreads();  // tile staged by the loaders
+      compute(buf);
+      __syncthreads();  // output tile complete
+      const GridTile g = grid_tile_fast(t, tpr, Ld);
+      const int64_t tok0 = (g.b * L + g.r) * L + g.c0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        V8 v = V8{};
-        if (xt < nvalid) v = ldg<V8>(x + tok * C + 32 * xq + 8 * e);
-        const int chunk = 4 * xq + e;
-        *reinterpret_cast<V8*>(&xs[xt * ROW + ((chunk ^ (xt & 7)) << 4)]) = v;
-      }
-    }
-    __syncthreads();
-    // ---- LN statistics (token xt, 4 threads per token) ----
-    {
-      float vy[32], vx[32];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int chunk = 4 * xq + e;
-        const V8 a = *reinterpret_cast<const V8*>(&ys[xt * ROW + ((chunk ^ (xt & 7)) << 4)]);
-        const V8 b = *reinterpret_cast<const V8*>(&xs[xt * ROW + ((chunk ^ (xt & 7)) << 4)]);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          vy[8 * e + k] = (float)a[k];
-          vx[8 * e + k] = (float)b[k];
+      for (int k = 0; k < 64 * COUT / 8 / NL; ++k) {
+        const int ci = k * NL + wt;  // token ci / 16, chunk ci % 16
+        const int tk = ci >> 4, c = ci & 15;
+        if (g.c0 + tk < L) {
+          const V8 v = *reinterpret_cast<const V8*>(&os[tk * COUT + ((c ^ (tk & 15)) << 3)]);
+          stg<V8>(out + (tok0 + tk) * COUT + 8 * c, v);
         }
       }
-      float sy = 0.f, sx = 0.f;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        sy += vy[k];
-        sx += vx[k];
-      }
-      const float my = group_sum<4>(sy) * (1.0f / C), mx = group_sum<4>(sx) * (1.0f / C);
-      float qy = 0.f, qx = 0.f;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) {
-        qy += (vy[k] - my) * (vy[k] - my);
-        qx += (vx[k] - mx) * (vx[k] - mx);
-      }
-      qy = group_sum<4>(qy);
-      qx = group_sum<4>(qx);
-      if (xq == 0) {
-        st[0][xt] = my;
-        st[1][xt] = rsqrtf(qy * (1.0f / C) + eps);
-        st[2][xt] = mx;
-        st[3][xt] = rsqrtf(qx * (1.0f / C) + eps);
-      }
+      buf ^= 1;
     }
-    __syncthreads();
-    // ---- projections + gate ----
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int t = sub * 32 + col;
-      f32x16 accP = {}, accG = {};
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int off = t * ROW + (((2 * k + hl) ^ (t & 7)) << 4);
-        accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(&ys[off]), accP);
-        accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(&xs[off]), accG);
-      }
-      if (t < nvalid) {
-        const float my = st[0][t], ry = st[1][t], mx = st[2][t], rx = st[3][t];
-        T* dst = out + (rowbase * L + g.c0 + t) * COUT + wave * 32 + 4 * hl;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          V4 o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int v = 4 * q + e;
-            const float P = ry * (accP[v] - my * csp[v]) + cbp[v];
-            const float G = rx * (accG[v] - mx * csg[v]) + cbg[v];
-            o[e] = (T)(P * sigmoid(G));
-          }
-          stg<V4>(dst + 8 * q, o);
-        }
-      }
-    }
-    __syncthreads();
   }
 }
 
@@ -523,28 +600,30 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
   if (L > 384) {
     const int t = (int)((L + 255) / 256);
     const int64_t grid = nslab * t * t;
-    hipLaunchKernelGGL((tmu_einsum_kernel<T, 256, 256>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
-                       ldy, nslab, t, t);
+    hipLaunchKernelGGL((tmu_einsum_kernel<T, 256, 256, 8>), dim3((unsigned)grid), dim3(512), 0, st, A, Bm, (T*)y, L,
+                       ld, ldy, nslab, t, t);
   } else {
     const int t = (int)((L + 127) / 128);
     const int64_t grid = nslab * t * t;
-    hipLaunchKernelGGL((tmu_einsum_kernel<T, 128, 128>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
-                       ldy, nslab, t, t);
+    hipLaunchKernelGGL((tmu_einsum_kernel<T, 128, 128, 4>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L,
+                       ld, ldy, nslab, t, t);
   }
   return launched("tops_tmu_einsum");
 }
 
 template <typename T>
 static int tmu_output_phase_t(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
-                              const float* sWg, const float* Bp, const float* Bg, void* out, int64_t B, int64_t L,
-                              int64_t ldy, float eps, hipStream_t st) {
-  const int tpr = (int)((L + 63) / 64);
+                              const float* Bp, const float* Bg, void* out, int64_t B, int64_t L, int64_t ldy,
+                              float eps, hipStream_t st) {
+  const int64_t tpr = (L + 63) / 64;
   const int64_t ntiles = B * L * tpr;
   if (ntiles == 0) return TOPS_OK;
   const int64_t cstride = B * L * ldy;
-  const int64_t grid = ntiles < 8LL * num_cus() ? ntiles : 8LL * num_cus();
-  hipLaunchKernelGGL((tmu_out_kernel<T, 128, 128>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)y, (const T*)x,
-                     (const T*)Wp, (const T*)Wg, sWp, sWg, Bp, Bg, (T*)out, L, ldy, cstride, eps, ntiles, tpr);
+  const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
+  const FastDiv tdiv((uint32_t)tpr), ldiv((uint32_t)L);
+  hipLaunchKernelGGL((tmu_out_kernel<T, 128, 128>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)y, (const T*)x,
+                     (const T*)Wp, (const T*)Wg, sWp, Bp, Bg, (T*)out, L, ldy, cstride, eps, (uint32_t)ntiles, tdiv,
+                     ldiv);
   return launched("tops_tmu_output_phase");
 }
 
@@ -577,8 +656,8 @@ extern "C" int tops_tmu_input_phase(const void* x, const void* mask, const void*
 extern "C" int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
                                void* stream) {
   TOPS_REQUIRE(ab && y, "tops_tmu_einsum: null pointer argument");
-  TOPS_REQUIRE(ld % 64 == 0 && ld >= L && ldy >= L && L >= 0 && nslab >= 0,
-               "tops_tmu_einsum: bad sizes nslab=%lld L=%lld ld=%lld ldy=%lld (ld must be a multiple of 64)",
+  TOPS_REQUIRE(ld % 64 == 0 && ldy % 64 == 0 && ld >= L && ldy >= L && L >= 0 && nslab >= 0,
+               "tops_tmu_einsum: bad sizes nslab=%lld L=%lld ld=%lld ldy=%lld (ld, ldy must be multiples of 64)",
                (long long)nslab, (long long)L, (long long)ld, (long long)ldy);
   if (L == 0 || nslab == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
@@ -594,11 +673,15 @@ extern "C" int tops_tmu_output_phase(const void* y, const void* x, const void* W
   TOPS_REQUIRE(y && x && Wp && Wg && sWp && sWg && Bp && Bg && out, "tops_tmu_output_phase: null pointer argument");
   TOPS_REQUIRE(C == 128 && C_out == 128, "tops_tmu_output_phase: C and C_out must be 128 (got %lld, %lld)",
                (long long)C, (long long)C_out);
-  TOPS_REQUIRE(B >= 0 && L >= 0 && ldy >= L, "tops_tmu_output_phase: bad sizes");
+  TOPS_REQUIRE(B >= 0 && L >= 0 && ldy >= L && ldy % 64 == 0,
+               "tops_tmu_output_phase: bad sizes B=%lld L=%lld ldy=%lld (ldy must be a multiple of 64)",
+               (long long)B, (long long)L, (long long)ldy);
+  TOPS_REQUIRE(B * L * ((L + 63) / 64) < (1LL << 31), "tops_tmu_output_phase: too many tokens");
+  (void)sWg;  // x is normalised before its GEMM: the column sums of Wg_c are not needed
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return tmu_output_phase_t<__bf16>(y, x, Wp, Wg, sWp, sWg, Bp, Bg, out, B, L, ldy, eps, st);
+    return tmu_output_phase_t<__bf16>(y, x, Wp, Wg, sWp, Bp, Bg, out, B, L, ldy, eps, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tmu_output_phase_t<_Float16>(y, x, Wp, Wg, sWp, sWg, Bp, Bg, out, B, L, ldy, eps, st);
+    return tmu_output_phase_t<_Float16>(y, x, Wp, Wg, sWp, Bp, Bg, out, B, L, ldy, eps, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_output_phase: unsupported dtype code %d", dtype);
 }

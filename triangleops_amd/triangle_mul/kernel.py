@@ -113,17 +113,24 @@ def output_phase(
     *,
     ldy=None,
 ):
-    """sigmoid(g_out(LN_in x)) * p_out(LN_out y) -> (B, L, L, C_out); y channel-major (C, B, L, ldy)."""
+    """sigmoid(g_out(LN_in x)) * p_out(LN_out y) -> (B, L, L, C_out); y channel-major (C, B, L, ldy).
+
+    The kernel reads y rows padded to a multiple of 64 (`ldy`); with the default (y as the
+    reference's (C, B, L, L) tensor) a padded copy is made when L is not a multiple of 64.
+    """
     B, L, _, C = x.shape
     C_out = p_out_combined.shape[0]
     code = io_dtype_code(x.dtype)
     _native.check_device(x, y_t, p_out_combined, g_out_combined)
     x = x if x.is_contiguous() else x.contiguous()
-    ldy = L if ldy is None else int(ldy)
-    if ldy == L:
-        y_t = y_t.reshape(C, B * L * L)
+    if ldy is None:
+        ldy = max(64, (L + 63) // 64 * 64)
+        y_t = y_t.reshape(C, B, L, L)
+        if ldy != L:
+            y_t = torch.nn.functional.pad(y_t, (0, ldy - L))
         y_t = y_t if y_t.is_contiguous() else y_t.contiguous()
     else:
+        ldy = int(ldy)
         assert y_t.is_contiguous() and y_t.numel() == C * B * L * ldy
     if y_t.dtype != x.dtype:
         y_t = y_t.to(x.dtype)
