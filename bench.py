@@ -415,6 +415,45 @@ def sweep(path, sizes, dev):
     return rows
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tmu_L1024_hbm_traffic.md")
+
+
+def measured_traffic(kernel, L):
+    """HBM bytes per launch of `kernel` at the default workload, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known size); None otherwise."""
+    if L != 1024 or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == kernel:
+            try:
+                return int(cells[4])
+            except ValueError:
+                return None
+    return None
+
+
+def traffic_run(L):
+    """Workload for the HBM-traffic counter runs (no timing): a 256 MiB bf16 negation whose bytes
+    are known (calibration), then two default steps (outgoing + incoming)."""
+    dev = torch.device("cuda:0")
+    src = torch.randn(128 * 1024 * 1024, device=dev).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    x_c, m_c, w_c = tmu_inputs(L)
+    x, m = x_c.to(dev), m_c.to(dev)
+    w = {k: v.to(dev) for k, v in w_c.items()}
+    pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+    for _ in range(2):
+        for d in ("outgoing", "incoming"):
+            tops.triangle_mul.forward(x, pre, direction=d, mask=m)
+    torch.cuda.synchronize()
+    print("traffic run done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -425,6 +464,8 @@ def main():
     ap.add_argument("--sweep-sizes", default="128,256,512,1024,2048")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-path reference timing")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="only run the workload of the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -436,6 +477,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     L = args.size
+    if args.traffic_run:
+        traffic_run(L)
+        return
 
     x_c, m_c, w_c = tmu_inputs(L)
     x, m = x_c.to(dev), m_c.to(dev)
@@ -469,7 +513,7 @@ def main():
     dominant = max(names, key=lambda n: ph[n])
     kd = kernels[dominant]
     roofline = {"kernel": dominant, "bound": kd["bound"], "achieved": kd["achieved"], "peak": kd["peak"],
-                "unit": kd["unit"], "frac": kd["frac"], "traffic": None}
+                "unit": kd["unit"], "frac": kd["frac"], "traffic": measured_traffic(dominant, L)}
 
     torch_ms = {} if args.no_torch else {d: time_ms(lambda: torch_tmu(x, d, m, **w), 5, 2)
                                           for d in ("outgoing", "incoming")}
