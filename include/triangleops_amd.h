@@ -109,8 +109,9 @@ int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const v
  * `fused_gate_kernel` (triangle_attn/kernel.py:387-470) and the apb epilogue
  * (attn_pair_bias/module.py:69-70):
  *   out[t] = ((o[t] * sigmoid(g[t] Wg^T + bg)) -> io) Wo^T + bo,  g = LN(gin) if apply_ln else gin
- *   o      io   token (m1, m2) at o[m1*so0 + m2*so1 + c], c < C
- *   gin    io   token (m1, m2) at gin[m1*sg0 + m2*sg1 + c];  w_ln, b_ln io (C,), ln_eps
+ *   o      io   token (m1, m2) at o[m1*so0 + m2*so1 + c], c < C (strides multiples of 8,
+ *               16-byte aligned base)
+ *   gin    io   token (m1, m2) at gin[m1*sg0 + m2*sg1 + c], same constraints;  w_ln, b_ln io (C,)
  *   Wg, Wo io   (C, C) in (out, in) layout;  bg, bo io (C,) or NULL
  *   out    io   (M1*M2, C) contiguous.  C == 128.
  */

@@ -7,137 +7,187 @@
 // strides) and attn_pair_bias/module.py:69-70 (gate on raw X with biases, then Wo).
 // Both weights are read in their (out, in) nn.Linear layout: no per-call transposes.
 //
-// 64-token tiles, 4 waves; wave w owns features [32w, 32w + 32) of both GEMMs with its weight
-// rows in registers.  The gate input and the gated activations go through token-major LDS
-// tiles (XOR-swizzled 16-byte chunks) so each GEMM reads all 128 channels of a token as k.
+// 64-token tiles, 8 waves.  Waves 0-3 fetch the o and gate-input tiles two tiles ahead (two
+// register stages; 16 lanes per 256-byte token row) and stage them in LDS, normalising the
+// gate input on the way; waves 4-7 write the results, so no wave has loads and stores in flight
+// together and each stage is waited for only when consumed.  All waves compute: wave w owns
+// features [32 (w & 3), +32) of both GEMMs for tokens [32 (w >> 2), +32), weight rows in
+// registers (permuted so each lane ends up with 16 consecutive features of one token).  The
+// gated activations overwrite the o tile in LDS and are the second GEMM's operand; the output
+// goes through a token-major LDS tile so each store instruction writes whole 256-byte rows.
 #include "capi.hpp"
 #include "common.hpp"
 
 namespace tops {
 
-template <typename T>
-__global__ __launch_bounds__(256) void gate_out_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
+template <typename T, bool LN>
+__global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
                                                       const T* __restrict__ gin, int64_t sg0, int64_t sg1,
                                                       const T* __restrict__ w_ln, const T* __restrict__ b_ln,
-                                                      float ln_eps, int apply_ln, const T* __restrict__ Wg,
+                                                      float ln_eps, const T* __restrict__ Wg,
                                                       const T* __restrict__ bg, const T* __restrict__ Wo,
-                                                      const T* __restrict__ bo, T* __restrict__ out, int64_t M2,
-                                                      int64_t M, int64_t ntiles) {
+                                                      const T* __restrict__ bo, T* __restrict__ out, FastDiv M2,
+                                                      uint32_t M, uint32_t ntiles) {
   constexpr int C = 128, ROW = C * 2, KS = C / 16;
+  constexpr int NL = 256;  // loader threads (waves 0-3); writers are waves 4-7
+  constexpr int PD = 2;    // register stages in flight
   using V8 = vec<T, 8>;
-  using V4 = vec<T, 4>;
-  __shared__ __attribute__((aligned(16))) char gs[64 * ROW];
-  __shared__ __attribute__((aligned(16))) char ts[64 * ROW];
+  using V2 = vec<T, 2>;
+
+  // one staging buffer suffices: the next tile is staged only after the third barrier, when
+  // every wave has finished reading this one
+  __shared__ __attribute__((aligned(16))) char gs[64 * ROW];   // gate input (normalised)
+  __shared__ __attribute__((aligned(16))) char ots[64 * ROW];  // o, then the gated values
+  __shared__ __attribute__((aligned(16))) T os[64 * C];          // output tile, token-major
+  __shared__ __attribute__((aligned(16))) float cst[2][C];       // -log2(e) bg, bo
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
+  const int fset = wave & 3, sub = wave >> 2;
 
+  for (int i = tid; i < C; i += 512) {
+    cst[0][i] = bg ? -kLog2e * (float)bg[i] : 0.f;
+    cst[1][i] = bo ? (float)bo[i] : 0.f;
+  }
+  // A operand row r = col holds feature 32 fset + prow: D slot v of lane half hl is then
+  // feature 32 fset + 16 hl + v
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
   V8 wg[KS], wo[KS];
   {
-    const int64_t frow = (int64_t)(wave * 32 + col) * C;
+    const int64_t frow = (int64_t)(32 * fset + prow) * C;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
       wo[s] = ldg<V8>(Wo + frow + 16 * s + 8 * hl);
     }
   }
-  float cbg[16], cbo[16];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int f = wave * 32 + 8 * (v / 4) + 4 * hl + (v % 4);
-    cbg[v] = bg ? (float)bg[f] : 0.f;
-    cbo[v] = bo ? (float)bo[f] : 0.f;
-  }
-  const int ltok = tid >> 2, part = tid & 3;  // gate-input loader: 4 threads per token
+  __syncthreads();  // cst
 
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t t0 = tile * 64;
-    // ---- gate input tile (LN applied if asked) -> LDS ----
-    {
-      const int64_t m = t0 + ltok;
-      float v[32];
-      if (m < M) {
-        const T* src = gin + (m / M2) * sg0 + (m % M2) * sg1 + 32 * part;
+  auto swz = [](int t, int chunk) { return (chunk ^ (t & 15)) << 4; };
+  const int f0 = 32 * fset + 16 * hl;
+  // GEMM 1, sigmoid gate, o * gate -> in place over the o tile (all waves)
+  auto compute1 = [&]() {
+    const int tok = 32 * sub + col;
+    const char* grow = &gs[tok * ROW];
+    char* orow = &ots[tok * ROW];
+    f32x16 acc = {};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const V8 a = ldg<V8>(src + 8 * e);
+    for (int k = 0; k < KS; ++k)
+      acc = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(grow + swz(tok, 2 * k + hl)), acc);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[8 * e + j] = (float)a[j];
-        }
-      } else {
+    for (int h = 0; h < 2; ++h) {
+      const int c = f0 / 8 + h;
+      V8* p = reinterpret_cast<V8*>(orow + swz(tok, c));
+      const V8 ov = *p;
+      V8 r;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = 0.f;
+      for (int e = 0; e < 8; ++e) {
+        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(acc[8 * h + e], -kLog2e, cst[0][f0 + 8 * h + e])));
+        r[e] = (T)((float)ov[e] * gate);
       }
-      if (apply_ln) {
-        float s = 0.f;
+      *p = r;
+    }
+  };
+  // GEMM 2 on the gated tile -> token-major output tile (all waves)
+  auto compute2 = [&]() {
+    const int tok = 32 * sub + col;
+    const char* trow = &ots[tok * ROW];
+    f32x16 acc = {};
 #pragma unroll
-        for (int e = 0; e < 32; ++e) s += v[e];
-        const float mean = group_sum<4>(s) * (1.0f / C);
-        float q = 0.f;
+    for (int k = 0; k < KS; ++k)
+      acc = Mma<T>::m32(wo[k], *reinterpret_cast<const V8*>(trow + swz(tok, 2 * k + hl)), acc);
 #pragma unroll
-        for (int e = 0; e < 32; ++e) q += (v[e] - mean) * (v[e] - mean);
-        const float rstd = rsqrtf(group_sum<4>(q) * (1.0f / C) + ln_eps);
+    for (int h = 0; h < 2; ++h) {
+      V8 r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const V8 w8 = ldg<V8>(w_ln + 32 * part + 8 * e);
-          const V8 b8 = b_ln ? ldg<V8>(b_ln + 32 * part + 8 * e) : V8{};
+      for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[1][f0 + 8 * h + e]);
+      const int c = f0 / 8 + h;
+      *reinterpret_cast<V8*>(&os[tok * C + ((c ^ (tok & 15)) << 3)]) = r;
+    }
+  };
+
+  const uint32_t G = gridDim.x;
+  uint32_t t = blockIdx.x;
+  if (wave < 4) {
+    // ================= loaders =================
+    const int ch = tid & 15;  // this thread's 16-byte chunk of every token row it loads
+    V8 lnw = {}, lnb = {};
+    if constexpr (LN) {
+      lnw = ldg<V8>(w_ln + 8 * ch);
+      if (b_ln) lnb = ldg<V8>(b_ln + 8 * ch);
+    }
+    struct Stage {
+      V8 o[4], g[4];
+    };
+    // same loads on every call (past the end: the last tile; tokens >= M read token M - 1)
+    auto fetch = [&](uint32_t tt, Stage& sg) {
+      tt = tt < ntiles ? tt : ntiles - 1;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[8 * e + j] = (v[8 * e + j] - mean) * rstd * (float)w8[j] + (float)b8[j];
-        }
+      for (int k = 0; k < 4; ++k) {
+        uint32_t m = tt * 64 + ((k * NL + tid) >> 4);
+        m = m < M ? m : M - 1;
+        const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
+        sg.o[k] = ldg<V8>(o + m1 * so0 + m2 * so1 + 8 * ch);
+        sg.g[k] = ldg<V8>(gin + m1 * sg0 + m2 * sg1 + 8 * ch);
       }
+    };
+    auto step = [&](uint32_t tt, Stage& sg) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        V8 r;
+      for (int k = 0; k < 4; ++k) {
+        const int tk = (k * NL + tid) >> 4;
+        V8 g = sg.g[k];
+        if constexpr (LN) {  // LayerNorm over the token's 16 lanes (sum and sum of squares in fp32)
+          float s1 = 0.f, s2 = 0.f;
+          const V2 one = {(T)1.f, (T)1.f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = (T)v[8 * e + j];
-        const int chunk = 4 * part + e;
-        *reinterpret_cast<V8*>(&gs[ltok * ROW + ((chunk ^ (ltok & 7)) << 4)]) = r;
+          for (int e = 0; e < 8; e += 2) {
+            const V2 pr = {g[e], g[e + 1]};
+            s1 = Mma<T>::dot2(pr, one, s1);
+            s2 = Mma<T>::dot2(pr, pr, s2);
+          }
+          const float mean = group_sum<16>(s1) * (1.0f / C);
+          const float var = fmaxf(group_sum<16>(s2) * (1.0f / C) - mean * mean, 0.f);
+          const float rstd = rsqrtf(var + ln_eps);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) g[e] = (T)(((float)g[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e]);
+        }
+        *reinterpret_cast<V8*>(&gs[tk * ROW + swz(tk, ch)]) = g;
+        *reinterpret_cast<V8*>(&ots[tk * ROW + swz(tk, ch)]) = sg.o[k];
+      }
+      __syncthreads();
+      fetch(tt + PD * G, sg);  // refill this stage
+      __builtin_amdgcn_sched_barrier(0);
+      compute1();
+      __syncthreads();
+      compute2();
+      __syncthreads();
+    };
+    Stage s0, s1;
+    fetch(t, s0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
+    fetch(t + G, s1);
+    for (; t < ntiles; t += 2 * G) {  // block-uniform trip count: barriers match the writers
+      step(t, s0);
+      if (t + G >= ntiles) break;
+      step(t + G, s1);
+    }
+  } else {
+    // ================= writers =================
+    const int wt = tid - NL;
+    for (; t < ntiles; t += G) {
+      __syncthreads();  // tile staged by the loaders
+      compute1();
+      __syncthreads();  // gated tile complete
+      compute2();
+      __syncthreads();  // output tile complete
+#pragma unroll
+      for (int k = 0; k < 64 * C / 8 / NL; ++k) {
+        const int ci = k * NL + wt;  // token ci / 16, chunk ci % 16
+        const int tk = ci >> 4, c = ci & 15;
+        const uint32_t m = t * 64 + tk;
+        if (m < M) stg<V8>(out + (int64_t)m * C + 8 * c, *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ (tk & 15)) << 3)]));
       }
     }
-    __syncthreads();
-    // ---- gate GEMM, sigmoid, multiply by o -> LDS ----
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int t = sub * 32 + col;
-      int64_t tok = t0 + t;
-      tok = tok < M ? tok : M - 1;
-      f32x16 acc = {};
-#pragma unroll
-      for (int k = 0; k < KS; ++k)
-        acc = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(&gs[t * ROW + (((2 * k + hl) ^ (t & 7)) << 4)]), acc);
-      const T* orow = o + (tok / M2) * so0 + (tok % M2) * so1 + wave * 32 + 4 * hl;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const V4 ov = ldg<V4>(orow + 8 * g);
-        V4 r;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (T)((float)ov[e] * sigmoid(acc[4 * g + e] + cbg[4 * g + e]));
-        const int chunk = wave * 4 + g;  // features [8 chunk, 8 chunk + 8)
-        *reinterpret_cast<V4*>(&ts[t * ROW + ((chunk ^ (t & 7)) << 4) + 8 * hl]) = r;
-      }
-    }
-    __syncthreads();
-    // ---- output GEMM ----
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int t = sub * 32 + col;
-      f32x16 acc = {};
-#pragma unroll
-      for (int k = 0; k < KS; ++k)
-        acc = Mma<T>::m32(wo[k], *reinterpret_cast<const V8*>(&ts[t * ROW + (((2 * k + hl) ^ (t & 7)) << 4)]), acc);
-      const int64_t tok = t0 + t;
-      if (tok < M) {
-        T* dst = out + tok * C + wave * 32 + 4 * hl;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          V4 r;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) r[e] = (T)(acc[4 * g + e] + cbo[4 * g + e]);
-          stg<V4>(dst + 8 * g, r);
-        }
-      }
-    }
-    __syncthreads();
   }
 }
 
@@ -148,10 +198,11 @@ static int gate_out_t(const void* o, int64_t so0, int64_t so1, const void* gin, 
   const int64_t M = M1 * M2;
   const int64_t ntiles = (M + 63) / 64;
   if (ntiles == 0) return TOPS_OK;
-  const int64_t grid = ntiles < 8LL * num_cus() ? ntiles : 8LL * num_cus();
-  hipLaunchKernelGGL((gate_out_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)o, so0, so1,
-                     (const T*)gin, sg0, sg1, (const T*)w_ln, (const T*)b_ln, ln_eps, apply_ln, (const T*)Wg,
-                     (const T*)bg, (const T*)Wo, (const T*)bo, (T*)out, M2, M, ntiles);
+  const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
+  auto kern = apply_ln ? gate_out_kernel<T, true> : gate_out_kernel<T, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), 0, st, (const T*)o, so0, so1, (const T*)gin, sg0, sg1,
+                     (const T*)w_ln, (const T*)b_ln, ln_eps, (const T*)Wg, (const T*)bg, (const T*)Wo,
+                     (const T*)bo, (T*)out, FastDiv((uint32_t)M2), (uint32_t)M, (uint32_t)ntiles);
   return launched("tops_gate_out");
 }
 
@@ -166,9 +217,11 @@ extern "C" int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void
   TOPS_REQUIRE(o && gin && Wg && Wo && out, "tops_gate_out: null pointer argument");
   TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out: w_ln is required when apply_ln != 0");
   TOPS_REQUIRE(C == 128, "tops_gate_out: C must be 128 (got %lld)", (long long)C);
-  TOPS_REQUIRE(M1 >= 0 && M2 >= 0, "tops_gate_out: bad sizes");
-  TOPS_REQUIRE(so0 % 4 == 0 && so1 % 4 == 0, "tops_gate_out: o token strides must be multiples of 4");
-  TOPS_REQUIRE(sg0 % 8 == 0 && sg1 % 8 == 0, "tops_gate_out: gate-input token strides must be multiples of 8");
+  TOPS_REQUIRE(M1 >= 0 && M2 >= 0 && M1 * M2 < (1LL << 31), "tops_gate_out: bad sizes");
+  TOPS_REQUIRE(so0 % 8 == 0 && so1 % 8 == 0 && sg0 % 8 == 0 && sg1 % 8 == 0,
+               "tops_gate_out: token strides must be multiples of 8 elements");
+  TOPS_REQUIRE((uintptr_t)o % 16 == 0 && (uintptr_t)gin % 16 == 0 && (uintptr_t)out % 16 == 0,
+               "tops_gate_out: o, gin and out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
     return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1, M2,

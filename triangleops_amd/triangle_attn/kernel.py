@@ -159,10 +159,10 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
     """
     N1, N2, C = o.shape
     _native.check_device(o, gin, W_g, W_o)
-    if o.stride(2) != 1 or o.stride(0) % 4 or o.stride(1) % 4:
+    if o.stride(2) != 1 or o.stride(0) % 8 or o.stride(1) % 8 or o.data_ptr() % 16:
         o = o.contiguous()
     gin = gin.reshape(N1, N2, C) if gin.dim() != 3 else gin
-    if gin.stride(2) != 1 or gin.stride(0) % 8 or gin.stride(1) % 8:
+    if gin.stride(2) != 1 or gin.stride(0) % 8 or gin.stride(1) % 8 or gin.data_ptr() % 16:
         gin = gin.contiguous()
     w_ln = b_ln = None
     eps = 1e-5
