@@ -166,11 +166,16 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
     fetch(t, s0);
     __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
     fetch(t + G, s1);
-    for (; t < ntiles; t += 2 * G) {  // block-uniform trip count: barriers match the writers
+    __builtin_amdgcn_sched_barrier(0);
+    // block-uniform trip count (barriers match the writers'); the odd last tile runs after the
+    // loop so that the back edge is the only way to the loop head (a break out of the unrolled
+    // body would merge into the latch and make the compiler wait for every load)
+    uint32_t n = t < ntiles ? (ntiles - t + G - 1) / G : 0;
+    for (; n >= 2; n -= 2, t += 2 * G) {
       step(t, s0);
-      if (t + G >= ntiles) break;
       step(t + G, s1);
     }
+    if (n > 0) step(t, s0);
   } else {
     // ================= writers =================
     const int wt = tid - NL;

@@ -188,18 +188,23 @@ __global__ __launch_bounds__(NW * 64) void tmu_in_kernel(const T* __restrict__ x
     int buf = 0;
     Stage s0, s1, s2;
     fetch(t, s0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
     fetch(t + G, s1);
+    __builtin_amdgcn_sched_barrier(0);
     fetch(t + 2 * G, s2);
-    for (; t < ntiles; t += 3 * G) {  // block-uniform trip count: barriers match the writers
+    __builtin_amdgcn_sched_barrier(0);
+    // block-uniform trip count (barriers match the writers'); the remainder runs after the
+    // loop so that its back edge is the only way to the loop head (a break out of the
+    // unrolled body would merge into the latch and make the compiler wait for every load)
+    uint32_t n = t < ntiles ? (ntiles - t + G - 1) / G : 0;
+    for (; n >= 3; n -= 3, t += 3 * G) {
       step(t, buf, s0);
-      buf ^= 1;
-      if (t + G >= ntiles) break;
-      step(t + G, buf, s1);
-      buf ^= 1;
-      if (t + 2 * G >= ntiles) break;
+      step(t + G, buf ^ 1, s1);
       step(t + 2 * G, buf, s2);
       buf ^= 1;
     }
+    if (n > 0) step(t, buf, s0);
+    if (n > 1) step(t + G, buf ^ 1, s1);
   } else {
     // ================= writers =================
     const int wt = tid - NL;

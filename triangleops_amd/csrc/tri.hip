@@ -34,134 +34,211 @@ namespace tops {
 constexpr int kKVBlock = 4096;  // elements per (row, head, 64-key) KV block: 64x32 K + 32x64 V^T
 
 // ---------------------------------------------------------------------------------------------
-// Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 256 threads: the LN mapping is
-// 4 threads per position (32 channels each); the GEMM mapping is wave w = head w with its
-// WQ^T / WK^T / WV^T rows in registers and the normalized tile read from LDS as MFMA operands.
-// Positions >= N are processed from zeros (finite values, masked by the attention kernel).
+// Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 8 waves in two roles:
+//   waves 0-3 (loaders) fetch x four tiles ahead (16 lanes per 256-byte token row; positions
+//   >= N reload position N - 1, so every fetch issues the same loads), take the LayerNorm and
+//   the 4 heads' pair bias in fp32, and stage the normalised tile in LDS (double-buffered);
+//   waves 4-7 (head w - 4) run that head's Q / K / V GEMM over the 64 positions with its WQ /
+//   WK / WV rows in registers, stage the results in a private LDS block in the HBM image of
+//   the tile (XOR-swizzled 16-byte chunks) and store it back, 1 KB per store instruction.
+// No wave has loads and stores in flight together, so each register stage is waited for only
+// when it is consumed, and the loaders' LayerNorm of tile n + 1 overlaps the writers' GEMM of
+// tile n: one barrier per tile.  Positions >= N are computed from zeros (finite values, masked
+// by the attention kernel).
 // ---------------------------------------------------------------------------------------------
-template <typename T, int H>
-__global__ __launch_bounds__(256, 1) void tri_prep_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
-                                                         const T* __restrict__ w_ln, const T* __restrict__ b_ln,
-                                                         int apply_ln, const T* __restrict__ wqkv,
-                                                         const T* __restrict__ WZ, const float* __restrict__ BZ,
-                                                         T* __restrict__ Qp, T* __restrict__ KV, T* __restrict__ bias,
-                                                         int64_t N, int64_t ldn, float eps, float qscale,
-                                                         float bias_scale, int64_t ntiles) {
-  constexpr int C = 128, D = 32, ROW = C * 2;
-  static_assert(H == 4, "one wave per head");
+template <typename T, bool LN>
+__global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
+                                                      const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                      const T* __restrict__ wqkv, const T* __restrict__ WZ,
+                                                      const float* __restrict__ BZ, T* __restrict__ Qp,
+                                                      T* __restrict__ KV, T* __restrict__ bias, uint32_t N,
+                                                      uint32_t ldn, float eps, float qscale, float bias_scale,
+                                                      uint32_t ntiles, FastDiv nkbd) {
+  constexpr int C = 128, D = 32, H = 4, ROW = C * 2, KS = C / 16;
+  constexpr int PD = 4;             // loader register stages in flight
+  constexpr int PART = 64 * D * 2;  // bytes of one head's Q, K or V^T block of a tile
   using V8 = vec<T, 8>;
-  __shared__ __attribute__((aligned(16))) char xs[64 * ROW];
+
+  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];    // normalised x tiles
+  __shared__ __attribute__((aligned(16))) char os[H][3 * PART];   // per writer wave: Q | K | V^T
+  __shared__ __attribute__((aligned(16))) T bs[2][H * 64];         // pair bias [head][position]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, col = lane & 31;
-  const int h = wave;
-  const int64_t nkb = ldn / 64, nkt = ldn / 32, nqt = (N + 31) / 32;
+  const uint32_t nkb = ldn / 64, nkt = ldn / 32, nqt = (N + 31) / 32;
+  const uint32_t G = gridDim.x;
+  uint32_t t = blockIdx.x;
 
-  V8 wq[8], wk[8], wv[8];
-  {
-    const T* wh = wqkv + (int64_t)h * 3 * D * C + (int64_t)col * C + 8 * hl;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      wq[s] = ldg<V8>(wh + 16 * s);
-      wk[s] = ldg<V8>(wh + D * C + 16 * s);
-      wv[s] = ldg<V8>(wh + 2 * D * C + 16 * s);
+  if (wave < 4) {
+    // ================= loaders =================
+    const int ch = tid & 15, tq = tid >> 4;  // 16-byte chunk ch of tokens 16 k + tq, k < 4
+    V8 lnw = {}, lnb = {}, wz[H];
+    if constexpr (LN) {
+      lnw = ldg<V8>(w_ln + 8 * ch);
+      if (b_ln) lnb = ldg<V8>(b_ln + 8 * ch);
     }
-  }
-  const int tok = tid >> 2, part = tid & 3;  // LN mapping
-
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t i = tile / nkb, kb = tile % nkb;
-    const int64_t p = kb * 64 + tok;  // position of this thread's token
-    // ---- LN + bias (fp32), normalized tile -> LDS ----
-    {
-      float v[32];
-      if (p < N) {
-        const T* src = x + i * sx0 + p * sx1 + 32 * part;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const V8 a = ldg<V8>(src + 8 * e);
+    for (int hh = 0; hh < H; ++hh) wz[hh] = ldg<V8>(WZ + hh * C + 8 * ch);
+    const float bz = BZ ? BZ[ch & 3] : 0.f;
+    struct Stage {
+      V8 x[4];
+    };
+    auto fetch = [&](uint32_t tt, Stage& sg) {
+      tt = tt < ntiles ? tt : ntiles - 1;
+      const uint32_t i = nkbd.div(tt), kb = tt - i * nkb;
+      const T* row = x + (int64_t)i * sx0 + 8 * ch;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[8 * e + j] = (float)a[j];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) v[e] = 0.f;
+      for (int k = 0; k < 4; ++k) {
+        uint32_t p = kb * 64 + 16 * k + tq;
+        p = p < N ? p : N - 1;
+        sg.x[k] = ldg<V8>(row + (int64_t)p * sx1);
       }
-      if (apply_ln) {
-        float s = 0.f;
+    };
+    auto step = [&](uint32_t tt, int bb, Stage& sg) {
+      const uint32_t kb = tt - nkbd.div(tt) * nkb;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) s += v[e];
-        const float mean = group_sum<4>(s) * (1.0f / C);
-        float q = 0.f;
+      for (int k = 0; k < 4; ++k) {
+        const int tk = 16 * k + tq;
+        const bool valid = kb * 64 + tk < N;
+        float v[8];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) q += (v[e] - mean) * (v[e] - mean);
-        const float rstd = rsqrtf(group_sum<4>(q) * (1.0f / C) + eps);
+        for (int e = 0; e < 8; ++e) v[e] = valid ? (float)sg.x[k][e] : 0.f;
+        if constexpr (LN) {  // two-pass statistics over the token's 16 lanes
+          float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const V8 w8 = ldg<V8>(w_ln + 32 * part + 8 * e);
-          const V8 b8 = b_ln ? ldg<V8>(b_ln + 32 * part + 8 * e) : V8{};
+          for (int e = 0; e < 8; ++e) s += v[e];
+          const float mean = group_sum<16>(s) * (1.0f / C);
+          float q = 0.f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[8 * e + j] = (v[8 * e + j] - mean) * rstd * (float)w8[j] + (float)b8[j];
+          for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+          const float rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (v[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e];
         }
-      }
+        // pair bias of the 4 heads (fp32 dot products); lanes ch, ch + 4, ... all store head
+        // ch & 3 (the same value), keeping the loop free of divergent branches
+        float bsel = 0.f;
 #pragma unroll
-      for (int hh = 0; hh < H; ++hh) {
-        float d = 0.f;
+        for (int hh = 0; hh < H; ++hh) {
+          float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const V8 w8 = ldg<V8>(WZ + hh * C + 32 * part + 8 * e);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) d += v[8 * e + j] * (float)w8[j];
+          for (int e = 0; e < 8; ++e) d = fmaf(v[e], (float)wz[hh][e], d);
+          d = group_sum<16>(d);
+          bsel = (ch & 3) == hh ? d : bsel;
         }
-        d = group_sum<4>(d);
-        if (part == 0) {
-          const int64_t off = (((int64_t)hh * nqt + i / 32) * nkt + p / 32) * 1024 +
-                              ((((p % 32) / 16) * 64 + ((p % 16) / 8) * 32 + i % 32) * 8 + p % 8);
-          bias[off] = p < N ? (T)((d + (BZ ? BZ[hh] : 0.f)) * bias_scale) : (T)0.f;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
+        bs[bb][(ch & 3) * 64 + tk] = valid ? (T)((bsel + bz) * bias_scale) : (T)0.f;
         V8 o;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = (T)v[8 * e + j];
-        const int chunk = 4 * part + e;
-        *reinterpret_cast<V8*>(&xs[tok * ROW + ((chunk ^ (tok & 7)) << 4)]) = o;
+        for (int e = 0; e < 8; ++e) o[e] = (T)v[e];
+        *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ (tk & 15)) << 4)]) = o;
+      }
+      __syncthreads();  // tile tt staged; the writers are done with the tile before tt - 1
+      fetch(tt + PD * G, sg);  // refill this stage
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    const int bb = 0;
+    Stage s0, s1, s2, s3;
+    fetch(t, s0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
+    fetch(t + G, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(t + 2 * G, s2);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(t + 3 * G, s3);
+    __builtin_amdgcn_sched_barrier(0);
+    // block-uniform trip count (barriers match the writers'); the remainder runs after the
+    // loop so that its back edge is the only way to the loop head (a break out of the
+    // unrolled body would merge into the latch and make the compiler wait for every load)
+    uint32_t n = (ntiles - t + G - 1) / G;
+    for (; n >= 4; n -= 4, t += 4 * G) {
+      step(t, bb, s0);
+      step(t + G, bb ^ 1, s1);
+      step(t + 2 * G, bb, s2);
+      step(t + 3 * G, bb ^ 1, s3);
+    }
+    if (n > 0) step(t, bb, s0);
+    if (n > 1) step(t + G, bb ^ 1, s1);
+    if (n > 2) step(t + 2 * G, bb, s2);
+  } else {
+    // ================= writers: wave 4 + h owns head h =================
+    const int h = wave - 4, hl = lane >> 5, col = lane & 31;
+    V8 wq[KS], wk[KS], wv[KS];
+    {
+      const T* wh = wqkv + (int64_t)h * 3 * D * C + (int64_t)col * C + 8 * hl;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        wq[s] = ldg<V8>(wh + 16 * s);
+        wk[s] = ldg<V8>(wh + D * C + 16 * s);
+        wv[s] = ldg<V8>(wh + 2 * D * C + 16 * s);
       }
     }
-    __syncthreads();
-    // ---- Q, K, V of head h for the 64 positions ----
-    T* qdst = Qp + ((i * H + h) * ldn + kb * 64) * D;
-    T* kvdst = KV + ((i * H + h) * nkb + kb) * kKVBlock;
+    char* oh = os[h];
+    int bb = 0;
+    for (; t < ntiles; t += G) {
+      __syncthreads();  // tile t staged
+      // Q^T = WQ . x^T and K^T (lane -> position, slots -> d), V = x . WV^T (lane -> d, slots
+      // -> positions).  Slot v = 8 j + e of lane half hl is element 16 j + 8 hl + e of the
+      // permuted group of 32: 16-byte chunk 2 j + hl of the position's (or d's) 32 elements.
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int t = sub * 32 + col;
-      f32x16 aq = {}, ak = {}, av = {};
+      for (int sub = 0; sub < 2; ++sub) {
+        const int tp = sub * 32 + col;
+        f32x16 aq = {}, ak = {}, av = {};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const V8 xb = *reinterpret_cast<const V8*>(&xs[t * ROW + (((2 * s + hl) ^ (t & 7)) << 4)]);
-        aq = Mma<T>::m32(wq[s], xb, aq);  // Q^T: lane -> position t, d rows
-        ak = Mma<T>::m32(wk[s], xb, ak);  // K^T: lane -> key t, d rows
-        av = Mma<T>::m32(xb, wv[s], av);  // V:   lane -> d = col, key rows
+        for (int s = 0; s < KS; ++s) {
+          const V8 xb = *reinterpret_cast<const V8*>(&xs[bb][tp * ROW + (((2 * s + hl) ^ (tp & 15)) << 4)]);
+          aq = Mma<T>::m32(wq[s], xb, aq);
+          ak = Mma<T>::m32(wk[s], xb, ak);
+          av = Mma<T>::m32(xb, wv[s], av);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          V8 q, k, v;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            q[e] = (T)(aq[8 * j + e] * qscale);
+            k[e] = (T)ak[8 * j + e];
+            v[e] = (T)av[8 * j + e];
+          }
+          // Q / K rows are 64 bytes (4 chunks, swizzled by (row >> 2) & 3), V^T rows 128 bytes
+          // (8 chunks, swizzled by (row >> 1) & 7): 16 lanes of a store hit 16 distinct chunks
+          const int cq = (2 * j + hl) ^ ((tp >> 2) & 3);
+          *reinterpret_cast<V8*>(oh + tp * 64 + (cq << 4)) = q;
+          *reinterpret_cast<V8*>(oh + PART + tp * 64 + (cq << 4)) = k;
+          const int cv = (4 * sub + 2 * j + hl) ^ ((col >> 1) & 7);
+          *reinterpret_cast<V8*>(oh + 2 * PART + col * 128 + (cv << 4)) = v;
+        }
       }
-      V8 q0, q1, k0, k1, v0, v1;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint32_t i = nkbd.div(t), kb = t - i * nkb;
+      const uint64_t ih = (uint64_t)i * H + h;
+      T* qdst = Qp + (ih * ldn + kb * 64) * D;
+      T* kvdst = KV + (ih * nkb + kb) * kKVBlock;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        q0[e] = (T)(aq[e] * qscale);
-        q1[e] = (T)(aq[8 + e] * qscale);
-        k0[e] = (T)ak[e];
-        k1[e] = (T)ak[8 + e];
-        v0[e] = (T)av[e];
-        v1[e] = (T)av[8 + e];
+      for (int part = 0; part < 3; ++part) {
+        T* dst = part == 0 ? qdst : kvdst + (part - 1) * 64 * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ci = r * 64 + lane;  // 16-byte chunk of the 4 KB block
+          int a;
+          if (part < 2) {
+            const int row = ci >> 2, c = ci & 3;
+            a = row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+          } else {
+            const int row = ci >> 3, c = ci & 7;
+            a = row * 128 + ((c ^ ((row >> 1) & 7)) << 4);
+          }
+          stg<V8>(dst + 8 * ci, *reinterpret_cast<const V8*>(oh + part * PART + a));
+        }
       }
-      stg<V8>(qdst + t * D + 8 * hl, q0);
-      stg<V8>(qdst + t * D + 16 + 8 * hl, q1);
-      stg<V8>(kvdst + t * D + 8 * hl, k0);
-      stg<V8>(kvdst + t * D + 16 + 8 * hl, k1);
-      stg<V8>(kvdst + 64 * D + col * 64 + sub * 32 + 8 * hl, v0);
-      stg<V8>(kvdst + 64 * D + col * 64 + sub * 32 + 16 + 8 * hl, v1);
+      if (lane < 8) {  // bias: 8 positions of this head per lane, 16 bytes
+        const int g = lane;
+        const uint64_t off = (((uint64_t)h * nqt + i / 32) * nkt + 2 * kb + (g >> 2)) * 1024 +
+                             (((g >> 1) & 1) * 64 + (g & 1) * 32 + (i & 31)) * 8;
+        stg<V8>(bias + off, *reinterpret_cast<const V8*>(&bs[bb][h * 64 + 8 * g]));
+      }
+      bb ^= 1;
     }
-    __syncthreads();
   }
 }
 
@@ -463,10 +540,11 @@ static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln,
                       int64_t ldn, float eps, float qscale, hipStream_t st) {
   const int64_t ntiles = N * (ldn / 64);
   if (ntiles == 0) return TOPS_OK;
-  const int64_t grid = ntiles < 2LL * num_cus() ? ntiles : 2LL * num_cus();
-  hipLaunchKernelGGL((tri_prep_kernel<T, 4>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)x, sx0, sx1,
-                     (const T*)w_ln, (const T*)b_ln, apply_ln, (const T*)wqkv, (const T*)WZ, BZ, (T*)Qp, (T*)KV,
-                     (T*)bias, N, ldn, eps, qscale, kLog2e, ntiles);
+  const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
+  auto kern = apply_ln ? tri_prep_kernel<T, true> : tri_prep_kernel<T, false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), 0, st, (const T*)x, sx0, sx1, (const T*)w_ln,
+                     (const T*)b_ln, (const T*)wqkv, (const T*)WZ, BZ, (T*)Qp, (T*)KV, (T*)bias, (uint32_t)N,
+                     (uint32_t)ldn, eps, qscale, kLog2e, (uint32_t)ntiles, FastDiv((uint32_t)(ldn / 64)));
   return launched("tops_tri_prep");
 }
 
@@ -505,7 +583,8 @@ extern "C" int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void
                "tops_tri_prep: supports C == 128, H == 4, D == 32 (got %lld, %lld, %lld)", (long long)C,
                (long long)H, (long long)D);
   TOPS_REQUIRE(N >= 0 && N <= 4096 && ldn >= N && ldn % 64 == 0, "tops_tri_prep: bad N / ldn");
-  TOPS_REQUIRE(sx0 % 8 == 0 && sx1 % 8 == 0, "tops_tri_prep: x token strides must be multiples of 8");
+  TOPS_REQUIRE(sx0 % 8 == 0 && sx1 % 8 == 0 && (uintptr_t)x % 16 == 0,
+               "tops_tri_prep: x needs token strides that are multiples of 8 and a 16-byte aligned base");
   hipStream_t st = (hipStream_t)stream;
   const float qscale = scale * kLog2e;
   if (dtype == TOPS_DTYPE_BF16)
