@@ -378,6 +378,176 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------
+// Einsum, large L: 256 x 256 block tile, 4 waves (one per SIMD) of 128 x 128, k-tile 32.
+// Accumulators (256 registers per lane) live in the accumulation registers, which leaves room
+// for two register stages of global loads (each k-tile is fetched two tiles before it is
+// stored to LDS) and two fragment sets.  LDS holds three k-tiles: tile kt + 1 is stored at the
+// start of iteration kt into the buffer last read at kt - 2, one barrier in mid-iteration
+// publishes it, and the fragments of its first k-step are read during the second k-step of
+// tile kt, so the MFMA stream never waits on a barrier.  64-byte LDS rows (4 chunks): A rows
+// are swizzled by (row >> 2) & 3, B rows (read in the permuted order) by
+// ((row >> 2) & 1) | ((row >> 3) & 2): 16 lanes of a fragment read hit 16 distinct chunks.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+                                                         T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
+                                                         int64_t nslab, int tiles) {
+  constexpr int BM = 256, BK = 32, MI = 4, NJ = 4;
+  constexpr int TILE = BM * BK;  // elements of one operand's k-tile
+  using V8 = vec<T, 8>;
+
+  __shared__ __attribute__((aligned(16))) T As[3][TILE];
+  __shared__ __attribute__((aligned(16))) T Bs[3][TILE];
+
+  const int64_t total = nslab * tiles * tiles;
+  int64_t id = blockIdx.x;
+  if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+  const int64_t slab = id / (tiles * tiles);
+  const int rem = (int)(id % (tiles * tiles));
+  const int tm = rem / tiles, tn = rem % tiles;
+
+  const T* Ab = A + slab * L * ld;
+  const T* Bb = Bmat + slab * L * ld;
+  T* Yb = Y + slab * L * ldy;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+
+  auto swa = [](int row, int c) { return row * BK + ((c ^ ((row >> 2) & 3)) << 3); };
+  auto swb = [](int row, int c) { return row * BK + ((c ^ (((row >> 2) & 1) | ((row >> 3) & 2))) << 3); };
+
+  // loader: thread -> chunk lc of rows lr + 64 r (r < 4) of both operands
+  const int lc = tid & 3, lr = tid >> 2;
+  const int nk = (int)(ld / BK);
+  const T* arow[4];
+  const T* brow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int64_t ra = (int64_t)tm * BM + lr + 64 * r, rb = (int64_t)tn * BM + lr + 64 * r;
+    ra = ra < L ? ra : L - 1;
+    rb = rb < L ? rb : L - 1;
+    arow[r] = Ab + ra * ld + 8 * lc;
+    brow[r] = Bb + rb * ld + 8 * lc;
+  }
+  struct Stage {
+    V8 a[4], b[4];
+  };
+  auto gload = [&](int kt, Stage& sg) {
+    kt = kt < nk ? kt : nk - 1;  // past the end: reload the last tile (stored, never read)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sg.a[r] = ldg<V8>(arow[r] + kt * BK);
+      sg.b[r] = ldg<V8>(brow[r] + kt * BK);
+    }
+  };
+  auto sstore = [&](int buf, const Stage& sg) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      *reinterpret_cast<V8*>(&As[buf][swa(lr + 64 * r, lc)]) = sg.a[r];
+      *reinterpret_cast<V8*>(&Bs[buf][swb(lr + 64 * r, lc)]) = sg.b[r];
+    }
+  };
+  struct Frags {
+    V8 a[MI], b[NJ];
+  };
+  auto frags = [&](int buf, int ks, Frags& f) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(&As[buf][swa(wm * 128 + 32 * i + col, 2 * ks + hl)]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) f.b[j] = *reinterpret_cast<const V8*>(&Bs[buf][swb(wn * 128 + 32 * j + prow, 2 * ks + hl)]);
+  };
+
+  f32x16 acc[NJ][MI];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int i = 0; i < MI; ++i) acc[j][i] = f32x16{};
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < MI; ++i) acc[j][i] = Mma<T>::m32(f.b[j], f.a[i], acc[j][i]);
+  };
+
+  // iteration kt: store tile kt + 1 (stage sn) and refill sn with tile kt + 3; k-step 0 of
+  // tile kt with the fragments of k-step 1 read alongside; barrier; k-step 1 with the
+  // fragments of k-step 0 of tile kt + 1 read alongside.
+  // The memory instructions are spread one per MFMA so that a single wave keeps its SIMD's
+  // matrix core fed while they issue (and while a store waits for its global load).
+  auto iter = [&](int kt, int b0, int b1, Stage& sn, Frags& f0, Frags& f1) {
+    mfmas(f0);
+    frags(b0, 1, f1);
+    sstore(b1, sn);
+    gload(kt + 3, sn);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the k-step's MFMAs issue before the barrier
+    __syncthreads();
+    mfmas(f1);
+    frags(b1, 0, f0);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  Stage s0, s1;
+  Frags fa, fb;
+  gload(0, s0);
+  gload(1, s1);
+  sstore(0, s0);
+  gload(2, s0);
+  __syncthreads();
+  frags(0, 0, fa);
+  // buffers rotate 0, 1, 2; tile kt lives in buffer kt % 3, its successor in (kt + 1) % 3
+  int b0 = 0, b1 = 1, b2 = 2;
+  for (int kt = 0; kt < nk; kt += 2) {  // nk is even (ld % 64 == 0)
+    iter(kt, b0, b1, s1, fa, fb);
+    iter(kt + 1, b1, b2, s0, fa, fb);
+    const int t = b0;
+    b0 = b2;
+    b2 = b1;
+    b1 = t;
+  }
+  // b0..b2 rotation: after kt, kt+1 the next even tile kt+2 lives in old b2, kt+3 in old b0
+
+  // ---- Y[i][j0 .. j0 + 15] per lane: two 16-byte stores (columns [L, ldy) get finite filler) ----
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int64_t ii = (int64_t)tm * BM + wm * 128 + i * 32 + col;
+    if (ii < L) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * hl;
+        if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
+        V8 o0, o1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o0[e] = (T)acc[j][i][e];
+          o1[e] = (T)acc[j][i][8 + e];
+        }
+        stg<V8>(Yb + ii * ldy + j0, o0);
+        stg<V8>(Yb + ii * ldy + j0 + 8, o1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Output phase (C = C_out = 128).  8 waves; wave w computes features [32 (w & 3), +32) for the
 // 32 tokens [32 (w >> 2), +32) of a 64-token tile with its Wp / Wg rows in registers (rows
 // permuted so each lane ends up with 16 consecutive features of one token).  Roles as in the
@@ -605,8 +775,8 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
   if (L > 384) {
     const int t = (int)((L + 255) / 256);
     const int64_t grid = nslab * t * t;
-    hipLaunchKernelGGL((tmu_einsum_kernel<T, 256, 256, 8>), dim3((unsigned)grid), dim3(512), 0, st, A, Bm, (T*)y, L,
-                       ld, ldy, nslab, t, t);
+    hipLaunchKernelGGL((tmu_einsum4_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld, ldy,
+                       nslab, t);
   } else {
     const int t = (int)((L + 127) / 128);
     const int64_t grid = nslab * t * t;
