@@ -136,6 +136,35 @@ int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0
                      const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M, int64_t C,
                      int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
 
+/*
+ * Any-shape triangle attention (C_in, H, D other than 128, 4, 32; e.g. the D = 16, C_in = 64
+ * "Apo" shape of tests/test_triangle_attn.py:137-192).  The same three phases as above with
+ * plain layouts; they replace the reference's Triton path for those shapes
+ * (triangle_attn/kernel.py:256-340 with `separate_kv = D == 16`, :282).
+ *
+ * tops_tri_generic_prep: per token (a, b) of x (token at x[a*sx0 + b*sx1 + c], c < C):
+ *   xln    io   (N*N, C) contiguous: LN(x) (or x when apply_ln == 0)
+ *   q,k,v  io   (N, N, H, D) contiguous: LN(x) . W^T per head, wqkv as in tops_tri_prep
+ *   bias   fp32 (H, N, N): LN(x[a, b]) . WZ[h] + BZ[h] (unrounded LN), WZ io (H, C), BZ fp32 or NULL
+ *   C <= 1024, H <= 64, D <= 64.
+ * tops_tri_generic_attention: out[i*so0 + q*so1 + h*D + d] =
+ *   softmax_k(scale * q[i,q,h] . k[i,k,h] + bias[h,q,k] (+ -1e9 where mask[i*sm0 + k*sm1] == 0)) v
+ *   (fp32 scores; mask int8 or NULL).
+ * tops_gate_out_generic: tops_gate_out for any (C_in, H*D, C_out) with C_in + H*D <= 1024:
+ *   Wg io (H*D, C_in), Wo io (C_out, H*D) in (out, in) layout, o / gin at any token strides.
+ */
+int tops_tri_generic_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
+                          const void* wqkv, const void* WZ, const float* BZ, void* xln, void* q, void* k, void* v,
+                          float* bias, int64_t N, int64_t C, int64_t H, int64_t D, float eps, int dtype,
+                          void* stream);
+int tops_tri_generic_attention(const void* q, const void* k, const void* v, const float* bias, const void* mask,
+                               int64_t sm0, int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t H,
+                               int64_t D, float scale, int dtype, void* stream);
+int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
+                          const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg,
+                          const void* bg, const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2,
+                          int64_t Cin, int64_t HD, int64_t Cout, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -217,6 +217,79 @@ def test_tri_config_sizes_sampled_rows(device, N):
         _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri N={N} end")
 
 
+@pytest.mark.parametrize("N", [257, 300, 520])
+@pytest.mark.parametrize("mask", ["none", "pad", "random"])
+def test_tri_large_n_kernel(device, N, mask):
+    """N > 256 runs the two-group attention kernel: ragged N, random / padded masks, sampled rows
+    (first, last, padded and interior rows)."""
+    inp = tri_inputs(N, seed=N + 7, mask=mask, bias_z=True)
+    out = _tri_call(inp, device)
+    rows = torch.tensor([0, 1, N // 3, N // 2 + 5, N - N // 10 - 1, N - 2, N - 1])
+    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} mask={mask}")
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_tri_apo_d16(device, masked):
+    """The Apo shape of the reference's tests/test_triangle_attn.py:137-192 (N=33, H=4, D=16, C_in=64)
+    runs the any-shape kernels; precompute keeps separate WK_c / WV_c for D = 16."""
+    inp = tri_inputs(33, C=64, H=4, D=16, seed=31, mask="random" if masked else "none", bias_z=True)
+    d = to_dev(inp, device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], 4, 16)
+    assert pre["WK_c"] is not None and pre["WK_c"].data_ptr() != pre["WKV_c"].data_ptr()
+    out = tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=inp["scale"], eps=1e-5,
+                                     W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None)
+    assert out.shape == (33, 33, 64)
+    _check(out, _tri_ref(inp), torch.bfloat16, f"tri Apo masked={masked}")
+
+
+@pytest.mark.parametrize("N,C,H,D", [(40, 96, 3, 24), (70, 64, 2, 64), (130, 32, 8, 8), (257, 64, 4, 16)])
+@pytest.mark.parametrize("mask", ["pad", "random"])
+def test_tri_any_shape(device, N, C, H, D, mask):
+    """Shapes outside the tuned (C_in, H, D) = (128, 4, 32) run the any-shape kernels."""
+    inp = tri_inputs(N, C=C, H=H, D=D, seed=N + C, mask=mask, bias_z=True)
+    out = _tri_call(inp, device)
+    _check(out, _tri_ref(inp), torch.bfloat16, f"tri any-shape N={N} C={C} H={H} D={D} mask={mask}")
+
+
+def test_tri_any_shape_fp16_and_low_level(device):
+    """fp16 any-shape op; the low-level triangle_attn_forward (separate WK_c / WV_c, D = 16) fills
+    Bias_buf with the pair bias and matches forward() followed by the gate."""
+    inp = tri_inputs(48, C=64, H=4, D=16, seed=3, mask="random", dtype=torch.float16, bias_z=True)
+    _check(_tri_call(inp, device), _tri_ref(inp), torch.float16, "tri any-shape fp16")
+    inp = to_dev(tri_inputs(48, C=64, H=4, D=16, seed=4, mask="random", bias_z=True), device)
+    H, D, N = 4, 16, 48
+    pre = tops.triangle_attn.precompute(inp["W_ln"], inp["B_ln"], inp["WQ"], inp["WK"], inp["WV"], inp["W_proj_z"],
+                                        inp["B_proj_z"], H, D)
+    X_ln = torch.nn.functional.layer_norm(inp["X"], (64,), inp["W_ln"], inp["B_ln"], 1e-5)
+    O = torch.empty(N, N, H * D, device=device, dtype=torch.bfloat16)
+    Bias = torch.empty(H, N, N, device=device, dtype=torch.bfloat16)
+    tops.triangle_attn.triangle_attn_forward(X_ln, pre["WQ_c"], pre["WKV_c"], pre["WZ_c"], pre["BZ"], O,
+                                             scale=inp["scale"], mask=inp["mask"], Bias_buf=Bias, WK_c=pre["WK_c"],
+                                             WV_c=pre["WV_c"])
+    cpu = to_dev(inp, "cpu")
+    bias_ref = (X_ln.cpu().float() @ cpu["W_proj_z"].float() + cpu["B_proj_z"].float()).permute(2, 0, 1)
+    _check(Bias, bias_ref, torch.bfloat16, "tri low-level Bias_buf")
+    out = tops.triangle_attn.fused_gate_forward(O.view(N, N, H, D), X_ln, inp["W_proj_g"], inp["W_proj_o"])
+    _check(out, _tri_ref(cpu), torch.bfloat16, "tri any-shape low-level")
+
+
+def test_tri_bias_buf_fast_shape(device):
+    """Bias_buf holds the plain pair bias (not the kernels' log2(e)-scaled tiles) on the tuned path too."""
+    N = 64
+    inp = to_dev(tri_inputs(N, seed=9, mask="pad", bias_z=True), device)
+    pre = tops.triangle_attn.precompute(inp["W_ln"], inp["B_ln"], inp["WQ"], inp["WK"], inp["WV"], inp["W_proj_z"],
+                                        inp["B_proj_z"], 4, 32)
+    X_ln = torch.nn.functional.layer_norm(inp["X"], (128,), inp["W_ln"], inp["B_ln"], 1e-5)
+    O = torch.empty(N, N, 128, device=device, dtype=torch.bfloat16)
+    Bias = torch.empty(4, N, N, device=device, dtype=torch.bfloat16)
+    tops.triangle_attn.triangle_attn_forward(X_ln, pre["WQ_c"], pre["WKV_c"], pre["WZ_c"], pre["BZ"], O,
+                                             scale=inp["scale"], mask=inp["mask"], Bias_buf=Bias)
+    cpu = to_dev(inp, "cpu")
+    bias_ref = (X_ln.cpu().float() @ cpu["W_proj_z"].float() + cpu["B_proj_z"].float()).permute(2, 0, 1)
+    _check(Bias, bias_ref, torch.bfloat16, "tri Bias_buf")
+
+
 # --------------------------------------------------------------------------- #
 # attention_pair_bias
 # --------------------------------------------------------------------------- #

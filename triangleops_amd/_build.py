@@ -22,7 +22,7 @@ LIB_NAME = "libtriangleops_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = os.environ.get("TOPS_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["capi.hip", "tmu.hip", "tri.hip", "gate.hip", "apb.hip"]
+SOURCES = ["capi.hip", "tmu.hip", "tri.hip", "gate.hip", "apb.hip", "generic.hip"]
 
 CFLAGS = [
     f"--offload-arch={ARCH}",

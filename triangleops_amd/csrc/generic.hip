@@ -1,0 +1,305 @@
+// Any-shape kernels for the triangle-attention op and the gate / output projection: the
+// shapes the tuned kernels do not cover (C_in != 128, D != 32, H != 4, C_out != 128, e.g. the
+// D = 16, C_in = 64 "Apo" configuration).  Plain fp32 VALU arithmetic (no MFMA), written for
+// correctness at small and medium sizes; the rounding points follow the tuned path:
+//   LN(x) is rounded to the I/O type before the Q / K / V and gate products, Q / K / V and the
+//   gated activations are rounded to the I/O type, the pair bias stays fp32.
+//
+//   tri_generic_prep_kernel   per token: LN(x) (fp32, two-pass), Q / K / V of all heads and
+//                             the row-shared pair bias bias[h][a][b] = LN(x[a, b]) . Wz[h] + bz[h]
+//   tri_generic_attn_kernel   one thread per (row i, head h, query q): online softmax over the
+//                             row's keys in fp32, scores q . k * scale + bias, masked keys get
+//                             the reference's fp32 "+ (-1e9)"
+//   gate_generic_kernel       per token: y = (o * sigmoid(g . Wg^T + bg)) -> io, out = y . Wo^T + bo
+//                             with g = LN(gin) or gin
+//
+// Reference: triangle_attn/module.py:57-125 and benchmarks/references.py:174-205 (the op),
+// triangle_attn/kernel.py:230-238 (-1e9 pair mask), :282-290 (D = 16 keeps separate K / V
+// weights), tests/test_triangle_attn.py:137-192 (the Apo shape).
+#include "capi.hpp"
+#include "common.hpp"
+
+namespace tops {
+
+constexpr int kGenTok = 16;  // tokens per block; 16 lanes per token for the LayerNorm sums
+
+// LayerNorm of kGenTok token rows held in LDS (fp32, row length C, row stride ld): 16
+// consecutive lanes per token, two-pass statistics.  Writes normalised rows back in place.
+template <typename T>
+__device__ void gen_layer_norm(float* rows, int ld, int C, const T* w_ln, const T* b_ln, float eps) {
+  const int tid = threadIdx.x, t = tid >> 4, part = tid & 15;
+  float* r = rows + t * ld;
+  float s = 0.f;
+  for (int c = part; c < C; c += 16) s += r[c];
+  const float mean = group_sum<16>(s) / (float)C;
+  float q = 0.f;
+  for (int c = part; c < C; c += 16) q = fmaf(r[c] - mean, r[c] - mean, q);
+  const float rstd = rsqrtf(group_sum<16>(q) / (float)C + eps);
+  for (int c = part; c < C; c += 16) {
+    const float w = w_ln ? (float)w_ln[c] : 1.f, b = b_ln ? (float)b_ln[c] : 0.f;
+    r[c] = (r[c] - mean) * rstd * w + b;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Pre-pass: 256 threads per kGenTok tokens.  xs holds the fp32 rows, LN'd in place.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tri_generic_prep_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
+                                                              const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                              int apply_ln, const T* __restrict__ wqkv,
+                                                              const T* __restrict__ WZ, const float* __restrict__ BZ,
+                                                              T* __restrict__ xln, T* __restrict__ qo,
+                                                              T* __restrict__ ko, T* __restrict__ vo,
+                                                              float* __restrict__ bias, int64_t N, int C, int H, int D,
+                                                              float eps) {
+  extern __shared__ float xs[];  // [kGenTok][C]
+  const int tid = threadIdx.x;
+  const int64_t ntok = N * N, tok0 = (int64_t)blockIdx.x * kGenTok;
+  for (int e = tid; e < kGenTok * C; e += 256) {
+    const int t = e / C, c = e % C;
+    const int64_t tok = tok0 + t;
+    float v = 0.f;
+    if (tok < ntok) v = (float)x[(tok / N) * sx0 + (tok % N) * sx1 + c];
+    xs[e] = v;
+  }
+  __syncthreads();
+  if (apply_ln) gen_layer_norm<T>(xs, C, C, w_ln, b_ln, eps);
+  __syncthreads();
+  const int HD = H * D, F = 3 * HD + H;
+  for (int e = tid; e < kGenTok * F; e += 256) {
+    const int t = e / F, f = e % F;
+    const int64_t tok = tok0 + t;
+    if (tok >= ntok) continue;
+    const float* r = xs + t * C;
+    if (f < 3 * HD) {  // head h, which (0 = Q, 1 = K, 2 = V), d
+      const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+      const T* w = wqkv + (int64_t)f * C;  // (H, 3, D, C): row f
+      float acc = 0.f;
+      for (int c = 0; c < C; ++c) acc = fmaf((float)(T)r[c], (float)w[c], acc);
+      T* dst = which == 0 ? qo : which == 1 ? ko : vo;
+      dst[tok * HD + h * D + d] = (T)acc;
+    } else {
+      const int h = f - 3 * HD;
+      const T* w = WZ + (int64_t)h * C;
+      float acc = 0.f;
+      for (int c = 0; c < C; ++c) acc = fmaf(r[c], (float)w[c], acc);
+      bias[(int64_t)h * ntok + tok] = acc + (BZ ? BZ[h] : 0.f);
+    }
+  }
+  for (int e = tid; e < kGenTok * C; e += 256) {
+    const int64_t tok = tok0 + e / C;
+    if (tok < ntok) xln[tok * C + e % C] = (T)xs[e];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Attention: thread = (row i, head h, query q), q fastest so a wave shares (i, h) and its K / V
+// loads are broadcasts.  DM >= D is the register length of q and o.
+// ---------------------------------------------------------------------------------------------
+template <typename T, int DM>
+__global__ __launch_bounds__(256) void tri_generic_attn_kernel(const T* __restrict__ qi_, const T* __restrict__ ki_,
+                                                              const T* __restrict__ vi_, const float* __restrict__ bias,
+                                                              const int8_t* __restrict__ mask, int64_t sm0, int64_t sm1,
+                                                              T* __restrict__ out, int64_t so0, int64_t so1, int64_t N,
+                                                              int H, int D, float scale) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * H * N) return;
+  const int64_t q = idx % N, ih = idx / N;
+  const int h = (int)(ih % H);
+  const int64_t i = ih / H;
+  const int HD = H * D;
+  float qv[DM], o[DM];
+  const T* qp = qi_ + (i * N + q) * HD + h * D;
+#pragma unroll
+  for (int d = 0; d < DM; ++d) {
+    qv[d] = d < D ? (float)qp[d] * scale : 0.f;
+    o[d] = 0.f;
+  }
+  const float* brow = bias + ((int64_t)h * N + q) * N;
+  float m = -INFINITY, l = 0.f;
+  for (int64_t k = 0; k < N; ++k) {
+    const T* kp = ki_ + (i * N + k) * HD + h * D;
+    float s = 0.f;
+#pragma unroll
+    for (int d = 0; d < DM; ++d)
+      if (d < D) s = fmaf(qv[d], (float)kp[d], s);
+    s += brow[k];
+    if (mask && mask[i * sm0 + k * sm1] == 0) s += -1e9f;
+    const float mn = fmaxf(m, s);
+    const float corr = __expf(m - mn), p = __expf(s - mn);
+    m = mn;
+    l = l * corr + p;
+    const T* vp = vi_ + (i * N + k) * HD + h * D;
+#pragma unroll
+    for (int d = 0; d < DM; ++d)
+      if (d < D) o[d] = fmaf(p, (float)vp[d], o[d] * corr);
+  }
+  const float inv = 1.f / l;
+  T* dst = out + i * so0 + q * so1 + h * D;
+#pragma unroll
+  for (int d = 0; d < DM; ++d)
+    if (d < D) dst[d] = (T)(o[d] * inv);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Gate + output projection, any (C_in, HD, C_out): 256 threads per kGenTok tokens.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void gate_generic_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
+                                                          const T* __restrict__ gin, int64_t sg0, int64_t sg1,
+                                                          const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                          float eps, int apply_ln, const T* __restrict__ Wg,
+                                                          const T* __restrict__ bg, const T* __restrict__ Wo,
+                                                          const T* __restrict__ bo, T* __restrict__ out, int64_t M1,
+                                                          int64_t M2, int Cin, int HD, int Cout) {
+  extern __shared__ float sm[];
+  float* gs = sm;                   // [kGenTok][Cin]  gate input (normalised)
+  float* ys = sm + kGenTok * Cin;   // [kGenTok][HD]   o, then the gated activations
+  const int tid = threadIdx.x;
+  const int64_t M = M1 * M2, tok0 = (int64_t)blockIdx.x * kGenTok;
+  for (int e = tid; e < kGenTok * Cin; e += 256) {
+    const int64_t tok = tok0 + e / Cin;
+    float v = 0.f;
+    if (tok < M) v = (float)gin[(tok / M2) * sg0 + (tok % M2) * sg1 + e % Cin];
+    gs[e] = v;
+  }
+  for (int e = tid; e < kGenTok * HD; e += 256) {
+    const int64_t tok = tok0 + e / HD;
+    float v = 0.f;
+    if (tok < M) v = (float)o[(tok / M2) * so0 + (tok % M2) * so1 + e % HD];
+    ys[e] = v;
+  }
+  __syncthreads();
+  if (apply_ln) gen_layer_norm<T>(gs, Cin, Cin, w_ln, b_ln, eps);
+  __syncthreads();
+  for (int e = tid; e < kGenTok * HD; e += 256) {
+    const int t = e / HD, j = e % HD;
+    const float* g = gs + t * Cin;
+    const T* w = Wg + (int64_t)j * Cin;
+    float acc = bg ? (float)bg[j] : 0.f;
+    for (int c = 0; c < Cin; ++c) acc = fmaf((float)(T)g[c], (float)w[c], acc);
+    ys[e] = (float)(T)(ys[e] * sigmoid(acc));
+  }
+  __syncthreads();
+  for (int e = tid; e < kGenTok * Cout; e += 256) {
+    const int t = e / Cout, c = e % Cout;
+    const int64_t tok = tok0 + t;
+    if (tok >= M) continue;
+    const float* y = ys + t * HD;
+    const T* w = Wo + (int64_t)c * HD;
+    float acc = bo ? (float)bo[c] : 0.f;
+    for (int j = 0; j < HD; ++j) acc = fmaf(y[j], (float)w[j], acc);
+    out[tok * Cout + c] = (T)acc;
+  }
+}
+
+template <typename T>
+static int tri_generic_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln,
+                              int apply_ln, const void* wqkv, const void* WZ, const float* BZ, void* xln, void* q,
+                              void* k, void* v, float* bias, int64_t N, int C, int H, int D, float eps,
+                              hipStream_t st) {
+  const int64_t blocks = (N * N + kGenTok - 1) / kGenTok;
+  if (blocks == 0) return TOPS_OK;
+  hipLaunchKernelGGL((tri_generic_prep_kernel<T>), dim3((unsigned)blocks), dim3(256), kGenTok * C * sizeof(float), st,
+                     (const T*)x, sx0, sx1, (const T*)w_ln, (const T*)b_ln, apply_ln, (const T*)wqkv, (const T*)WZ,
+                     BZ, (T*)xln, (T*)q, (T*)k, (T*)v, bias, N, C, H, D, eps);
+  return launched("tops_tri_generic_prep");
+}
+
+template <typename T>
+static int tri_generic_attention_t(const void* q, const void* k, const void* v, const float* bias, const void* mask,
+                                   int64_t sm0, int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int H,
+                                   int D, float scale, hipStream_t st) {
+  const int64_t blocks = (N * H * N + 255) / 256;
+  if (blocks == 0) return TOPS_OK;
+#define TOPS_GEN_ATTN(DMV)                                                                                        \
+  hipLaunchKernelGGL((tri_generic_attn_kernel<T, DMV>), dim3((unsigned)blocks), dim3(256), 0, st, (const T*)q,   \
+                     (const T*)k, (const T*)v, bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, H, D, \
+                     scale)
+  if (D <= 16)
+    TOPS_GEN_ATTN(16);
+  else if (D <= 32)
+    TOPS_GEN_ATTN(32);
+  else
+    TOPS_GEN_ATTN(64);
+#undef TOPS_GEN_ATTN
+  return launched("tops_tri_generic_attention");
+}
+
+template <typename T>
+static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
+                          const void* w_ln, const void* b_ln, float eps, int apply_ln, const void* Wg, const void* bg,
+                          const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2, int Cin, int HD, int Cout,
+                          hipStream_t st) {
+  const int64_t blocks = (M1 * M2 + kGenTok - 1) / kGenTok;
+  if (blocks == 0) return TOPS_OK;
+  hipLaunchKernelGGL((gate_generic_kernel<T>), dim3((unsigned)blocks), dim3(256),
+                     (size_t)kGenTok * (Cin + HD) * sizeof(float), st, (const T*)o, so0, so1, (const T*)gin, sg0, sg1,
+                     (const T*)w_ln, (const T*)b_ln, eps, apply_ln, (const T*)Wg, (const T*)bg, (const T*)Wo,
+                     (const T*)bo, (T*)out, M1, M2, Cin, HD, Cout);
+  return launched("tops_gate_out_generic");
+}
+
+}  // namespace tops
+
+using namespace tops;
+
+extern "C" int tops_tri_generic_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln,
+                                     int apply_ln, const void* wqkv, const void* WZ, const float* BZ, void* xln,
+                                     void* q, void* k, void* v, float* bias, int64_t N, int64_t C, int64_t H,
+                                     int64_t D, float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(x && wqkv && WZ && xln && q && k && v && bias, "tops_tri_generic_prep: null pointer argument");
+  TOPS_REQUIRE(!apply_ln || w_ln, "tops_tri_generic_prep: w_ln is required when apply_ln != 0");
+  TOPS_REQUIRE(N >= 0 && N <= 65536, "tops_tri_generic_prep: bad N %lld", (long long)N);
+  TOPS_REQUIRE(C >= 1 && C <= 1024 && H >= 1 && H <= 64 && D >= 1 && D <= 64,
+               "tops_tri_generic_prep: supports C <= 1024, H <= 64, D <= 64 (got %lld, %lld, %lld)", (long long)C,
+               (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return tri_generic_prep_t<__bf16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, xln, q, k, v, bias, N, (int)C,
+                                      (int)H, (int)D, eps, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return tri_generic_prep_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, xln, q, k, v, bias, N,
+                                        (int)C, (int)H, (int)D, eps, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_tri_generic_prep: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_tri_generic_attention(const void* q, const void* k, const void* v, const float* bias,
+                                          const void* mask, int64_t sm0, int64_t sm1, void* out, int64_t so0,
+                                          int64_t so1, int64_t N, int64_t H, int64_t D, float scale, int dtype,
+                                          void* stream) {
+  TOPS_REQUIRE(q && k && v && bias && out, "tops_tri_generic_attention: null pointer argument");
+  TOPS_REQUIRE(N >= 0 && N <= 65536 && H >= 1 && H <= 64 && D >= 1 && D <= 64,
+               "tops_tri_generic_attention: supports H <= 64, D <= 64 (got N=%lld H=%lld D=%lld)", (long long)N,
+               (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return tri_generic_attention_t<__bf16>(q, k, v, bias, mask, sm0, sm1, out, so0, so1, N, (int)H, (int)D, scale,
+                                           st);
+  if (dtype == TOPS_DTYPE_F16)
+    return tri_generic_attention_t<_Float16>(q, k, v, bias, mask, sm0, sm1, out, so0, so1, N, (int)H, (int)D, scale,
+                                             st);
+  return fail(TOPS_EUNSUPPORTED, "tops_tri_generic_attention: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
+                                     int64_t sg1, const void* w_ln, const void* b_ln, float ln_eps, int apply_ln,
+                                     const void* Wg, const void* bg, const void* Wo, const void* bo, void* out,
+                                     int64_t M1, int64_t M2, int64_t Cin, int64_t HD, int64_t Cout, int dtype,
+                                     void* stream) {
+  TOPS_REQUIRE(o && gin && Wg && Wo && out, "tops_gate_out_generic: null pointer argument");
+  TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out_generic: w_ln is required when apply_ln != 0");
+  TOPS_REQUIRE(M1 >= 0 && M2 >= 0, "tops_gate_out_generic: bad sizes");
+  TOPS_REQUIRE(Cin >= 1 && HD >= 1 && Cout >= 1 && Cin + HD <= 1024 && Cout <= 4096,
+               "tops_gate_out_generic: supports C_in + H*D <= 1024, C_out <= 4096 (got %lld, %lld, %lld)",
+               (long long)Cin, (long long)HD, (long long)Cout);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return gate_generic_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1,
+                                  M2, (int)Cin, (int)HD, (int)Cout, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return gate_generic_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out,
+                                    M1, M2, (int)Cin, (int)HD, (int)Cout, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_gate_out_generic: unsupported dtype code %d", dtype);
+}

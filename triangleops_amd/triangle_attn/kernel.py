@@ -82,6 +82,86 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
     return Qp, KV, bias, ldn
 
 
+LOG2E = 1.4426950408889634
+
+
+def fast_shape(C, H, D, C_out=None):
+    """True when the tuned kernels apply: C_in = 128, H = 4, D = 32 (and C_out = 128)."""
+    return C == 128 and H == 4 and D == 32 and (C_out is None or C_out == 128)
+
+
+def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=True):
+    """Any-shape pre-pass over X (N, N, C): (xln, q, k, v, bias) with q/k/v (N, N, H, D) in X's
+    dtype and bias (H, N, N) fp32 (tops_tri_generic_prep)."""
+    N, _, C = X.shape
+    H, _, D, _ = wqkv.shape
+    _native.check_device(X, wqkv, WZ_c, W_ln)
+    if X.stride(2) != 1:
+        X = X.contiguous()
+    dt = X.dtype
+    xln = torch.empty(N, N, C, device=X.device, dtype=dt)
+    q, k, v = (torch.empty(N, N, H, D, device=X.device, dtype=dt) for _ in range(3))
+    bias = torch.empty(H, N, N, device=X.device, dtype=torch.float32)
+    BZf = None if BZ is None else BZ.float().contiguous()
+    _native.call(
+        "tops_tri_generic_prep",
+        X.data_ptr(),
+        X.stride(0),
+        X.stride(1),
+        _native.ptr(_as(X, W_ln)) if apply_ln else None,
+        _native.ptr(_as(X, B_ln)) if apply_ln else None,
+        1 if apply_ln else 0,
+        _as(X, wqkv).data_ptr(),
+        _as(X, WZ_c).data_ptr(),
+        _native.ptr(BZf),
+        xln.data_ptr(),
+        q.data_ptr(),
+        k.data_ptr(),
+        v.data_ptr(),
+        bias.data_ptr(),
+        N,
+        C,
+        H,
+        D,
+        float(eps),
+        io_dtype_code(dt),
+        _native.stream_of(X),
+    )
+    return xln, q, k, v, bias
+
+
+def generic_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
+    """Any-shape attention core: out[i, q, h*D:(h+1)*D] = softmax_k(scale q.k + bias - 1e9 [masked]) v."""
+    N, _, H, D = q.shape
+    _native.check_device(q, k, v, bias, out, mask)
+    assert out.shape == (N, N, H * D) and out.stride(2) == 1, "out must be (N, N, H*D) with unit last stride"
+    m8 = None
+    sm0 = sm1 = 0
+    if mask is not None:
+        m8 = mask.view(torch.int8) if mask.dtype in (torch.bool, torch.uint8) else mask.to(torch.int8)
+        sm0, sm1 = m8.stride()
+    _native.call(
+        "tops_tri_generic_attention",
+        q.data_ptr(),
+        k.data_ptr(),
+        v.data_ptr(),
+        bias.data_ptr(),
+        _native.ptr(m8),
+        sm0,
+        sm1,
+        out.data_ptr(),
+        out.stride(0),
+        out.stride(1),
+        N,
+        H,
+        D,
+        float(scale),
+        io_dtype_code(q.dtype),
+        _native.stream_of(q),
+    )
+    return out
+
+
 def untile_bias(bias, N):
     """(H, N, N) view-copy of the pre-pass bias tiles (log2(e)-scaled, see tops_tri_prep)."""
     H, nqt, nkt, _ = bias.shape
@@ -136,7 +216,7 @@ def triangle_attn_forward(
 ):
     """Bias projection + attention over a pre-normalized X_ln (N, N, C), written into out (N, N, H*D).
 
-    `Bias_buf` (optional (H, N, N) scratch) receives log2(e) * bias, the form the kernel uses.
+    `Bias_buf` (optional (H, N, N) scratch) receives the pair bias, as in the reference.
     """
     N, N2, C = X_ln.shape
     assert N == N2
@@ -145,9 +225,14 @@ def triangle_attn_forward(
     assert WKV_c.shape == (C, 2 * H * D)
     assert out.shape == (N, N, H * D)
     wqkv = wqkv_from_layouts(_as(X_ln, WQ_c), _as(X_ln, WKV_c), H, D, _as(X_ln, WK_c), _as(X_ln, WV_c))
+    if not fast_shape(C, H, D):
+        xln, q, k, v, bias = generic_prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, apply_ln=False)
+        if Bias_buf is not None:
+            Bias_buf.copy_(bias)
+        return generic_attention(q, k, v, bias, out, scale=scale, mask=mask)
     Qp, KV, bias, ldn = prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, scale=scale, apply_ln=False)
     if Bias_buf is not None:
-        Bias_buf.copy_(untile_bias(bias, N))
+        Bias_buf.copy_(untile_bias(bias, N).float() * (1.0 / LOG2E))
     return attention_core(Qp, KV, bias, out, N=N, ldn=ldn, mask=mask)
 
 
@@ -159,6 +244,9 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
     """
     N1, N2, C = o.shape
     _native.check_device(o, gin, W_g, W_o)
+    Cin = gin.shape[-1]
+    if not (C == 128 and Cin == 128 and W_o.shape[0] == 128):
+        return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln)
     if o.stride(2) != 1 or o.stride(0) % 8 or o.stride(1) % 8 or o.data_ptr() % 16:
         o = o.contiguous()
     gin = gin.reshape(N1, N2, C) if gin.dim() != 3 else gin
@@ -189,6 +277,49 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
         N1,
         N2,
         C,
+        io_dtype_code(o.dtype),
+        _native.stream_of(o),
+    )
+    return out
+
+
+def _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
+    """gate_out_forward for any (C_in, H*D, C_out) (tops_gate_out_generic)."""
+    N1, N2, HD = o.shape
+    Cin, Cout = gin.shape[-1], W_o.shape[0]
+    assert W_g.shape == (HD, Cin) and W_o.shape == (Cout, HD), "W_g (H*D, C_in) and W_o (C_out, H*D) expected"
+    gin = gin.reshape(N1, N2, Cin) if gin.dim() != 3 else gin
+    if o.stride(2) != 1:
+        o = o.contiguous()
+    if gin.stride(2) != 1:
+        gin = gin.contiguous()
+    w_ln = b_ln = None
+    eps = 1e-5
+    if ln is not None:
+        w_ln, b_ln, eps = ln
+    out = torch.empty(N1, N2, Cout, device=o.device, dtype=o.dtype)
+    _native.call(
+        "tops_gate_out_generic",
+        o.data_ptr(),
+        o.stride(0),
+        o.stride(1),
+        gin.data_ptr(),
+        gin.stride(0),
+        gin.stride(1),
+        _native.ptr(_as(o, w_ln)),
+        _native.ptr(_as(o, b_ln)),
+        float(eps),
+        1 if ln is not None else 0,
+        _as(o, W_g).data_ptr(),
+        _native.ptr(_as(o, b_g)),
+        _as(o, W_o).data_ptr(),
+        _native.ptr(_as(o, b_o)),
+        out.data_ptr(),
+        N1,
+        N2,
+        Cin,
+        HD,
+        Cout,
         io_dtype_code(o.dtype),
         _native.stream_of(o),
     )

@@ -17,7 +17,7 @@ read the transposed view in place, so no transpose copy is made.  Any N is handl
 import torch
 
 from .._common.layouts import interleave_kv, qkv_head_major
-from .kernel import attention_core, gate_out_forward, prep_forward
+from .kernel import attention_core, fast_shape, gate_out_forward, generic_attention, generic_prep_forward, prep_forward
 
 
 def precompute(W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, H, D):
@@ -53,7 +53,12 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
     wqkv = pre["wqkv_hm"]
     if wqkv.dtype != X.dtype:
         wqkv = wqkv.to(X.dtype)
-    H, _, D, _ = wqkv.shape
+    H, _, D, C = wqkv.shape
+    if not fast_shape(C, H, D, W_proj_o.shape[0]):  # any-shape kernels (e.g. D = 16, C_in = 64)
+        xln, q, k, v, bias = generic_prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], eps=eps)
+        O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
+        generic_attention(q, k, v, bias, O, scale=scale, mask=mask)
+        return gate_out_forward(O, xln, W_proj_g, None, W_proj_o, None)
     Qp, KV, bias, ldn = prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], scale=scale, eps=eps)
     O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
     attention_core(Qp, KV, bias, O, N=N, ldn=ldn, mask=mask)
