@@ -274,6 +274,15 @@ def test_tri_any_shape_fp16_and_low_level(device):
     _check(out, _tri_ref(cpu), torch.bfloat16, "tri any-shape low-level")
 
 
+@pytest.mark.parametrize("C,H,D", [(128, 4, 32), (64, 4, 16)])
+def test_tri_fp32_io(device, C, H, D):
+    """fp32 I/O runs the any-shape kernels with every value in fp32 (max |d| <= 1e-4)."""
+    inp = tri_inputs(40, C=C, H=H, D=D, seed=C + 1, mask="random", dtype=torch.float32, bias_z=True)
+    out = _tri_call(inp, device)
+    assert out.dtype == torch.float32
+    _check(out, _tri_ref(inp), torch.float32, f"tri fp32 C={C}")
+
+
 def test_tri_bias_buf_fast_shape(device):
     """Bias_buf holds the plain pair bias (not the kernels' log2(e)-scaled tiles) on the tuned path too."""
     N = 64

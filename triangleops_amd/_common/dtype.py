@@ -18,7 +18,8 @@ TORCH_TO_TL = {
     torch.float32: DTYPE_F32,
 }
 
-# dtypes the gfx950 kernels compute on (MFMA operands); fp32 I/O is rejected by the kernels.
+# dtypes the tuned gfx950 kernels compute on (MFMA operands).  fp32 I/O is taken by the
+# any-shape fp32 kernels where an op has them (`any_shape_dtype_code`).
 KERNEL_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -38,3 +39,8 @@ def io_dtype_code(dtype: torch.dtype) -> int:
             f"IO dtype {dtype} is not supported by the gfx950 kernels; use torch.bfloat16 or torch.float16"
         )
     return code
+
+
+def any_shape_dtype_code(dtype: torch.dtype) -> int:
+    """C-ABI dtype code for the any-shape kernels, which also take fp32 I/O."""
+    return tl_io_dtype(dtype)

@@ -1,7 +1,8 @@
 // Any-shape kernels for the triangle-attention op and the gate / output projection: the
 // shapes the tuned kernels do not cover (C_in != 128, D != 32, H != 4, C_out != 128, e.g. the
 // D = 16, C_in = 64 "Apo" configuration).  Plain fp32 VALU arithmetic (no MFMA), written for
-// correctness at small and medium sizes; the rounding points follow the tuned path:
+// correctness at small and medium sizes, and the path of fp32 I/O (then every value stays fp32);
+// with 16-bit I/O the rounding points follow the tuned path:
 //   LN(x) is rounded to the I/O type before the Q / K / V and gate products, Q / K / V and the
 //   gated activations are rounded to the I/O type, the pair bias stays fp32.
 //
@@ -262,6 +263,9 @@ extern "C" int tops_tri_generic_prep(const void* x, int64_t sx0, int64_t sx1, co
   if (dtype == TOPS_DTYPE_F16)
     return tri_generic_prep_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, xln, q, k, v, bias, N,
                                         (int)C, (int)H, (int)D, eps, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return tri_generic_prep_t<float>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, xln, q, k, v, bias, N, (int)C,
+                                     (int)H, (int)D, eps, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_generic_prep: unsupported dtype code %d", dtype);
 }
 
@@ -280,6 +284,8 @@ extern "C" int tops_tri_generic_attention(const void* q, const void* k, const vo
   if (dtype == TOPS_DTYPE_F16)
     return tri_generic_attention_t<_Float16>(q, k, v, bias, mask, sm0, sm1, out, so0, so1, N, (int)H, (int)D, scale,
                                              st);
+  if (dtype == TOPS_DTYPE_F32)
+    return tri_generic_attention_t<float>(q, k, v, bias, mask, sm0, sm1, out, so0, so1, N, (int)H, (int)D, scale, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_generic_attention: unsupported dtype code %d", dtype);
 }
 
@@ -301,5 +307,8 @@ extern "C" int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, co
   if (dtype == TOPS_DTYPE_F16)
     return gate_generic_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out,
                                     M1, M2, (int)Cin, (int)HD, (int)Cout, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return gate_generic_t<float>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1, M2,
+                                 (int)Cin, (int)HD, (int)Cout, st);
   return fail(TOPS_EUNSUPPORTED, "tops_gate_out_generic: unsupported dtype code %d", dtype);
 }

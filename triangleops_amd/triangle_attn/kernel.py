@@ -11,7 +11,7 @@ Same names and arguments as the reference's launchers (`triangle_attn/kernel.py:
 import torch
 
 from .. import _native
-from .._common.dtype import io_dtype_code
+from .._common.dtype import any_shape_dtype_code, io_dtype_code
 
 
 def _as(x, t):
@@ -124,7 +124,7 @@ def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=Tr
         H,
         D,
         float(eps),
-        io_dtype_code(dt),
+        any_shape_dtype_code(dt),
         _native.stream_of(X),
     )
     return xln, q, k, v, bias
@@ -156,7 +156,7 @@ def generic_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
         H,
         D,
         float(scale),
-        io_dtype_code(q.dtype),
+        any_shape_dtype_code(q.dtype),
         _native.stream_of(q),
     )
     return out
@@ -225,7 +225,7 @@ def triangle_attn_forward(
     assert WKV_c.shape == (C, 2 * H * D)
     assert out.shape == (N, N, H * D)
     wqkv = wqkv_from_layouts(_as(X_ln, WQ_c), _as(X_ln, WKV_c), H, D, _as(X_ln, WK_c), _as(X_ln, WV_c))
-    if not fast_shape(C, H, D):
+    if not fast_shape(C, H, D) or X_ln.dtype == torch.float32:
         xln, q, k, v, bias = generic_prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, apply_ln=False)
         if Bias_buf is not None:
             Bias_buf.copy_(bias)
@@ -245,7 +245,7 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
     N1, N2, C = o.shape
     _native.check_device(o, gin, W_g, W_o)
     Cin = gin.shape[-1]
-    if not (C == 128 and Cin == 128 and W_o.shape[0] == 128):
+    if not (C == 128 and Cin == 128 and W_o.shape[0] == 128) or o.dtype == torch.float32:
         return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln)
     if o.stride(2) != 1 or o.stride(0) % 8 or o.stride(1) % 8 or o.data_ptr() % 16:
         o = o.contiguous()
@@ -320,7 +320,7 @@ def _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
         Cin,
         HD,
         Cout,
-        io_dtype_code(o.dtype),
+        any_shape_dtype_code(o.dtype),
         _native.stream_of(o),
     )
     return out
