@@ -51,6 +51,29 @@ def test_tmu_fp16(device, dtype, direction):
     _check(out, expect, dtype, f"tmu fp16 {direction}")
 
 
+@pytest.mark.parametrize("C", [32, 64, 96, 192])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_any_channels(device, C, direction):
+    """C != 128 runs the any-shape input / output phases; the einsum kernels take any channel count."""
+    x, m, w = tmu_inputs(70, C=C, seed=C, mask="random")
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device))
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.bfloat16, f"tmu C={C} {direction}")
+
+
+@pytest.mark.parametrize("C,L", [(128, 40), (64, 130)])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_fp32_io(device, C, L, direction):
+    """fp32 I/O: any-shape phases and the fp32 batched product, every value fp32 (max |d| <= 1e-4)."""
+    x, m, w = tmu_inputs(L, C=C, seed=L + C, mask="pad", dtype=torch.float32)
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device))
+    assert out.dtype == torch.float32
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.float32, f"tmu fp32 C={C} L={L} {direction}")
+
+
 def test_tmu_batch(device):
     x, m, w = tmu_inputs(48, B=3, seed=7, mask="random")
     for direction in ("outgoing", "incoming"):

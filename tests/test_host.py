@@ -148,12 +148,14 @@ def test_cpu_tensors_rejected():
         tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
 
 
-def test_fp32_io_rejected_clearly():
-    C = 128
+def test_fp32_io_rejected_clearly_by_apb():
+    """attention_pair_bias has no fp32 kernels: fp32 tensors raise ValueError before any launch."""
     r = _w(dt=torch.float32)
-    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    M, C, H, D = 8, 128, 4, 32
+    pre = tops.attn_pair_bias.precompute(r(C, H * D), r(C, H * D), r(C, H * D), r(C), r(C), r(C, H), None, H, D)
     with pytest.raises(ValueError, match="not supported by the gfx950 kernels"):
-        tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
+        tops.attn_pair_bias.forward(r(M, C), r(M, M, C), pre, W_proj_g=r(C, C), B_proj_g=None, W_proj_o=r(C, C),
+                                    B_proj_o=None)
 
 
 def test_missing_library_fresh_process(tmp_path):

@@ -14,11 +14,18 @@
 //   gate_generic_kernel       per token: y = (o * sigmoid(g . Wg^T + bg)) -> io, out = y . Wo^T + bo
 //                             with g = LN(gin) or gin
 //
+//   tmu_generic_in_kernel     triangle_multiplicative_update input phase at any C / C_out:
+//                             ab[f] = (xn . Wp[f] + Bp[f]) * sigmoid(xn . Wg[f] + Bg[f]) * mask,
+//                             xn = (x - mean) * rstd (the LN affine is folded into Wp / Wg)
+//   tmu_generic_einsum_kernel fp32 batched y = A . B^T (64 x 64 tiles, 4 x 4 per thread)
+//   tmu_generic_out_kernel    output phase: (yn . Wp + Bp) * sigmoid(xn . Wg + Bg), yn = LN_out(y)
+//
 // Reference: triangle_attn/module.py:57-125 and benchmarks/references.py:174-205 (the op),
 // triangle_attn/kernel.py:230-238 (-1e9 pair mask), :282-290 (D = 16 keeps separate K / V
 // weights), tests/test_triangle_attn.py:137-192 (the Apo shape).
 #include "capi.hpp"
 #include "common.hpp"
+#include "generic.hpp"
 
 namespace tops {
 
@@ -240,6 +247,206 @@ static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* g
                      (const T*)w_ln, (const T*)b_ln, eps, apply_ln, (const T*)Wg, (const T*)bg, (const T*)Wo,
                      (const T*)bo, (T*)out, M1, M2, Cin, HD, Cout);
   return launched("tops_gate_out_generic");
+}
+
+// ---------------------------------------------------------------------------------------------
+// triangle_multiplicative_update, any C (triangle_mul/module.py:8-12: x is (B, L, L, D), any D;
+// triangle_mul/kernel.py:235-326).  Tokens t = (b, i, j) in row-major order.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_generic_in_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
+                                                            const T* __restrict__ Wp, const T* __restrict__ Wg,
+                                                            const float* __restrict__ Bp, const float* __restrict__ Bg,
+                                                            T* __restrict__ ab, int64_t B, int64_t L, int C, int Cout,
+                                                            int64_t ld, int transpose, float eps) {
+  extern __shared__ float xs[];  // [kGenTok][C]
+  const int tid = threadIdx.x;
+  const int64_t ntok = B * L * L, tok0 = (int64_t)blockIdx.x * kGenTok;
+  for (int e = tid; e < kGenTok * C; e += 256) {
+    const int64_t tok = tok0 + e / C;
+    xs[e] = tok < ntok ? (float)x[tok * C + e % C] : 0.f;
+  }
+  __syncthreads();
+  gen_layer_norm<T>(xs, C, C, nullptr, nullptr, eps);
+  __syncthreads();
+  for (int e = tid; e < kGenTok * C; e += 256) xs[e] = (float)(T)xs[e];  // GEMM operand in the I/O type
+  __syncthreads();
+  const int64_t fstride = B * L * ld;
+  for (int e = tid; e < kGenTok * Cout; e += 256) {
+    const int t = e / Cout, f = e % Cout;
+    const int64_t tok = tok0 + t;
+    if (tok >= ntok) continue;
+    const float* r = xs + t * C;
+    const T* wp = Wp + (int64_t)f * C;
+    const T* wg = Wg + (int64_t)f * C;
+    float p = Bp[f], g = Bg[f];
+    for (int c = 0; c < C; ++c) {
+      p = fmaf(r[c], (float)wp[c], p);
+      g = fmaf(r[c], (float)wg[c], g);
+    }
+    const float m = mask ? (mask[tok] != 0 ? 1.f : 0.f) : 1.f;
+    const int64_t b = tok / (L * L), rem = tok % (L * L), i = rem / L, j = rem % L;
+    const int64_t row = transpose ? j : i, col = transpose ? i : j;
+    T* dst = ab + f * fstride + (b * L + row) * ld;
+    dst[col] = (T)(p * sigmoid(g) * m);
+    if (col == L - 1)  // zero k-padding of this row for the einsum
+      for (int64_t c = L; c < ld; ++c) dst[c] = (T)0.f;
+  }
+}
+
+// fp32 batched product: per slab s, Y[i][j] = sum_k A[i][k] B[j][k], k < ld (A, B zero-padded).
+__global__ __launch_bounds__(256) void tmu_generic_einsum_kernel(const float* __restrict__ A,
+                                                                const float* __restrict__ Bm, float* __restrict__ Y,
+                                                                int64_t L, int64_t ld, int64_t ldy, int tiles) {
+  constexpr int TM = 64, TK = 16;
+  __shared__ float As[TK][TM + 1], Bs[TK][TM + 1];
+  const int64_t slab = blockIdx.x / (tiles * tiles);
+  const int rem = (int)(blockIdx.x % (tiles * tiles));
+  const int tm = rem / tiles, tn = rem % tiles;
+  const float* Ab = A + slab * L * ld;
+  const float* Bb = Bm + slab * L * ld;
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < ld; k0 += TK) {
+    for (int e = tid; e < TM * TK; e += 256) {
+      const int r = e / TK, k = e % TK;
+      const int64_t ia = (int64_t)tm * TM + r, ib = (int64_t)tn * TM + r;
+      As[k][r] = ia < L ? Ab[ia * ld + k0 + k] : 0.f;
+      Bs[k][r] = ib < L ? Bb[ib * ld + k0 + k] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < TK; ++k) {
+      float a[4], b[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[u] = As[k][ty * 4 + u];
+        b[u] = Bs[k][tx * 4 + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(a[u], b[v], acc[u][v]);
+    }
+    __syncthreads();
+  }
+  float* Yb = Y + slab * L * ldy;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = (int64_t)tm * TM + ty * 4 + u;
+    if (i >= L) continue;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t j = (int64_t)tn * TM + tx * 4 + v;
+      if (j < L) Yb[i * ldy + j] = acc[u][v];
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
+                                                             const T* __restrict__ Wp, const T* __restrict__ Wg,
+                                                             const float* __restrict__ Bp,
+                                                             const float* __restrict__ Bg, T* __restrict__ out,
+                                                             int64_t B, int64_t L, int C, int Cout, int64_t ldy,
+                                                             float eps) {
+  extern __shared__ float sm[];
+  float* ys = sm;                 // [kGenTok][C]  y of the tile's tokens (token-major)
+  float* xs = sm + kGenTok * C;   // [kGenTok][C]  x
+  const int tid = threadIdx.x;
+  const int64_t ntok = B * L * L, tok0 = (int64_t)blockIdx.x * kGenTok, cstride = B * L * ldy;
+  for (int e = tid; e < kGenTok * C; e += 256) {
+    const int t = e % kGenTok, c = e / kGenTok;  // token fastest: y is channel-major
+    const int64_t tok = tok0 + t;
+    float v = 0.f;
+    if (tok < ntok) {
+      const int64_t b = tok / (L * L), rem = tok % (L * L);
+      v = (float)y[c * cstride + (b * L + rem / L) * ldy + rem % L];
+    }
+    ys[t * C + c] = v;
+  }
+  for (int e = tid; e < kGenTok * C; e += 256) {
+    const int64_t tok = tok0 + e / C;
+    xs[e] = tok < ntok ? (float)x[tok * C + e % C] : 0.f;
+  }
+  __syncthreads();
+  gen_layer_norm<T>(ys, C, C, nullptr, nullptr, eps);
+  gen_layer_norm<T>(xs, C, C, nullptr, nullptr, eps);
+  __syncthreads();
+  for (int e = tid; e < 2 * kGenTok * C; e += 256) sm[e] = (float)(T)sm[e];
+  __syncthreads();
+  for (int e = tid; e < kGenTok * Cout; e += 256) {
+    const int t = e / Cout, f = e % Cout;
+    const int64_t tok = tok0 + t;
+    if (tok >= ntok) continue;
+    const float* yr = ys + t * C;
+    const float* xr = xs + t * C;
+    const T* wp = Wp + (int64_t)f * C;
+    const T* wg = Wg + (int64_t)f * C;
+    float p = Bp[f], g = Bg[f];
+    for (int c = 0; c < C; ++c) {
+      p = fmaf(yr[c], (float)wp[c], p);
+      g = fmaf(xr[c], (float)wg[c], g);
+    }
+    out[tok * Cout + f] = (T)(p * sigmoid(g));
+  }
+}
+
+int tmu_generic_input_phase(const void* x, const void* mask, const void* Wp, const void* Wg, const float* Bp,
+                            const float* Bg, void* ab, int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ld,
+                            int transpose, float eps, int dtype, hipStream_t st) {
+  TOPS_REQUIRE(C >= 1 && C <= 1024 && C_out >= 1 && C_out <= 4096,
+               "tops_tmu_input_phase: supports C <= 1024, C_out <= 4096 (got %lld, %lld)", (long long)C,
+               (long long)C_out);
+  const int64_t blocks = (B * L * L + kGenTok - 1) / kGenTok;
+  if (blocks == 0) return TOPS_OK;
+  const size_t lds = (size_t)kGenTok * C * sizeof(float);
+#define TOPS_GEN_IN(TT)                                                                                            hipLaunchKernelGGL((tmu_generic_in_kernel<TT>), dim3((unsigned)blocks), dim3(256), lds, st, (const TT*)x,                           (const int8_t*)mask, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (TT*)ab, B, L, (int)C, (int)C_out,                      ld, transpose, eps)
+  if (dtype == TOPS_DTYPE_BF16)
+    TOPS_GEN_IN(__bf16);
+  else if (dtype == TOPS_DTYPE_F16)
+    TOPS_GEN_IN(_Float16);
+  else if (dtype == TOPS_DTYPE_F32)
+    TOPS_GEN_IN(float);
+  else
+    return fail(TOPS_EUNSUPPORTED, "tops_tmu_input_phase: unsupported dtype code %d", dtype);
+#undef TOPS_GEN_IN
+  return launched("tops_tmu_input_phase");
+}
+
+int tmu_generic_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
+                       hipStream_t st) {
+  TOPS_REQUIRE(dtype == TOPS_DTYPE_F32, "tops_tmu_einsum: the any-shape product is fp32 only (dtype %d)", dtype);
+  const int tiles = (int)((L + 63) / 64);
+  const int64_t grid = nslab * tiles * tiles;
+  if (grid == 0) return TOPS_OK;
+  TOPS_REQUIRE(grid < (1LL << 31), "tops_tmu_einsum: too many tiles");
+  const float* A = (const float*)ab;
+  hipLaunchKernelGGL(tmu_generic_einsum_kernel, dim3((unsigned)grid), dim3(256), 0, st, A, A + nslab * L * ld,
+                     (float*)y, L, ld, ldy, tiles);
+  return launched("tops_tmu_einsum");
+}
+
+int tmu_generic_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* Bp,
+                             const float* Bg, void* out, int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ldy,
+                             float eps, int dtype, hipStream_t st) {
+  TOPS_REQUIRE(C >= 1 && C <= 512 && C_out >= 1 && C_out <= 4096,
+               "tops_tmu_output_phase: supports C <= 512, C_out <= 4096 (got %lld, %lld)", (long long)C,
+               (long long)C_out);
+  const int64_t blocks = (B * L * L + kGenTok - 1) / kGenTok;
+  if (blocks == 0) return TOPS_OK;
+  const size_t lds = (size_t)2 * kGenTok * C * sizeof(float);
+#define TOPS_GEN_OUT(TT)                                                                                        hipLaunchKernelGGL((tmu_generic_out_kernel<TT>), dim3((unsigned)blocks), dim3(256), lds, st, (const TT*)y,                      (const TT*)x, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (TT*)out, B, L, (int)C, (int)C_out, ldy, eps)
+  if (dtype == TOPS_DTYPE_BF16)
+    TOPS_GEN_OUT(__bf16);
+  else if (dtype == TOPS_DTYPE_F16)
+    TOPS_GEN_OUT(_Float16);
+  else if (dtype == TOPS_DTYPE_F32)
+    TOPS_GEN_OUT(float);
+  else
+    return fail(TOPS_EUNSUPPORTED, "tops_tmu_output_phase: unsupported dtype code %d", dtype);
+#undef TOPS_GEN_OUT
+  return launched("tops_tmu_output_phase");
 }
 
 }  // namespace tops

@@ -13,6 +13,7 @@
 //   LN(x) . W^T = rstd * (x . Wc^T - mean * sum(Wc)) + W . beta.
 #include "capi.hpp"
 #include "common.hpp"
+#include "generic.hpp"
 
 namespace tops {
 
@@ -811,13 +812,13 @@ extern "C" int tops_tmu_input_phase(const void* x, const void* mask, const void*
                                     int64_t C, int64_t C_out, int64_t ld, int transpose, float eps, int dtype,
                                     void* stream) {
   TOPS_REQUIRE(x && Wp && Wg && sWp && sWg && Bp && Bg && ab, "tops_tmu_input_phase: null pointer argument");
-  TOPS_REQUIRE(C == 128, "tops_tmu_input_phase: C must be 128 (got %lld)", (long long)C);
-  TOPS_REQUIRE(C_out == 128 || C_out == 256, "tops_tmu_input_phase: C_out must be 128 or 256 (got %lld)",
-               (long long)C_out);
   TOPS_REQUIRE(B >= 0 && L >= 0 && ld >= L && ld % 64 == 0,
                "tops_tmu_input_phase: bad sizes B=%lld L=%lld ld=%lld (ld must be a multiple of 64)", (long long)B,
                (long long)L, (long long)ld);
   TOPS_REQUIRE(B * L * (ld / 64) < (1LL << 31), "tops_tmu_input_phase: too many tokens");
+  if (C != 128 || (C_out != 128 && C_out != 256) || dtype == TOPS_DTYPE_F32)  // any-shape kernels
+    return tmu_generic_input_phase(x, mask, Wp, Wg, Bp, Bg, ab, B, L, C, C_out, ld, transpose, eps, dtype,
+                                   (hipStream_t)stream);
   (void)sWp;  // the kernel normalises x before the GEMM: the column sums of the folded weights
   (void)sWg;  // are part of the ABI (reference layout) but not needed
   hipStream_t st = (hipStream_t)stream;
@@ -836,6 +837,7 @@ extern "C" int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L
                (long long)nslab, (long long)L, (long long)ld, (long long)ldy);
   if (L == 0 || nslab == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_F32) return tmu_generic_einsum(ab, y, nslab, L, ld, ldy, dtype, st);
   if (dtype == TOPS_DTYPE_BF16) return tmu_einsum_t<__bf16>(ab, y, nslab, L, ld, ldy, st);
   if (dtype == TOPS_DTYPE_F16) return tmu_einsum_t<_Float16>(ab, y, nslab, L, ld, ldy, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_einsum: unsupported dtype code %d", dtype);
@@ -846,12 +848,12 @@ extern "C" int tops_tmu_output_phase(const void* y, const void* x, const void* W
                                      int64_t L, int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype,
                                      void* stream) {
   TOPS_REQUIRE(y && x && Wp && Wg && sWp && sWg && Bp && Bg && out, "tops_tmu_output_phase: null pointer argument");
-  TOPS_REQUIRE(C == 128 && C_out == 128, "tops_tmu_output_phase: C and C_out must be 128 (got %lld, %lld)",
-               (long long)C, (long long)C_out);
   TOPS_REQUIRE(B >= 0 && L >= 0 && ldy >= L && ldy % 64 == 0,
                "tops_tmu_output_phase: bad sizes B=%lld L=%lld ldy=%lld (ldy must be a multiple of 64)",
                (long long)B, (long long)L, (long long)ldy);
   TOPS_REQUIRE(B * L * ((L + 63) / 64) < (1LL << 31), "tops_tmu_output_phase: too many tokens");
+  if (C != 128 || C_out != 128 || dtype == TOPS_DTYPE_F32)  // any-shape kernels
+    return tmu_generic_output_phase(y, x, Wp, Wg, Bp, Bg, out, B, L, C, C_out, ldy, eps, dtype, (hipStream_t)stream);
   (void)sWg;  // x is normalised before its GEMM: the column sums of Wg_c are not needed
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)

@@ -2,6 +2,8 @@
 
 Same wrapper names, arguments and return layouts as the reference's Triton launchers
 (`triangle_mul/kernel.py:235-326`): `input_phase` returns ab as (2C, B, L, L) channel-major,
+any C and bf16 / fp16 / fp32 I/O (the library runs C = 128 in 16-bit types on the tuned
+kernels, everything else on its any-shape kernels),
 `output_phase` consumes y as (C, B, L, L) channel-major and returns (B, L, L, C).  The extra
 keyword arguments (`transpose`, `ld`, `ldy`) expose the layout options the fused `forward`
 uses; their defaults reproduce the reference layout exactly.
@@ -10,7 +12,7 @@ uses; their defaults reproduce the reference layout exactly.
 import torch
 
 from .. import _native
-from .._common.dtype import io_dtype_code
+from .._common.dtype import any_shape_dtype_code
 
 
 def _prep_weights(x, *ws):
@@ -46,7 +48,7 @@ def input_phase(
     C_out = p_in_combined.shape[0]
     trim = ld is None and L % 64 != 0
     ld = max(64, (L + 63) // 64 * 64) if ld is None else int(ld)
-    code = io_dtype_code(x.dtype)
+    code = any_shape_dtype_code(x.dtype)
     _native.check_device(x, p_in_combined, g_in_combined, mask)
     x = x if x.is_contiguous() else x.contiguous()
     Wp, Wg = _prep_weights(x, p_in_combined, g_in_combined)
@@ -94,7 +96,7 @@ def triangle_einsum(ab, L, ld, C, B):
         L,
         ld,
         ld,
-        io_dtype_code(ab.dtype),
+        any_shape_dtype_code(ab.dtype),
         _native.stream_of(ab),
     )
     return y
@@ -120,7 +122,7 @@ def output_phase(
     """
     B, L, _, C = x.shape
     C_out = p_out_combined.shape[0]
-    code = io_dtype_code(x.dtype)
+    code = any_shape_dtype_code(x.dtype)
     _native.check_device(x, y_t, p_out_combined, g_out_combined)
     x = x if x.is_contiguous() else x.contiguous()
     if ldy is None:
