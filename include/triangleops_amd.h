@@ -32,13 +32,14 @@ int tops_abi_version(void);
 /*
  * triangle_multiplicative_update, input phase.
  * Replaces `input_phase` + its Triton kernel (triangle_mul/kernel.py:235-279, :54-162).
- *   x      io   (B, L, L, C) contiguous, C == 128
+ *   x      io   (B, L, L, C) contiguous
  *   mask   int8 (B, L, L) contiguous (bool storage is accepted: 0/1), or NULL; multiplies the output
  *   Wp, Wg io   (C_out, C) LN-folded weights (out, in);  sWp, sWg, Bp, Bg fp32 (C_out,)
  *   ab     io   out[f * B*L*ld + (b*L + r)*ld + c] for f < C_out, r < L, c < ld (ld >= L, ld % 64 == 0)
  *               = sigmoid(G) * P * mask of token (b, i, j) with (i, j) = (r, c), or (c, r) when
  *               transpose != 0; positions c >= L are written as 0.
- * C_out must be 128 or 256.
+ * C == 128, C_out in {128, 256} with bf16 / fp16 I/O runs the tuned kernel; any other C <= 1024,
+ * C_out <= 4096, or fp32 I/O runs the any-shape kernel (every value fp32 with fp32 I/O).
  */
 int tops_tmu_input_phase(const void* x, const void* mask, const void* Wp, const void* Wg, const float* sWp,
                          const float* sWg, const float* Bp, const float* Bg, void* ab, int64_t B, int64_t L,
@@ -51,7 +52,7 @@ int tops_tmu_input_phase(const void* x, const void* mask, const void* Wp, const 
  * with a = ab, b = ab + nslab*L*ld, for i, j < L.  ld and ldy must be multiples of 64 and
  * the columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them); columns
  * [L, ldy) of y receive unspecified finite values.  Outgoing feeds the natural token grid,
- * incoming the transposed one (transpose=1 above).
+ * incoming the transposed one (transpose=1 above).  fp32 I/O runs an fp32 VALU product.
  */
 int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
                     void* stream);
@@ -63,6 +64,8 @@ int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t l
  *   x      io   (B, L, L, C) contiguous
  *   Wp, Wg io   (C_out, C);  sWp, sWg, Bp, Bg fp32 (C_out,)
  *   out    io   (B, L, L, C_out) contiguous = p_out(LN_out(y)) * sigmoid(g_out(LN_in(x)))
+ * C == C_out == 128 with bf16 / fp16 I/O runs the tuned kernel; other C <= 512 or fp32 I/O the
+ * any-shape kernel.
  */
 int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
                           const float* sWg, const float* Bp, const float* Bg, void* out, int64_t B, int64_t L,
@@ -160,6 +163,20 @@ int tops_tri_generic_prep(const void* x, int64_t sx0, int64_t sx1, const void* w
 int tops_tri_generic_attention(const void* q, const void* k, const void* v, const float* bias, const void* mask,
                                int64_t sm0, int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t H,
                                int64_t D, float scale, int dtype, void* stream);
+/*
+ * Any-shape attention_pair_bias (C_s, C_z, H, D other than 128, 128, 4, 32) and its fp32 I/O;
+ * replaces attn_pair_bias/kernel.py:205-257 for those shapes.
+ * tops_apb_generic_prep: q, k, v io (M, H, D) = X . W per head (wqkv as in tops_apb_forward);
+ *   bias fp32 (H, M, M) = LN(Z[q, k, :]) . W + b in the folded form (Wc fp32 (H, Cz), Bc fp32 (H,)).
+ * tops_apb_generic_attention: Og io (M, H*D) = softmax_k(scale q . k + bias, masked keys -inf) v;
+ *   mask int8 (M,) or NULL.
+ * The gate + output projection is tops_gate_out / tops_gate_out_generic.
+ */
+int tops_apb_generic_prep(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
+                          const float* Bc, void* q, void* k, void* v, float* bias, int64_t M, int64_t C, int64_t Cz,
+                          int64_t H, int64_t D, float eps, int dtype, void* stream);
+int tops_apb_generic_attention(const void* q, const void* k, const void* v, const float* bias, const void* mask,
+                               void* Og, int64_t M, int64_t H, int64_t D, float scale, int dtype, void* stream);
 int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
                           const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg,
                           const void* bg, const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2,

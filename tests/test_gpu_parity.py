@@ -339,6 +339,23 @@ def _apb_ref(inp, rows=None):
                                    mask=inp["mask"], rows=rows)
 
 
+@pytest.mark.parametrize("M,C,Cz,H,D", [(40, 96, 64, 3, 24), (130, 64, 32, 2, 64), (70, 128, 128, 8, 16)])
+@pytest.mark.parametrize("mask", ["none", "pad"])
+def test_apb_any_shape(device, M, C, Cz, H, D, mask):
+    """Shapes outside (C_s, C_z, H, D) = (128, 128, 4, 32) run the any-shape kernels (with biases)."""
+    inp = apb_inputs(M, C=C, Cz=Cz, H=H, D=D, seed=M + C, mask=mask, biases=True)
+    _check(_apb_call(inp, device), _apb_ref(inp), torch.bfloat16, f"apb any-shape M={M} C={C} Cz={Cz} H={H} D={D}")
+
+
+@pytest.mark.parametrize("M", [40, 96])
+def test_apb_fp32_io(device, M):
+    """fp32 I/O: every value fp32 (max |d| <= 1e-4)."""
+    inp = apb_inputs(M, seed=M, mask="pad", biases=True, dtype=torch.float32)
+    out = _apb_call(inp, device)
+    assert out.dtype == torch.float32
+    _check(out, _apb_ref(inp), torch.float32, f"apb fp32 M={M}")
+
+
 @pytest.mark.parametrize("M", [40, 128, 200, 512])
 @pytest.mark.parametrize("mask", ["none", "pad", "random"])
 @pytest.mark.parametrize("biases", [False, True])

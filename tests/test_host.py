@@ -148,14 +148,18 @@ def test_cpu_tensors_rejected():
         tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
 
 
-def test_fp32_io_rejected_clearly_by_apb():
-    """attention_pair_bias has no fp32 kernels: fp32 tensors raise ValueError before any launch."""
-    r = _w(dt=torch.float32)
+def test_unsupported_io_dtype_rejected_clearly():
+    """float64 I/O raises the reference's ValueError (`_common/dtype.py:19`) before any launch;
+    bf16, fp16 and fp32 are accepted."""
+    r = _w(dt=torch.float64)
     M, C, H, D = 8, 128, 4, 32
     pre = tops.attn_pair_bias.precompute(r(C, H * D), r(C, H * D), r(C, H * D), r(C), r(C), r(C, H), None, H, D)
-    with pytest.raises(ValueError, match="not supported by the gfx950 kernels"):
+    with pytest.raises(ValueError, match="unsupported IO dtype"):
         tops.attn_pair_bias.forward(r(M, C), r(M, M, C), pre, W_proj_g=r(C, C), B_proj_g=None, W_proj_o=r(C, C),
                                     B_proj_o=None)
+    pre = tops.triangle_mul.precompute(r(C), r(C), r(2 * C, C), r(2 * C, C), r(C), r(C), r(C, C), r(C, C))
+    with pytest.raises(ValueError, match="unsupported IO dtype"):
+        tops.triangle_mul.forward(r(1, 4, 4, C), pre, direction="outgoing")
 
 
 def test_missing_library_fresh_process(tmp_path):

@@ -40,6 +40,10 @@ _SIGNATURES = {
         _p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p,
     ],
     "tops_tri_generic_attention": [_p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p],
+    "tops_apb_generic_prep": [
+        _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p,
+    ],
+    "tops_apb_generic_attention": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p],
     "tops_gate_out_generic": [
         _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32,
         _p,

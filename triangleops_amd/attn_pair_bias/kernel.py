@@ -8,7 +8,7 @@ with two keyword-only additions: `mask` (an optional (M,) key mask, masked keys 
 import torch
 
 from .. import _native
-from .._common.dtype import io_dtype_code
+from .._common.dtype import any_shape_dtype_code, io_dtype_code
 
 
 def wqkv_from_interleaved(W_QKV, H, D):
@@ -29,6 +29,8 @@ def apb_forward(X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0,
     assert W_combined.shape == (H, Cz)
     assert B_const.shape == (H,)
     assert Og.shape == (M, H * D)
+    if not (C == 128 and Cz == 128 and H == 4 and D == 32) or X.dtype == torch.float32:
+        return _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm, H, D)
     code = io_dtype_code(X.dtype)
     _native.check_device(X, W_QKV, Z, W_combined, Og, mask)
     X = X if X.is_contiguous() else X.contiguous()
@@ -70,4 +72,36 @@ def apb_forward(X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0,
         code,
         _native.stream_of(X),
     )
+    return Og
+
+
+def _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm, H, D):
+    """apb_forward at any (C_s, C_z, H, D) or with fp32 I/O (tops_apb_generic_prep / _attention);
+    the Q/K/V and bias scratch is allocated here."""
+    M, C = X.shape
+    Cz = Z.shape[2]
+    code = any_shape_dtype_code(X.dtype)
+    _native.check_device(X, W_QKV, Z, W_combined, Og, mask)
+    X = X if X.is_contiguous() else X.contiguous()
+    if Z.stride(2) != 1:
+        Z = Z.contiguous()
+    if wqkv_hm is None:
+        wqkv_hm = wqkv_from_interleaved(W_QKV, H, D)
+    if wqkv_hm.dtype != X.dtype:
+        wqkv_hm = wqkv_hm.to(X.dtype)
+    wqkv_hm = wqkv_hm.contiguous()
+    Wc = W_combined.float().contiguous()
+    Bc = B_const.float().contiguous()
+    m8 = _native.mask_i8(mask)
+    if m8 is not None:
+        assert m8.numel() == M, "mask must be (M,)"
+    assert Og.is_contiguous()
+    q, k, v = (torch.empty(M, H, D, device=X.device, dtype=X.dtype) for _ in range(3))
+    bias = torch.empty(H, M, M, device=X.device, dtype=torch.float32)
+    st = _native.stream_of(X)
+    _native.call("tops_apb_generic_prep", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
+                 Wc.data_ptr(), Bc.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(), M, C, Cz, H,
+                 D, float(eps), code, st)
+    _native.call("tops_apb_generic_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
+                 _native.ptr(m8), Og.data_ptr(), M, H, D, float(scale), code, st)
     return Og

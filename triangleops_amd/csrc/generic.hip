@@ -102,17 +102,20 @@ __global__ __launch_bounds__(256) void tri_generic_prep_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention: thread = (row i, head h, query q), q fastest so a wave shares (i, h) and its K / V
-// loads are broadcasts.  DM >= D is the register length of q and o.
+// Attention over R rows of N queries and N keys: thread = (row i, head h, query q), q fastest
+// so a wave shares (i, h) and its K / V loads are broadcasts.  DM >= D is the register length
+// of q and o.  Masked keys (mask[i*sm0 + k*sm1] == 0) get "+ (-1e9)" in fp32 (triangle
+// attention) or -inf (MASK_INF, attention_pair_bias: a row without valid keys gives NaN, as
+// torch's softmax does).
 // ---------------------------------------------------------------------------------------------
-template <typename T, int DM>
+template <typename T, int DM, bool MASK_INF>
 __global__ __launch_bounds__(256) void tri_generic_attn_kernel(const T* __restrict__ qi_, const T* __restrict__ ki_,
                                                               const T* __restrict__ vi_, const float* __restrict__ bias,
                                                               const int8_t* __restrict__ mask, int64_t sm0, int64_t sm1,
-                                                              T* __restrict__ out, int64_t so0, int64_t so1, int64_t N,
-                                                              int H, int D, float scale) {
+                                                              T* __restrict__ out, int64_t so0, int64_t so1, int64_t R,
+                                                              int64_t N, int H, int D, float scale) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= N * H * N) return;
+  if (idx >= R * H * N) return;
   const int64_t q = idx % N, ih = idx / N;
   const int h = (int)(ih % H);
   const int64_t i = ih / H;
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(256) void tri_generic_attn_kernel(const T* __restri
     for (int d = 0; d < DM; ++d)
       if (d < D) s = fmaf(qv[d], (float)kp[d], s);
     s += brow[k];
-    if (mask && mask[i * sm0 + k * sm1] == 0) s += -1e9f;
+    if (mask && mask[i * sm0 + k * sm1] == 0) s = MASK_INF ? -INFINITY : s + -1e9f;
     const float mn = fmaxf(m, s);
     const float corr = __expf(m - mn), p = __expf(s - mn);
     m = mn;
@@ -221,10 +224,10 @@ static int tri_generic_attention_t(const void* q, const void* k, const void* v, 
                                    int D, float scale, hipStream_t st) {
   const int64_t blocks = (N * H * N + 255) / 256;
   if (blocks == 0) return TOPS_OK;
-#define TOPS_GEN_ATTN(DMV)                                                                                        \
-  hipLaunchKernelGGL((tri_generic_attn_kernel<T, DMV>), dim3((unsigned)blocks), dim3(256), 0, st, (const T*)q,   \
-                     (const T*)k, (const T*)v, bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, H, D, \
-                     scale)
+#define TOPS_GEN_ATTN(DMV)                                                                                           \
+  hipLaunchKernelGGL((tri_generic_attn_kernel<T, DMV, false>), dim3((unsigned)blocks), dim3(256), 0, st,            \
+                     (const T*)q, (const T*)k, (const T*)v, bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, \
+                     N, N, H, D, scale)
   if (D <= 16)
     TOPS_GEN_ATTN(16);
   else if (D <= 32)
@@ -247,6 +250,90 @@ static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* g
                      (const T*)w_ln, (const T*)b_ln, eps, apply_ln, (const T*)Wg, (const T*)bg, (const T*)Wo,
                      (const T*)bo, (T*)out, M1, M2, Cin, HD, Cout);
   return launched("tops_gate_out_generic");
+}
+
+// ---------------------------------------------------------------------------------------------
+// attention_pair_bias, any (C_s, C_z, H, D) (attn_pair_bias/kernel.py:205-257):
+//   apb_generic_qkv_kernel   per token m: q / k / v [m][h][d] = X[m] . W (rounded to the I/O type)
+//   apb_generic_bias_kernel  per pair (q, k): bias[h][q][k] = zn . Wc[h] + Bc[h], zn = (z - mean) * rstd
+//                            of z = Z[q, k, :] (the LN affine is folded into Wc / Bc)
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void apb_generic_qkv_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
+                                                             T* __restrict__ qo, T* __restrict__ ko,
+                                                             T* __restrict__ vo, int64_t M, int C, int H, int D) {
+  const int HD = H * D;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * 3 * HD) return;
+  const int64_t m = idx / (3 * HD);
+  const int f = (int)(idx % (3 * HD));  // row of the (H, 3, D, C) weight
+  const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+  const T* xr = X + m * C;
+  const T* w = wqkv + (int64_t)f * C;
+  float acc = 0.f;
+  for (int c = 0; c < C; ++c) acc = fmaf((float)xr[c], (float)w[c], acc);
+  T* dst = which == 0 ? qo : which == 1 ? ko : vo;
+  dst[m * HD + h * D + d] = (T)acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void apb_generic_bias_kernel(const T* __restrict__ Z, int64_t sz0, int64_t sz1,
+                                                              const float* __restrict__ Wc,
+                                                              const float* __restrict__ Bc, float* __restrict__ bias,
+                                                              int64_t M, int Cz, int H, float eps) {
+  extern __shared__ float zs[];  // [kGenTok][Cz]
+  const int tid = threadIdx.x;
+  const int64_t npair = M * M, p0 = (int64_t)blockIdx.x * kGenTok;
+  for (int e = tid; e < kGenTok * Cz; e += 256) {
+    const int64_t pr = p0 + e / Cz;
+    zs[e] = pr < npair ? (float)Z[(pr / M) * sz0 + (pr % M) * sz1 + e % Cz] : 0.f;
+  }
+  __syncthreads();
+  gen_layer_norm<T>(zs, Cz, Cz, nullptr, nullptr, eps);
+  __syncthreads();
+  for (int e = tid; e < kGenTok * H; e += 256) {
+    const int t = e / H, h = e % H;
+    const int64_t pr = p0 + t;
+    if (pr >= npair) continue;
+    const float* z = zs + t * Cz;
+    const float* w = Wc + (int64_t)h * Cz;
+    float acc = Bc[h];
+    for (int c = 0; c < Cz; ++c) acc = fmaf(z[c], w[c], acc);
+    bias[(int64_t)h * npair + pr] = acc;
+  }
+}
+
+template <typename T>
+static int apb_generic_prep_t(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
+                              const float* Wc, const float* Bc, void* q, void* k, void* v, float* bias, int64_t M,
+                              int C, int Cz, int H, int D, float eps, hipStream_t st) {
+  const int64_t b1 = (M * 3 * H * D + 255) / 256, b2 = (M * M + kGenTok - 1) / kGenTok;
+  if (b1 == 0) return TOPS_OK;
+  hipLaunchKernelGGL((apb_generic_qkv_kernel<T>), dim3((unsigned)b1), dim3(256), 0, st, (const T*)X,
+                     (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
+  hipLaunchKernelGGL((apb_generic_bias_kernel<T>), dim3((unsigned)b2), dim3(256), (size_t)kGenTok * Cz * sizeof(float),
+                     st, (const T*)Z, sz0, sz1, Wc, Bc, bias, M, Cz, H, eps);
+  return launched("tops_apb_generic_prep");
+}
+
+template <typename T>
+static int apb_generic_attention_t(const void* q, const void* k, const void* v, const float* bias, const void* mask,
+                                   void* Og, int64_t M, int H, int D, float scale, hipStream_t st) {
+  const int64_t blocks = (M * H + 255) / 256;
+  if (blocks == 0) return TOPS_OK;
+  const int64_t HD = (int64_t)H * D;
+#define TOPS_GEN_APB(DMV)                                                                                         \
+  hipLaunchKernelGGL((tri_generic_attn_kernel<T, DMV, true>), dim3((unsigned)blocks), dim3(256), 0, st,          \
+                     (const T*)q, (const T*)k, (const T*)v, bias, (const int8_t*)mask, 0, 1, (T*)Og, 0, HD, 1, M, \
+                     H, D, scale)
+  if (D <= 16)
+    TOPS_GEN_APB(16);
+  else if (D <= 32)
+    TOPS_GEN_APB(32);
+  else
+    TOPS_GEN_APB(64);
+#undef TOPS_GEN_APB
+  return launched("tops_apb_generic_attention");
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -494,6 +581,46 @@ extern "C" int tops_tri_generic_attention(const void* q, const void* k, const vo
   if (dtype == TOPS_DTYPE_F32)
     return tri_generic_attention_t<float>(q, k, v, bias, mask, sm0, sm1, out, so0, so1, N, (int)H, (int)D, scale, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_generic_attention: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_apb_generic_prep(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
+                                     const float* Wc, const float* Bc, void* q, void* k, void* v, float* bias,
+                                     int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float eps, int dtype,
+                                     void* stream) {
+  TOPS_REQUIRE(X && wqkv && Z && Wc && Bc && q && k && v && bias, "tops_apb_generic_prep: null pointer argument");
+  TOPS_REQUIRE(M >= 0 && M <= 65536 && C >= 1 && C <= 4096 && Cz >= 1 && Cz <= 1024 && H >= 1 && H <= 64 && D >= 1 &&
+                   D <= 64,
+               "tops_apb_generic_prep: supports C <= 4096, Cz <= 1024, H <= 64, D <= 64 (got M=%lld C=%lld Cz=%lld "
+               "H=%lld D=%lld)",
+               (long long)M, (long long)C, (long long)Cz, (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return apb_generic_prep_t<__bf16>(X, wqkv, Z, sz0, sz1, Wc, Bc, q, k, v, bias, M, (int)C, (int)Cz, (int)H, (int)D,
+                                      eps, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return apb_generic_prep_t<_Float16>(X, wqkv, Z, sz0, sz1, Wc, Bc, q, k, v, bias, M, (int)C, (int)Cz, (int)H,
+                                        (int)D, eps, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return apb_generic_prep_t<float>(X, wqkv, Z, sz0, sz1, Wc, Bc, q, k, v, bias, M, (int)C, (int)Cz, (int)H, (int)D,
+                                     eps, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_generic_prep: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_apb_generic_attention(const void* q, const void* k, const void* v, const float* bias,
+                                          const void* mask, void* Og, int64_t M, int64_t H, int64_t D, float scale,
+                                          int dtype, void* stream) {
+  TOPS_REQUIRE(q && k && v && bias && Og, "tops_apb_generic_attention: null pointer argument");
+  TOPS_REQUIRE(M >= 0 && M <= 65536 && H >= 1 && H <= 64 && D >= 1 && D <= 64,
+               "tops_apb_generic_attention: supports H <= 64, D <= 64 (got M=%lld H=%lld D=%lld)", (long long)M,
+               (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return apb_generic_attention_t<__bf16>(q, k, v, bias, mask, Og, M, (int)H, (int)D, scale, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return apb_generic_attention_t<_Float16>(q, k, v, bias, mask, Og, M, (int)H, (int)D, scale, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return apb_generic_attention_t<float>(q, k, v, bias, mask, Og, M, (int)H, (int)D, scale, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_generic_attention: unsupported dtype code %d", dtype);
 }
 
 extern "C" int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
