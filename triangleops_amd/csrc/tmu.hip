@@ -46,184 +46,179 @@ __device__ inline GridTile grid_tile_fast(uint32_t t, const FastDiv& tpr, const 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Input phase.  NW waves; wave w owns output features f = 32w + lane%32 of both P and G, with
-// its weight rows in registers as the MFMA B operand.  A block walks 64-token tiles in a
-// grid-stride loop, with two roles: waves [0, NW/2) fetch x (three tiles ahead, in a ring of
-// register stages) and waves [NW/2, NW) write the results, so neither role ever has loads and
-// stores outstanding together and the in-order memory counter waits only for the stage being
-// consumed.  The loaders normalise each token with its LayerNorm statistics (one pass, fp32,
-// packed dot products) on the way into LDS, so the GEMM yields LN(x) . Wc^T directly and the
-// epilogue is a bias add and the gate.  The A operand reads tokens in a permuted order so
-// that D = x . W^T leaves 16 consecutive tokens of one feature in each lane; the gated result
-// goes through a feature-major LDS tile and every store instruction writes whole 128-byte
-// rows (8 features x 64 tokens) of the channel-major output.
+// Input phase.  64-token tiles (64 consecutive positions c of one row r of the (B, L, ld)
+// store grid), 8 waves in two roles:
+//   waves 0-3 (loaders) fetch x four tiles ahead (16 lanes per 256-byte token row; positions
+//   c >= L reload position L - 1 and get mask 0, so every fetch issues the same loads), take
+//   each token's LayerNorm statistics (two-pass, fp32) and stage the normalised tile and the
+//   mask in LDS (double-buffered);
+//   waves 4 .. 4 + NWR - 1 (writers, NWR = C_out / 32) each own 32 output features: P and G weight rows in
+//   registers as the MFMA B operand, D = x . W^T with the A operand read in a permuted token
+//   order so each lane ends up with 16 consecutive tokens of one feature, the bias add, gate
+//   and mask in the epilogue, and a private feature-major LDS tile that the same wave stores
+//   with whole 128-byte rows (8 features x 64 tokens per store instruction).
+// No wave has loads and stores in flight together; one barrier per tile, and the loaders'
+// LayerNorm of tile n + 1 overlaps the writers' GEMM of tile n.  The LN affine is folded into
+// the weights, so the GEMM of the normalised x gives LN(x) . W^T directly.
 // ---------------------------------------------------------------------------------------------
-template <typename T, int C, int NW>
-__global__ __launch_bounds__(NW * 64) void tmu_in_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
-                                                        const T* __restrict__ Wp, const T* __restrict__ Wg,
-                                                        const float* __restrict__ Bp, const float* __restrict__ Bg,
-                                                        T* __restrict__ ab, int64_t L, int64_t ld, int64_t fstride,
-                                                        int transpose, float eps, uint32_t ntiles, FastDiv tpr,
-                                                        FastDiv Ld) {
-  constexpr int NT = NW * 64;
-  constexpr int NL = NT / 2;          // loader threads
-  constexpr int TPT = NL / 64;        // loader threads per token
-  constexpr int CPT = (C / 8) / TPT;  // 16-byte chunks per loader thread
-  constexpr int ROW = C * 2;          // LDS bytes per token row
-  constexpr int KS = C / 16;          // MFMA k-steps
-  constexpr int PD = 3;               // register stages in flight
-  static_assert(CPT * TPT * 8 == C, "channel split");
+template <typename T, int NWR>
+__global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
+                                                    const T* __restrict__ Wp, const T* __restrict__ Wg,
+                                                    const float* __restrict__ Bp, const float* __restrict__ Bg,
+                                                    T* __restrict__ ab, int64_t L, int64_t ld, int64_t fstride,
+                                                    int transpose, float eps, uint32_t ntiles, FastDiv tpr,
+                                                    FastDiv Ld) {
+  constexpr int C = 128, ROW = C * 2, KS = C / 16, FW = 32;
+  constexpr int PD = 4;  // loader register stages in flight
   using V8 = vec<T, 8>;
-  using V2 = vec<T, 2>;
 
-  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x tile
+  __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x tiles
   __shared__ __attribute__((aligned(16))) float smask[2][64];
-  __shared__ __attribute__((aligned(16))) T os[NW * 32 * 64];  // gated tile, [feature][token]
+  __shared__ __attribute__((aligned(16))) T os[NWR][FW * 64];   // per writer wave: [feature][token]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, col = lane & 31;
-  const int f = wave * 32 + col;
-
-  V8 wp[KS], wg[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    wp[s] = ldg<V8>(Wp + (int64_t)f * C + 16 * s + 8 * hl);
-    wg[s] = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
-  }
-  const float cbp = Bp[f], cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
-
-  // token of MFMA row r: 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3), so D slot v of lane
-  // half hl is token 16 hl + v of the 32-token sub-tile
-  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
-  // GEMMs + gate of one staged tile -> feature-major LDS tile (all waves)
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int tok = sub * 32 + prow;
-      f32x16 accP = {}, accG = {};
-#pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const V8 xa = *reinterpret_cast<const V8*>(&xs[buf][tok * ROW + (((2 * k + hl) ^ (tok & 7)) << 4)]);
-        accP = Mma<T>::m32(xa, wp[k], accP);
-        accG = Mma<T>::m32(xa, wg[k], accG);
-      }
-      const int tb = sub * 32 + 16 * hl;  // first of this lane's 16 tokens
-      V8 o[2];
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const f32x4 rm = *reinterpret_cast<const f32x4*>(&smask[buf][tb + 4 * gq]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int v = 4 * gq + j;
-          const float P = accP[v] + cbp;
-          const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
-          o[v / 8][v % 8] = (T)(P * gate * rm[j]);
-        }
-      }
-      // 16-byte chunks c = tb / 8 + {0, 1} of feature row f, XOR-swizzled by (f >> 1) & 7
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int c = tb / 8 + h;
-        *reinterpret_cast<V8*>(&os[f * 64 + ((c ^ ((f >> 1) & 7)) << 3)]) = o[h];
-      }
-    }
-  };
-
+  // LDS chunk swizzle of a 256-byte token row: distinct for the 16 rows a fragment read touches
+  // (the permuted order below visits rows {0-3, 16-19, 4-7, 20-23} + 8 per lane half)
+  auto key = [](int t) { return (t & 7) | ((t >> 1) & 8); };
   const uint32_t G = gridDim.x;
   uint32_t t = blockIdx.x;
-  if (wave < NW / 2) {
+
+  if (wave < 4) {
     // ================= loaders =================
-    const int my_tok = tid / TPT, my_part = tid % TPT;
+    const int ch = tid & 15, tq = tid >> 4;  // 16-byte chunk ch of tokens 16 k + tq, k < 4
     struct Stage {
-      V8 x[CPT];
-      int mb;   // raw mask byte and position flag, combined when the stage is consumed so
-      bool ok;  // the fetch itself never waits for its loads
+      V8 x[4];
+      int mb[4];  // raw mask bytes, converted when the stage is consumed
     };
-    // Every fetch issues the same loads (past the end it reloads the last tile; positions
-    // c >= L read token L - 1 and get mask 0), keeping the memory-counter accounting exact.
     auto fetch = [&](uint32_t tt, Stage& sg) {
       tt = tt < ntiles ? tt : ntiles - 1;
       const GridTile g = grid_tile_fast(tt, tpr, Ld);
-      int64_t c = g.c0 + my_tok;
-      const bool ok = c < L;
-      c = ok ? c : L - 1;
-      const int64_t i = transpose ? c : g.r, j = transpose ? g.r : c;
-      const int64_t tok = (g.b * L + i) * L + j;
-      const T* src = x + tok * C + my_part * CPT * 8;
 #pragma unroll
-      for (int e = 0; e < CPT; ++e) sg.x[e] = ldg<V8>(src + 8 * e);
-      sg.mb = *(mask ? mask + tok : reinterpret_cast<const int8_t*>(x));
-      sg.ok = ok;
-    };
-    auto step = [&](uint32_t tt, int buf, Stage& sg) {
-      // LayerNorm of this thread's token (sum and sum of squares in fp32) -> LDS
-      float s1 = 0.f, s2 = 0.f;
-      const V2 one = {(T)1.f, (T)1.f};
-#pragma unroll
-      for (int e = 0; e < CPT; ++e)
-#pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-          const V2 pr = {sg.x[e][k], sg.x[e][k + 1]};
-          s1 = Mma<T>::dot2(pr, one, s1);
-          s2 = Mma<T>::dot2(pr, pr, s2);
-        }
-      const float mean = group_sum<TPT>(s1) * (1.0f / C);
-      const float var = fmaxf(group_sum<TPT>(s2) * (1.0f / C) - mean * mean, 0.f);
-      const float rstd = rsqrtf(var + eps), shift = -mean * rstd;
-#pragma unroll
-      for (int e = 0; e < CPT; ++e) {
-        V8 h;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) h[k] = (T)((float)sg.x[e][k] * rstd + shift);
-        const int chunk = my_part * CPT + e;
-        *reinterpret_cast<V8*>(&xs[buf][my_tok * ROW + ((chunk ^ (my_tok & 7)) << 4)]) = h;
+      for (int k = 0; k < 4; ++k) {
+        int64_t c = g.c0 + 16 * k + tq;
+        c = c < L ? c : L - 1;
+        const int64_t i = transpose ? c : g.r, j = transpose ? g.r : c;
+        const int64_t tok = (g.b * L + i) * L + j;
+        sg.x[k] = ldg<V8>(x + tok * C + 8 * ch);
+        sg.mb[k] = *(mask ? mask + tok : reinterpret_cast<const int8_t*>(x));
       }
-      // every thread of the token stores the same value: no divergent branch in the loop (it
-      // would make the compiler wait for all outstanding loads at the loop head)
-      smask[buf][my_tok] = sg.ok ? (mask ? (float)sg.mb : 1.f) : 0.f;
-      __syncthreads();
-      fetch(tt + PD * G, sg);  // refill this stage
-      compute(buf);
-      __syncthreads();
     };
-    int buf = 0;
-    Stage s0, s1, s2;
+    auto step = [&](uint32_t tt, int bb, Stage& sg) {
+      const GridTile g = grid_tile_fast(tt, tpr, Ld);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int tk = 16 * k + tq;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)sg.x[k][e];
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+        const float mean = group_sum<16>(s) * (1.0f / C);
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+        const float rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+        V8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (T)((v[e] - mean) * rstd);
+        *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ key(tk)) << 4)]) = o;
+        // every lane of the token stores the same value: no divergent branch in the loop
+        smask[bb][tk] = g.c0 + tk < L ? (mask ? (float)(sg.mb[k] != 0) : 1.f) : 0.f;
+      }
+      __syncthreads();  // tile tt staged; the writers are done with the tile before tt - 1
+      fetch(tt + PD * G, sg);  // refill this stage
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    const int bb = 0;
+    Stage s0, s1, s2, s3;
     fetch(t, s0);
     __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
     fetch(t + G, s1);
     __builtin_amdgcn_sched_barrier(0);
     fetch(t + 2 * G, s2);
     __builtin_amdgcn_sched_barrier(0);
+    fetch(t + 3 * G, s3);
+    __builtin_amdgcn_sched_barrier(0);
     // block-uniform trip count (barriers match the writers'); the remainder runs after the
     // loop so that its back edge is the only way to the loop head (a break out of the
     // unrolled body would merge into the latch and make the compiler wait for every load)
     uint32_t n = t < ntiles ? (ntiles - t + G - 1) / G : 0;
-    for (; n >= 3; n -= 3, t += 3 * G) {
-      step(t, buf, s0);
-      step(t + G, buf ^ 1, s1);
-      step(t + 2 * G, buf, s2);
-      buf ^= 1;
+    for (; n >= 4; n -= 4, t += 4 * G) {
+      step(t, bb, s0);
+      step(t + G, bb ^ 1, s1);
+      step(t + 2 * G, bb, s2);
+      step(t + 3 * G, bb ^ 1, s3);
     }
-    if (n > 0) step(t, buf, s0);
-    if (n > 1) step(t + G, buf ^ 1, s1);
+    if (n > 0) step(t, bb, s0);
+    if (n > 1) step(t + G, bb ^ 1, s1);
+    if (n > 2) step(t + 2 * G, bb, s2);
   } else {
-    // ================= writers =================
-    const int wt = tid - NL;
-    int buf = 0;
+    // ================= writers: wave 4 + w owns features [32 w, 32 w + 32) =================
+    const int w = wave - 4, hl = lane >> 5, col = lane & 31;
+    const int f0 = w * FW;
+    V8 wp[KS], wg[KS];
+    const int f = f0 + col;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      wp[s] = ldg<V8>(Wp + (int64_t)f * C + 16 * s + 8 * hl);
+      wg[s] = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
+    }
+    const float cbp = Bp[f], cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
+    // token of MFMA row r: 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3), so D slot v of lane
+    // half hl is token 16 hl + v of the 32-token sub-tile
+    const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+    T* ow = os[w];
+    int bb = 0;
     for (; t < ntiles; t += G) {
-      __syncthreads();  // tile staged by the loaders
-      compute(buf);
-      __syncthreads();  // feature-major tile complete
+      __syncthreads();  // tile t staged
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int tok = sub * 32 + prow;
+        const int tb = sub * 32 + 16 * hl;  // first of this lane's 16 tokens
+        {
+          f32x16 accP = {}, accG = {};
+#pragma unroll
+          for (int k = 0; k < KS; ++k) {
+            const V8 xa = *reinterpret_cast<const V8*>(&xs[bb][tok * ROW + (((2 * k + hl) ^ key(tok)) << 4)]);
+            accP = Mma<T>::m32(xa, wp[k], accP);
+            accG = Mma<T>::m32(xa, wg[k], accG);
+          }
+          V8 o[2];
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            const f32x4 rm = *reinterpret_cast<const f32x4*>(&smask[bb][tb + 4 * gq]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int v = 4 * gq + j;
+              const float P = accP[v] + cbp;
+              const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+              o[v / 8][v % 8] = (T)(P * gate * rm[j]);
+            }
+          }
+          // 16-byte chunks c = tb / 8 + {0, 1} of local feature row ff, XOR-swizzled by (ff >> 1) & 7
+          const int ff = col;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int c = tb / 8 + h;
+            *reinterpret_cast<V8*>(&ow[ff * 64 + ((c ^ ((ff >> 1) & 7)) << 3)]) = o[h];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one sub-tile's accumulators live at a time
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       const GridTile g = grid_tile_fast(t, tpr, Ld);
       const int64_t rowoff = (g.b * L + g.r) * ld + g.c0;
 #pragma unroll
-      for (int k = 0; k < NW * 32 * 8 / NL; ++k) {
-        const int ci = k * NL + wt;  // chunk index: feature ci / 8, chunk ci % 8
+      for (int q = 0; q < FW / 8; ++q) {
+        const int ci = q * 64 + lane;  // chunk index: local feature ci / 8, chunk ci % 8
         const int ff = ci >> 3, c = ci & 7;
-        const V8 v = *reinterpret_cast<const V8*>(&os[ff * 64 + ((c ^ ((ff >> 1) & 7)) << 3)]);
-        stg<V8>(ab + (int64_t)ff * fstride + rowoff + 8 * c, v);
+        const V8 v = *reinterpret_cast<const V8*>(&ow[ff * 64 + ((c ^ ((ff >> 1) & 7)) << 3)]);
+        stg<V8>(ab + (int64_t)(f0 + ff) * fstride + rowoff + 8 * c, v);
       }
-      buf ^= 1;
+      bb ^= 1;
     }
   }
 }
@@ -757,15 +752,14 @@ static int tmu_input_phase_t(const void* x, const void* mask, const void* Wp, co
   const int64_t fstride = B * L * ld;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
   const FastDiv tdiv((uint32_t)tpr), ldiv((uint32_t)L);
-  if (C_out == 256) {
-    hipLaunchKernelGGL((tmu_in_kernel<T, 128, 8>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)x,
+  if (C_out == 256)
+    hipLaunchKernelGGL((tmu_in_kernel<T, 8>), dim3((unsigned)grid), dim3(768), 0, st, (const T*)x,
                        (const int8_t*)mask, (const T*)Wp, (const T*)Wg, Bp, Bg, (T*)ab, L, ld, fstride, transpose, eps,
                        (uint32_t)ntiles, tdiv, ldiv);
-  } else {
-    hipLaunchKernelGGL((tmu_in_kernel<T, 128, 4>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)x,
+  else
+    hipLaunchKernelGGL((tmu_in_kernel<T, 4>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)x,
                        (const int8_t*)mask, (const T*)Wp, (const T*)Wg, Bp, Bg, (T*)ab, L, ld, fstride, transpose, eps,
                        (uint32_t)ntiles, tdiv, ldiv);
-  }
   return launched("tops_tmu_input_phase");
 }
 
