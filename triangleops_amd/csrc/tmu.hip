@@ -544,112 +544,48 @@ __global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Output phase (C = C_out = 128).  8 waves; wave w computes features [32 (w & 3), +32) for the
-// 32 tokens [32 (w >> 2), +32) of a 64-token tile with its Wp / Wg rows in registers (rows
-// permuted so each lane ends up with 16 consecutive features of one token).  Roles as in the
-// input phase: waves 0-3 fetch y and x two tiles ahead, waves 4-7 write the output.
+// Output phase (C = C_out = 128).  64-token tiles, 12 waves in two roles:
+//   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
-//   registers (4 channels x 8 tokens per thread) into a token-major LDS tile; its LN
-//   statistics are taken from LDS by the waves that use them and applied in the epilogue.
-//   x (token-major) is normalised on the way into LDS.
-//   The gated result goes through a token-major LDS tile: whole 256-byte output rows per store.
+//   registers (4 channels x 8 tokens per thread) into a token-major tile; x (token-major) is
+//   normalised on the way in (16 lanes per token, two-pass statistics);
+//   waves 4-11 (writers) compute features [32 (w & 3), +32) for the 32 tokens [32 (w >> 2), +32)
+//   (w = wave - 4) with their Wp / Wg rows in registers (rows permuted so each lane ends up with
+//   16 consecutive features of one token), take the LN statistics of y from LDS and apply them
+//   in the epilogue, and write a token-major output tile (double-buffered); tile n is stored,
+//   whole 256-byte rows per 16 lanes, after the barrier of tile n + 1, when every writer has
+//   finished it.  One barrier per tile.
 // ---------------------------------------------------------------------------------------------
-template <typename T, int C, int COUT>
-__global__ __launch_bounds__(512) void tmu_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
+template <typename T>
+__global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
                                                      const T* __restrict__ Wp, const T* __restrict__ Wg,
                                                      const float* __restrict__ sWp, const float* __restrict__ Bp,
                                                      const float* __restrict__ Bg, T* __restrict__ out, int64_t L,
                                                      int64_t ldy, int64_t cstride, float eps, uint32_t ntiles,
                                                      FastDiv tpr, FastDiv Ld) {
-  static_assert(C == 128 && COUT == 128, "tmu_out_kernel is specialised for C = C_out = 128");
+  constexpr int C = 128, COUT = 128;
   constexpr int ROW = C * 2;  // LDS bytes per token row (16 chunks of 16 bytes)
   constexpr int KS = C / 16;
-  constexpr int NL = 256;  // loader threads (waves 0-3); writers are waves 4-7
-  constexpr int PD = 2;    // register stages in flight
+  constexpr int NL = 256;  // loader threads (waves 0-3); the writers are the other 512
+  constexpr int PD = 3;    // loader register stages in flight
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
   using V2 = vec<T, 2>;
 
   __shared__ __attribute__((aligned(16))) char ys[2][64 * ROW];  // raw y, token-major
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x
-  __shared__ __attribute__((aligned(16))) T os[64 * COUT];       // gated output, token-major
+  __shared__ __attribute__((aligned(16))) T os[2][64 * COUT];    // gated output, token-major
   __shared__ __attribute__((aligned(16))) float cst[3][COUT];    // sum(Wp_c), Bp, -log2(e) Bg
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hl = lane >> 5, col = lane & 31;
-  const int fset = wave & 3, sub = wave >> 2;
-
-  for (int i = tid; i < COUT; i += 512) {
+  for (int i = tid; i < COUT; i += 768) {
     cst[0][i] = sWp[i];
     cst[1][i] = Bp[i];
     cst[2][i] = -kLog2e * Bg[i];
   }
-  // A operand row r = col holds feature 32 fset + prow: D slot v of lane half hl is then
-  // feature 32 fset + 16 hl + v
-  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
-  V8 wp[KS], wg[KS];
-  {
-    const int64_t frow = (int64_t)(32 * fset + prow) * C;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      wp[s] = ldg<V8>(Wp + frow + 16 * s + 8 * hl);
-      wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
-    }
-  }
   __syncthreads();  // cst
 
   auto yswz = [](int t) { return (t ^ (t >> 3)) & 7; };
-  // GEMMs, y statistics and gate of one staged tile -> token-major LDS output tile (all waves)
-  auto compute = [&](int buf) {
-    const int tok = 32 * sub + col;
-    const char* yrow = &ys[buf][tok * ROW];
-    const char* xrow = &xs[buf][tok * ROW];
-    f32x16 accP = {}, accG = {};
-#pragma unroll
-    for (int k = 0; k < KS; ++k) {
-      accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
-      accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(xrow + (((2 * k + hl) ^ (tok & 7)) << 4)), accG);
-    }
-    // LN statistics of y for this token: this lane sums chunks [8 hl, 8 hl + 8), its partner the rest
-    float s1 = 0.f, s2 = 0.f;
-    {
-      const V2 one = {(T)1.f, (T)1.f};
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const V8 v = *reinterpret_cast<const V8*>(yrow + (((8 * hl + c) ^ yswz(tok)) << 4));
-#pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-          const V2 pr = {v[k], v[k + 1]};
-          s1 = Mma<T>::dot2(pr, one, s1);
-          s2 = Mma<T>::dot2(pr, pr, s2);
-        }
-      }
-    }
-    const float mean = halves_sum(s1) * (1.0f / C);
-    const float var = fmaxf(halves_sum(s2) * (1.0f / C) - mean * mean, 0.f);
-    const float ra = rsqrtf(var + eps), rb = -mean * ra;
-    const int f0 = 32 * fset + 16 * hl;
-    V8 o[2];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const f32x4 cs = *reinterpret_cast<const f32x4*>(&cst[0][f0 + 4 * q]);
-      const f32x4 cb = *reinterpret_cast<const f32x4*>(&cst[1][f0 + 4 * q]);
-      const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int v = 4 * q + j;
-        const float P = fmaf(accP[v], ra, fmaf(rb, cs[j], cb[j]));
-        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cg[j])));
-        o[v / 8][v % 8] = (T)(P * gate);
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = f0 / 8 + h;
-      *reinterpret_cast<V8*>(&os[tok * COUT + ((c ^ (tok & 15)) << 3)]) = o[h];
-    }
-  };
-
   const uint32_t G = gridDim.x;
   uint32_t t = blockIdx.x;
   if (wave < 4) {
@@ -674,71 +610,147 @@ __global__ __launch_bounds__(512) void tmu_out_kernel(const T* __restrict__ y, c
         sg.x[k] = ldg<V8>(x + (rowbase * L + j) * C + 8 * (ci & 15));
       }
     };
-    auto step = [&](uint32_t tt, int buf, Stage& sg) {
-      // x: normalise (16 lanes per token) -> LDS
+    auto step = [&](int bb, Stage& sg, uint32_t tnext) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 4; ++k) {  // x: LayerNorm (16 lanes per token) -> LDS
         const int ci = k * NL + tid, xt = ci >> 4, ch = ci & 15;
-        float s1 = 0.f, s2 = 0.f;
-        const V2 one = {(T)1.f, (T)1.f};
+        float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const V2 pr = {sg.x[k][e], sg.x[k][e + 1]};
-          s1 = Mma<T>::dot2(pr, one, s1);
-          s2 = Mma<T>::dot2(pr, pr, s2);
-        }
-        const float mean = group_sum<16>(s1) * (1.0f / C);
-        const float var = fmaxf(group_sum<16>(s2) * (1.0f / C) - mean * mean, 0.f);
-        const float rstd = rsqrtf(var + eps), shift = -mean * rstd;
+        for (int e = 0; e < 8; ++e) v[e] = (float)sg.x[k][e];
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+        const float mean = group_sum<16>(s) * (1.0f / C);
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+        const float rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
         V8 h;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = (T)((float)sg.x[k][e] * rstd + shift);
-        *reinterpret_cast<V8*>(&xs[buf][xt * ROW + ((ch ^ (xt & 7)) << 4)]) = h;
+        for (int e = 0; e < 8; ++e) h[e] = (T)((v[e] - mean) * rstd);
+        *reinterpret_cast<V8*>(&xs[bb][xt * ROW + ((ch ^ (xt & 15)) << 4)]) = h;
       }
-      // y: 4 x 8 register transpose -> token-major rows (8 bytes = 4 channels per write)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 8; ++e) {  // y: 4 x 8 register transpose -> token-major rows
         const int tk = 8 * tg + e;
         const V4 q4 = {sg.y[0][e], sg.y[1][e], sg.y[2][e], sg.y[3][e]};
-        *reinterpret_cast<V4*>(&ys[buf][tk * ROW + (((cq >> 1) ^ yswz(tk)) << 4) + ((cq & 1) << 3)]) = q4;
+        *reinterpret_cast<V4*>(&ys[bb][tk * ROW + (((cq >> 1) ^ yswz(tk)) << 4) + ((cq & 1) << 3)]) = q4;
       }
-      __syncthreads();
-      fetch(tt + PD * G, sg);  // refill this stage
-      compute(buf);
-      __syncthreads();
+      __syncthreads();  // tile staged
+      fetch(tnext, sg);  // refill this stage
+      __builtin_amdgcn_sched_barrier(0);
     };
-    int buf = 0;
-    Stage s0, s1;
+    const int bb = 0;
+    Stage s0, s1, s2;
     fetch(t, s0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the stages' loads in issue order
     fetch(t + G, s1);
-    for (; t < ntiles; t += 2 * G) {  // block-uniform trip count: barriers match the writers
-      step(t, buf, s0);
-      buf ^= 1;
-      if (t + G >= ntiles) break;
-      step(t + G, buf, s1);
-      buf ^= 1;
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(t + 2 * G, s2);
+    __builtin_amdgcn_sched_barrier(0);
+    // block-uniform trip count (barriers match the writers'); step k uses stage k % 3 and
+    // buffer k % 2, so the loop runs rounds of six steps and the remainder follows it (the back
+    // edge stays the only way to the loop head)
+    uint32_t n = t < ntiles ? (ntiles - t + G - 1) / G : 0;
+    for (; n >= 6; n -= 6, t += 6 * G) {
+      step(bb, s0, t + 3 * G);
+      step(bb ^ 1, s1, t + 4 * G);
+      step(bb, s2, t + 5 * G);
+      step(bb ^ 1, s0, t + 6 * G);
+      step(bb, s1, t + 7 * G);
+      step(bb ^ 1, s2, t + 8 * G);
     }
+    if (n > 0) step(bb, s0, t + 3 * G);
+    if (n > 1) step(bb ^ 1, s1, t + 4 * G);
+    if (n > 2) step(bb, s2, t + 5 * G);
+    if (n > 3) step(bb ^ 1, s0, t + 6 * G);
+    if (n > 4) step(bb, s1, t + 7 * G);
+    __syncthreads();  // the writers' final store waits for this
   } else {
     // ================= writers =================
-    const int wt = tid - NL;
-    int buf = 0;
-    for (; t < ntiles; t += G) {
-      __syncthreads();  // tile staged by the loaders
-      compute(buf);
-      __syncthreads();  // output tile complete
-      const GridTile g = grid_tile_fast(t, tpr, Ld);
+    const int w = wave - 4, hl = lane >> 5, col = lane & 31;
+    const int fset = w & 3, sub = w >> 2;
+    // A operand row r = col holds feature 32 fset + prow: D slot v of lane half hl is then
+    // feature 32 fset + 16 hl + v
+    const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+    V8 wp[KS], wg[KS];
+    {
+      const int64_t frow = (int64_t)(32 * fset + prow) * C;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        wp[s] = ldg<V8>(Wp + frow + 16 * s + 8 * hl);
+        wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+      }
+    }
+    const int wt = tid - NL;  // store role: 16-byte chunks wt and 512 + wt of the output tile
+    auto store = [&](uint32_t tt, int ob) {
+      const GridTile g = grid_tile_fast(tt, tpr, Ld);
       const int64_t tok0 = (g.b * L + g.r) * L + g.c0;
 #pragma unroll
-      for (int k = 0; k < 64 * COUT / 8 / NL; ++k) {
-        const int ci = k * NL + wt;  // token ci / 16, chunk ci % 16
+      for (int k = 0; k < 2; ++k) {
+        const int ci = k * 512 + wt;  // token ci / 16, chunk ci % 16
         const int tk = ci >> 4, c = ci & 15;
         if (g.c0 + tk < L) {
-          const V8 v = *reinterpret_cast<const V8*>(&os[tk * COUT + ((c ^ (tk & 15)) << 3)]);
+          const V8 v = *reinterpret_cast<const V8*>(&os[ob][tk * COUT + ((c ^ (tk & 15)) << 3)]);
           stg<V8>(out + (tok0 + tk) * COUT + 8 * c, v);
         }
       }
-      buf ^= 1;
+    };
+    int bb = 0;
+    for (; t < ntiles; t += G) {
+      __syncthreads();  // tile t staged; every writer has finished tile t - G
+      const int tok = 32 * sub + col;
+      const char* yrow = &ys[bb][tok * ROW];
+      const char* xrow = &xs[bb][tok * ROW];
+      f32x16 accP = {}, accG = {};
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
+        accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(xrow + (((2 * k + hl) ^ (tok & 15)) << 4)), accG);
+      }
+      // LN statistics of y for this token: this lane sums chunks [8 hl, 8 hl + 8), its partner the rest
+      float s1 = 0.f, s2 = 0.f;
+      {
+        const V2 one = {(T)1.f, (T)1.f};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const V8 v = *reinterpret_cast<const V8*>(yrow + (((8 * hl + c) ^ yswz(tok)) << 4));
+#pragma unroll
+          for (int k = 0; k < 8; k += 2) {
+            const V2 pr = {v[k], v[k + 1]};
+            s1 = Mma<T>::dot2(pr, one, s1);
+            s2 = Mma<T>::dot2(pr, pr, s2);
+          }
+        }
+      }
+      const float mean = halves_sum(s1) * (1.0f / C);
+      const float var = fmaxf(halves_sum(s2) * (1.0f / C) - mean * mean, 0.f);
+      const float ra = rsqrtf(var + eps), rb = -mean * ra;
+      const int f0 = 32 * fset + 16 * hl;
+      V8 o[2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 cs = *reinterpret_cast<const f32x4*>(&cst[0][f0 + 4 * q]);
+        const f32x4 cb = *reinterpret_cast<const f32x4*>(&cst[1][f0 + 4 * q]);
+        const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int v = 4 * q + j;
+          const float P = fmaf(accP[v], ra, fmaf(rb, cs[j], cb[j]));
+          const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cg[j])));
+          o[v / 8][v % 8] = (T)(P * gate);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = f0 / 8 + h;
+        *reinterpret_cast<V8*>(&os[bb][tok * COUT + ((c ^ (tok & 15)) << 3)]) = o[h];
+      }
+      if (t >= (uint32_t)blockIdx.x + G) store(t - G, bb ^ 1);  // previous tile, complete since the barrier
+      bb ^= 1;
     }
+    __syncthreads();  // the last tile is complete
+    if (t >= (uint32_t)blockIdx.x + G) store(t - G, bb ^ 1);
   }
 }
 
@@ -791,7 +803,7 @@ static int tmu_output_phase_t(const void* y, const void* x, const void* Wp, cons
   const int64_t cstride = B * L * ldy;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
   const FastDiv tdiv((uint32_t)tpr), ldiv((uint32_t)L);
-  hipLaunchKernelGGL((tmu_out_kernel<T, 128, 128>), dim3((unsigned)grid), dim3(512), 0, st, (const T*)y, (const T*)x,
+  hipLaunchKernelGGL((tmu_out_kernel<T>), dim3((unsigned)grid), dim3(768), 0, st, (const T*)y, (const T*)x,
                      (const T*)Wp, (const T*)Wg, sWp, Bp, Bg, (T*)out, L, ldy, cstride, eps, (uint32_t)ntiles, tdiv,
                      ldiv);
   return launched("tops_tmu_output_phase");
