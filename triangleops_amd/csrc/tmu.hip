@@ -11,6 +11,8 @@
 // launchers) and triangle_mul/module.py:80-84 (einsum).  The LayerNorm affines are folded
 // into the weights at precompute time exactly as in _common/ln_absorption.py:28-44:
 //   LN(x) . W^T = rstd * (x . Wc^T - mean * sum(Wc)) + W . beta.
+#include <type_traits>
+
 #include "capi.hpp"
 #include "common.hpp"
 #include "generic.hpp"
@@ -374,26 +376,36 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------
-// Einsum, large L: 256 x 256 block tile, 4 waves (one per SIMD) of 128 x 128, k-tile 32.
-// Accumulators (256 registers per lane) live in the accumulation registers, which leaves room
-// for two register stages of global loads (each k-tile is fetched two tiles before it is
-// stored to LDS) and two fragment sets.  LDS holds three k-tiles: tile kt + 1 is stored at the
-// start of iteration kt into the buffer last read at kt - 2, one barrier in mid-iteration
-// publishes it, and the fragments of its first k-step are read during the second k-step of
-// tile kt, so the MFMA stream never waits on a barrier.  64-byte LDS rows (4 chunks): A rows
-// are swizzled by (row >> 2) & 3, B rows (read in the permuted order) by
-// ((row >> 2) & 1) | ((row >> 3) & 2): 16 lanes of a fragment read hit 16 distinct chunks.
+// Einsum, large L: 256 x 256 block tile, 4 waves of 128 x 128 (accumulators in AGPRs), k-tile 64,
+// operands copied from HBM / L2 straight into LDS with global_load_lds (no staging registers, no
+// LDS store instructions), double-buffered.  One load instruction fills 1 KB of LDS in lane order
+// and covers 8 rows x 128 bytes, i.e. 8 whole cache lines: a footprint of half lines (k-tile 32)
+// halves the rate at which L2 feeds LDS and leaves the loop load-bound.  Each lane fetches the
+// 16-byte chunk that belongs at its LDS position under the fragment reads' XOR swizzle.
+// Per k-tile kt (stage kt % 2): k-steps 0-2 run with the next k-step's fragments read alongside;
+// then each wave waits for its loads of tile kt + 1 and for its fragment reads, and the block meets
+// at one barrier; after it the loads of tile kt + 2 go into the stage just drained, and k-step 3
+// runs with tile kt + 1's first fragments read alongside.  The waits and the barrier are written
+// out explicitly (the compiler's fence before a barrier would wait for every load in flight), and
+// the loads are inline asm, so the compiler adds no waits of its own for them.
+// The k order of each block is rotated by 2 (tm + tn) k-tiles: the blocks that share an A row block
+// (same tm) or a B row block (same tn) run side by side on one XCD and would otherwise request each
+// line together, all waiting out the same HBM miss; staggered, the first request's miss turns into
+// L2 hits for the others.  The fp32 accumulation order differs between blocks accordingly.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+__global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
                                                          T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
                                                          int64_t nslab, int tiles) {
-  constexpr int BM = 256, BK = 32, MI = 4, NJ = 4;
-  constexpr int TILE = BM * BK;  // elements of one operand's k-tile
+  constexpr int BM = 256, BK = 64, MI = 4, NJ = 4;
+  constexpr int TILE = BM * BK;  // elements of one operand's k-tile (32 KB)
   using V8 = vec<T, 8>;
 
-  __shared__ __attribute__((aligned(16))) T As[3][TILE];
-  __shared__ __attribute__((aligned(16))) T Bs[3][TILE];
+  // one LDS object per stage and operand (static stage indices: the k-loop is unrolled by two)
+  __shared__ __attribute__((aligned(16))) T As0[TILE], As1[TILE];
+  __shared__ __attribute__((aligned(16))) T Bs0[TILE], Bs1[TILE];
+  auto abuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? As0 : As1; };
+  auto bbuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? Bs0 : Bs1; };
 
   const int64_t total = nslab * tiles * tiles;
   int64_t id = blockIdx.x;
@@ -406,53 +418,64 @@ __global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ 
   const T* Bb = Bmat + slab * L * ld;
   T* Yb = Y + slab * L * ldy;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, col = lane & 31;
   const int wm = wave & 1, wn = wave >> 1;
   const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
 
-  auto swa = [](int row, int c) { return row * BK + ((c ^ ((row >> 2) & 3)) << 3); };
-  auto swb = [](int row, int c) { return row * BK + ((c ^ (((row >> 2) & 1) | ((row >> 3) & 2))) << 3); };
+  // LDS rows are 128 bytes (8 chunks of 16); physical chunk = logical chunk ^ swz(row).  A fragment
+  // reads cover 16 consecutive rows per 16 lanes, B fragment reads the rows prow() picks: both
+  // swizzles put the 16 lanes of each group on 16 distinct 16-byte bank groups.
+  auto swa = [](int row) { return (row >> 1) & 7; };
+  auto swb = [](int row) { return ((row >> 1) & 3) | ((row >> 2) & 4); };
 
-  // loader: thread -> chunk lc of rows lr + 64 r (r < 4) of both operands
-  const int lc = tid & 3, lr = tid >> 2;
+  // loads: wave w, instruction j < 8 fills LDS bytes [(8 w + j) KB, +1 KB) of an operand's tile,
+  // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + lane / 8, physical chunk lane % 8
+  // <- logical chunk (lane % 8) ^ swz(r).  Rows past L reload row L - 1 (their products are never
+  // stored).
   const int nk = (int)(ld / BK);
-  const T* arow[4];
-  const T* brow[4];
+  const char* abase = reinterpret_cast<const char*>(Ab + (int64_t)tm * BM * ld);
+  const char* bbase = reinterpret_cast<const char*>(Bb + (int64_t)tn * BM * ld);
+  uint32_t aoff[8], boff[8];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    int64_t ra = (int64_t)tm * BM + lr + 64 * r, rb = (int64_t)tn * BM + lr + 64 * r;
-    ra = ra < L ? ra : L - 1;
-    rb = rb < L ? rb : L - 1;
-    arow[r] = Ab + ra * ld + 8 * lc;
-    brow[r] = Bb + rb * ld + 8 * lc;
+  for (int j = 0; j < 8; ++j) {
+    const int r = 8 * (8 * wave + j) + (lane >> 3), cp = lane & 7;
+    const int ra = (int64_t)tm * BM + r < L ? r : (int)(L - 1 - (int64_t)tm * BM);
+    const int rb = (int64_t)tn * BM + r < L ? r : (int)(L - 1 - (int64_t)tn * BM);
+    aoff[j] = (uint32_t)((ra * ld + 8 * (cp ^ swa(r))) * (int64_t)sizeof(T));
+    boff[j] = (uint32_t)((rb * ld + 8 * (cp ^ swb(r))) * (int64_t)sizeof(T));
   }
-  struct Stage {
-    V8 a[4], b[4];
-  };
-  auto gload = [&](int kt, Stage& sg) {
-    kt = kt < nk ? kt : nk - 1;  // past the end: reload the last tile (stored, never read)
+  const int kofs = (int)(((int64_t)(tm + tn) * 2) % nk);
+  auto gload = [&](int kt, auto S) {  // k-tile kt of this block's rotated order
+    kt += kofs;
+    if (kt >= nk) kt -= nk;
+    const char* ak = abase + (int64_t)kt * BK * sizeof(T);
+    const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
+    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 8 * 1024);
+    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 8 * 1024);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sg.a[r] = ldg<V8>(arow[r] + kt * BK);
-      sg.b[r] = ldg<V8>(brow[r] + kt * BK);
-    }
-  };
-  auto sstore = [&](int buf, const Stage& sg) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      *reinterpret_cast<V8*>(&As[buf][swa(lr + 64 * r, lc)]) = sg.a[r];
-      *reinterpret_cast<V8*>(&Bs[buf][swb(lr + 64 * r, lc)]) = sg.b[r];
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t va = aoff[j], vb = boff[j], ma = as + 1024 * j, mb = bs + 1024 * j;
+      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
+      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
     }
   };
   struct Frags {
     V8 a[MI], b[NJ];
   };
-  auto frags = [&](int buf, int ks, Frags& f) {
+  auto frags = [&](auto S, int ks, Frags& f) {
+    const T* as = abuf(S);
+    const T* bs = bbuf(S);
 #pragma unroll
-    for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(&As[buf][swa(wm * 128 + 32 * i + col, 2 * ks + hl)]);
+    for (int i = 0; i < MI; ++i) {
+      const int row = wm * 128 + 32 * i + col;
+      f.a[i] = *reinterpret_cast<const V8*>(&as[row * BK + (((2 * ks + hl) ^ swa(row)) << 3)]);
+    }
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) f.b[j] = *reinterpret_cast<const V8*>(&Bs[buf][swb(wn * 128 + 32 * j + prow, 2 * ks + hl)]);
+    for (int j = 0; j < NJ; ++j) {
+      const int row = wn * 128 + 32 * j + prow;
+      f.b[j] = *reinterpret_cast<const V8*>(&bs[row * BK + (((2 * ks + hl) ^ swb(row)) << 3)]);
+    }
   };
 
   f32x16 acc[NJ][MI];
@@ -466,32 +489,7 @@ __global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < MI; ++i) acc[j][i] = Mma<T>::m32(f.b[j], f.a[i], acc[j][i]);
   };
-
-  // iteration kt: store tile kt + 1 (stage sn) and refill sn with tile kt + 3; k-step 0 of
-  // tile kt with the fragments of k-step 1 read alongside; barrier; k-step 1 with the
-  // fragments of k-step 0 of tile kt + 1 read alongside.
-  // The memory instructions are spread one per MFMA so that a single wave keeps its SIMD's
-  // matrix core fed while they issue (and while a store waits for its global load).
-  auto iter = [&](int kt, int b0, int b1, Stage& sn, Frags& f0, Frags& f1) {
-    mfmas(f0);
-    frags(b0, 1, f1);
-    sstore(b1, sn);
-    gload(kt + 3, sn);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-    }
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);  // the k-step's MFMAs issue before the barrier
-    __syncthreads();
-    mfmas(f1);
-    frags(b1, 0, f0);
+  auto interleave = [] {
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
@@ -501,34 +499,50 @@ __global__ __launch_bounds__(256) void tmu_einsum4_kernel(const T* __restrict__ 
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  Stage s0, s1;
   Frags fa, fb;
-  gload(0, s0);
-  gload(1, s1);
-  sstore(0, s0);
-  gload(2, s0);
-  __syncthreads();
-  frags(0, 0, fa);
-  // buffers rotate 0, 1, 2; tile kt lives in buffer kt % 3, its successor in (kt + 1) % 3
-  int b0 = 0, b1 = 1, b2 = 2;
-  for (int kt = 0; kt < nk; kt += 2) {  // nk is even (ld % 64 == 0)
-    iter(kt, b0, b1, s1, fa, fb);
-    iter(kt + 1, b1, b2, s0, fa, fb);
-    const int t = b0;
-    b0 = b2;
-    b2 = b1;
-    b1 = t;
+  auto tile = [&](int kt, auto S) {
+    using N = std::integral_constant<int, 1 - decltype(S)::value>;
+    mfmas(fa);
+    frags(S, 1, fb);
+    interleave();
+    mfmas(fb);
+    frags(S, 2, fa);
+    interleave();
+    mfmas(fa);
+    frags(S, 3, fb);
+    interleave();
+    // tile kt + 1 complete for this wave, this wave's reads of stage S done; then the block barrier
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 2 < nk) gload(kt + 2, S);
+    mfmas(fb);
+    frags(N{}, 0, fa);  // past the last tile: reads stage N's stale contents, never used
+    interleave();
+  };
+
+  gload(0, std::integral_constant<int, 0>{});
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // tile 0 in LDS
+  if (1 < nk) gload(1, std::integral_constant<int, 1>{});
+  frags(std::integral_constant<int, 0>{}, 0, fa);
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    tile(kt, std::integral_constant<int, 0>{});
+    tile(kt + 1, std::integral_constant<int, 1>{});
   }
-  // b0..b2 rotation: after kt, kt+1 the next even tile kt+2 lives in old b2, kt+3 in old b0
+  if (kt < nk) tile(kt, std::integral_constant<int, 0>{});
 
   // ---- Y[i][j0 .. j0 + 15] per lane: two 16-byte stores (columns [L, ldy) get finite filler) ----
+  // (lane coordinates recomputed from an opaque copy of the thread index, so they are not kept
+  // live across the k-loop)
+  unsigned t2 = threadIdx.x;
+  asm volatile("" : "+v"(t2));
+  const int ecol = (int)(t2 & 31), ehl = (int)((t2 >> 5) & 1);
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
-    const int64_t ii = (int64_t)tm * BM + wm * 128 + i * 32 + col;
+    const int64_t ii = (int64_t)tm * BM + wm * 128 + i * 32 + ecol;
     if (ii < L) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * hl;
+        const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * ehl;
         if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
         V8 o0, o1;
 #pragma unroll
@@ -782,7 +796,7 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
   if (L > 384) {
     const int t = (int)((L + 255) / 256);
     const int64_t grid = nslab * t * t;
-    hipLaunchKernelGGL((tmu_einsum4_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld, ldy,
+    hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld, ldy,
                        nslab, t);
   } else {
     const int t = (int)((L + 127) / 128);
