@@ -388,10 +388,6 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 // runs with tile kt + 1's first fragments read alongside.  The waits and the barrier are written
 // out explicitly (the compiler's fence before a barrier would wait for every load in flight), and
 // the loads are inline asm, so the compiler adds no waits of its own for them.
-// The k order of each block is rotated by 2 (tm + tn) k-tiles: the blocks that share an A row block
-// (same tm) or a B row block (same tn) run side by side on one XCD and would otherwise request each
-// line together, all waiting out the same HBM miss; staggered, the first request's miss turns into
-// L2 hits for the others.  The fp32 accumulation order differs between blocks accordingly.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
@@ -445,10 +441,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
     aoff[j] = (uint32_t)((ra * ld + 8 * (cp ^ swa(r))) * (int64_t)sizeof(T));
     boff[j] = (uint32_t)((rb * ld + 8 * (cp ^ swb(r))) * (int64_t)sizeof(T));
   }
-  const int kofs = (int)(((int64_t)(tm + tn) * 2) % nk);
-  auto gload = [&](int kt, auto S) {  // k-tile kt of this block's rotated order
-    kt += kofs;
-    if (kt >= nk) kt -= nk;
+  auto gload = [&](int kt, auto S) {
     const char* ak = abase + (int64_t)kt * BK * sizeof(T);
     const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
     const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 8 * 1024);
