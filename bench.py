@@ -15,7 +15,7 @@ Prints ONE JSON line with the contract fields plus:
   kernels       the same figures for each kernel of the step;
   torch_path_ms the reference's pure-torch bf16 formulation on the same GPU;
   cpu_baseline  the fp32 CPU oracle on this host (one full outgoing call at the same size).
-`--sweep FILE` additionally times all three ops at sizes 128..2048 (ours, the torch path and
+`--sweep FILE` additionally times all three ops and the apb qk-norm variant at sizes 128..2048 (ours, the torch path and
 per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
 """
 
@@ -37,7 +37,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 import triangleops_amd as tops  # noqa: E402
-from triangleops_amd.attn_pair_bias.kernel import apb_forward  # noqa: E402
+from triangleops_amd.attn_pair_bias.kernel import apb_forward, apb_forward_qkv, apb_qkn_prep  # noqa: E402
 from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, prep_forward  # noqa: E402
 from triangleops_amd.triangle_mul.kernel import input_phase, output_phase, triangle_einsum  # noqa: E402
 
@@ -125,6 +125,15 @@ def apb_inputs(M, seed=0):
     return d
 
 
+def apb_qkn_params(seed=0):
+    """Q bias and qk-norm affine parameters of the qk-norm variant (benchmarks/references.py:230-250)."""
+    g = _gen(seed + 7)
+    p = dict(b_q=0.5 * torch.randn(H * D, generator=g), qkn_w_q=1 + 0.2 * torch.randn(H * D, generator=g),
+             qkn_b_q=0.2 * torch.randn(H * D, generator=g), qkn_w_k=1 + 0.2 * torch.randn(H * D, generator=g),
+             qkn_b_k=0.2 * torch.randn(H * D, generator=g))
+    return {k: v.to(torch.bfloat16) for k, v in p.items()}
+
+
 def to_dev(d, dev):
     return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
 
@@ -177,6 +186,23 @@ def torch_apb(d, eps=1e-5):
     o = torch.matmul(torch.softmax(scores, -1), v).permute(1, 0, 2).reshape(M, H * D)
     g = torch.sigmoid(F.linear(X, d["W_proj_g"], d["B_proj_g"]))
     return F.linear(g * o, d["W_proj_o"], d["B_proj_o"])
+
+
+def torch_apb_qknorm(d, p, eps=1e-5):
+    """benchmarks/references.py:258-277 in bf16 (the key mask fill keeps the scores' dtype)."""
+    X, Z = d["X"], d["Z"]
+    M = X.shape[0]
+    q = F.layer_norm(X @ d["WQ"] + p["b_q"], (H * D,), p["qkn_w_q"], p["qkn_b_q"], eps=eps)
+    k = F.layer_norm(X @ d["WK"], (H * D,), p["qkn_w_k"], p["qkn_b_k"], eps=eps)
+    q = q.reshape(M, H, D).permute(1, 0, 2)
+    k = k.reshape(M, H, D).permute(1, 2, 0).contiguous()
+    v = (X @ d["WV"]).reshape(M, H, D).permute(1, 0, 2).contiguous()
+    bp = (F.layer_norm(Z, (C,), d["W_ln"], d["B_ln"], eps=eps) @ d["W_proj_z"] + d["B_proj_z"]).permute(2, 0, 1)
+    scores = torch.matmul((q * D**-0.5).contiguous(), k) + bp
+    scores = scores.masked_fill(~d["mask"][None, None, :], float("-inf"))
+    o = torch.matmul(torch.softmax(scores, -1), v).permute(1, 0, 2).reshape(M, H * D)
+    g = torch.sigmoid(F.linear(X, d["W_proj_g"]))
+    return F.linear(g * o, d["W_proj_o"])
 
 
 # --------------------------------------------------------------------------- #
@@ -315,6 +341,30 @@ def apb_work(M):
     return {"apb_attention": ("hbm", 2 * M * M * C), "apb_gate_out": ("hbm", 3 * 2 * M * C)}
 
 
+def apb_qkn_phases(d, pre, p):
+    st = {}
+    M = d["X"].shape[0]
+
+    def p_prep():
+        st["qkv"] = apb_qkn_prep(d["X"], pre["wqkv_hm"], p["b_q"],
+                                 (p["qkn_w_q"], p["qkn_b_q"], p["qkn_w_k"], p["qkn_b_k"]))
+
+    def p_att():
+        st["og"] = torch.empty(M, H * D, device=d["X"].device, dtype=d["X"].dtype)
+        apb_forward_qkv(*st["qkv"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], st["og"],
+                        scale=D**-0.5, mask=d["mask"])
+
+    def p_gate():
+        st["out"] = gate_out_forward(st["og"].view(M, 1, H * D), d["X"], d["W_proj_g"], None, d["W_proj_o"], None)
+
+    return [p_prep, p_att, p_gate]
+
+
+def apb_qkn_work(M):
+    return {"apb_qkn_prep": ("hbm", 2 * M * C + 3 * 2 * M * H * D), "apb_attention": ("hbm", 2 * M * M * C),
+            "apb_gate_out": ("hbm", 3 * 2 * M * C)}
+
+
 def run_phases(phase_lists, names, iters, warmup):
     """Times the phase lists (one list per call in a step); returns (avg ms per phase name)."""
     for _ in range(warmup):
@@ -411,7 +461,22 @@ def sweep(path, sizes, dev):
             f.write(json.dumps(r) + "\n")
             f.flush()
             rows.append(r)
-            del d, pre
+            # the qk-norm variant on the same inputs (Q bias, LN over H*D of Q and K, key mask)
+            p = to_dev(apb_qkn_params(), dev)
+            fwd = lambda: tops.attn_pair_bias.forward_qknorm(  # noqa: E731
+                d["X"], d["Z"], pre, b_q=p["b_q"], qkn_w_q=p["qkn_w_q"], qkn_b_q=p["qkn_b_q"], qkn_w_k=p["qkn_w_k"],
+                qkn_b_k=p["qkn_b_k"], key_mask=d["mask"], scale=D**-0.5, W_proj_g=d["W_proj_g"],
+                W_proj_o=d["W_proj_o"])
+            ms = time_ms(fwd, 20, 5)
+            tms = time_ms(lambda: torch_apb_qknorm(d, p), 10, 2)
+            ph = run_phases([apb_qkn_phases(d, pre, p)], list(apb_qkn_work(M)), 20, 5)
+            kern = {n: kernel_entry(n, ph[n], *apb_qkn_work(M)[n]) for n in ph}
+            r = {"op": "attention_pair_bias_qknorm", "size": M, "ms": round(ms, 4), "calls_per_s": round(1e3 / ms, 1),
+                 "torch_path_ms": round(tms, 4), "kernels": kern}
+            f.write(json.dumps(r) + "\n")
+            f.flush()
+            rows.append(r)
+            del d, pre, p
     return rows
 
 

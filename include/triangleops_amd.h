@@ -132,12 +132,38 @@ int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, int6
  *   Wc     fp32 (H, Cz) LN-folded bias weight;  sWc, Bc fp32 (H,)
  *   mask   int8 (M,) key mask (nonzero = valid) or NULL; masked keys get -inf
  *   Og     io   (M, H*D) contiguous: softmax_k(scale * Q.K + LN(Z[q,k]) . W + b) V
- *   work   device scratch of tops_apb_workspace_bytes(M, H, D) bytes (caller-owned)
+ *   work   device scratch of tops_apb_workspace_bytes(M, H, D) bytes (caller-owned): the
+ *          projected Q / K / V (3 * M * 128 * 2 bytes) and the split partials
  */
 int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D);
 int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
                      const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M, int64_t C,
                      int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
+
+/*
+ * Q / K / V pre-pass and the attention with given Q / K / V.  tops_apb_forward is the two run
+ * back to back (Q scaled by `scale` in the pre-pass, Q / K / V at the head of `work`).  They also
+ * serve the qk-norm variant of attention_pair_bias (the K-Fold formulation the reference states
+ * in benchmarks/references.py:230-277 as `torch_attn_pair_bias_qknorm`; the reference has no
+ * kernel for it, so these entry points replace that torch function).
+ * tops_apb_qkn_prep, any C, H, D with C + 3*H*D <= 2040, io bf16 / fp16 / fp32:
+ *   X      io   (M, C) contiguous;  wqkv io (H, 3, D, C) as in tops_apb_forward
+ *   bq     io   (H*D,) Q bias or NULL
+ *   qkn    1: q and k are LayerNormed over the full H*D channel (eps) with affine
+ *           gq / bqn (for q) and gk / bkn (for k), io (H*D,) each or NULL (= 1 / 0)
+ *   q,k,v  io   (M, H*D) contiguous: qscale * LN(X.Wq + bq), LN(X.Wk), X.Wv (fp32 accumulation,
+ *               one rounding)
+ * tops_apb_forward_qkv, the tuned shape (H*D == Cz == 128, H == 4, D == 32), bf16 / fp16: as
+ *   tops_apb_forward with Q, K, V (M, H*D) contiguous taken as they are: Og = softmax_k(scale *
+ *   q.k + LN(Z[q,k]) . W + b, masked keys -inf) v;  work as for tops_apb_forward.
+ */
+int tops_apb_qkn_prep(const void* X, const void* wqkv, const void* bq, int qkn, const void* gq, const void* bqn,
+                      const void* gk, const void* bkn, void* q, void* k, void* v, int64_t M, int64_t C, int64_t H,
+                      int64_t D, float qscale, float eps, int dtype, void* stream);
+int tops_apb_forward_qkv(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0, int64_t sz1,
+                         const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og, void* work,
+                         int64_t M, int64_t HD, int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype,
+                         void* stream);
 
 /*
  * Any-shape triangle attention (C_in, H, D other than 128, 4, 32; e.g. the D = 16, C_in = 64

@@ -153,3 +153,39 @@ def attention_pair_bias(X, WQ, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj
         g = [_sig(z) for z in _lin(X[q], Wg, Bg)]
         out.append(_lin([g[c] * o[c] for c in range(len(o))], Wo, Bo))
     return out
+
+
+def attention_pair_bias_qknorm(X, WQ, b_q, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj_g, W_proj_o, H, D, *,
+                               qkn_w_q=None, qkn_b_q=None, qkn_w_k=None, qkn_b_k=None, key_mask=None, scale=1.0,
+                               eps=1e-5):
+    """Loop restatement of benchmarks/references.py:230-277 (per token, per head, per key)."""
+    X, WQ, WK, WV, Z = _l(X), _l(WQ), _l(WK), _l(WV), _l(Z)
+    W_ln, B_ln, Wz, Bz = _l(W_ln), _l(B_ln), _l(W_proj_z), _l(B_proj_z)
+    Wg, Wo, mask, bq = _l(W_proj_g), _l(W_proj_o), _l(key_mask), _l(b_q)
+    gq, bqn, gk, bkn = _l(qkn_w_q), _l(qkn_b_q), _l(qkn_w_k), _l(qkn_b_k)
+    M, HD = len(X), H * D
+    qv = [_matvec_in_out(X[m], WQ) for m in range(M)]
+    if bq is not None:
+        qv = [[qv[m][c] + bq[c] for c in range(HD)] for m in range(M)]
+    kv = [_matvec_in_out(X[m], WK) for m in range(M)]
+    vv = [_matvec_in_out(X[m], WV) for m in range(M)]
+    if gq is not None:  # one LayerNorm over all H*D channels of each token's q and k
+        qv = [_ln(qv[m], gq, bqn, eps) for m in range(M)]
+        kv = [_ln(kv[m], gk, bkn, eps) for m in range(M)]
+    out = []
+    for q in range(M):
+        zb = [_matvec_in_out(_ln(Z[q][k], W_ln, B_ln, eps), Wz) for k in range(M)]
+        o = []
+        for h in range(H):
+            sc = []
+            for k in range(M):
+                s = sum(qv[q][h * D + d] * scale * kv[k][h * D + d] for d in range(D)) + zb[k][h]
+                s += Bz[h] if Bz is not None else 0.0
+                if mask is not None and not mask[k]:
+                    s = -math.inf
+                sc.append(s)
+            p = _softmax_weights(sc)
+            o.extend(sum(p[k] * vv[k][h * D + d] for k in range(M)) for d in range(D))
+        g = [_sig(z) for z in _lin(X[q], Wg)]
+        out.append(_lin([g[c] * o[c] for c in range(len(o))], Wo))
+    return out

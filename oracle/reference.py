@@ -19,6 +19,9 @@ Reference files followed (paths relative to the reference repository root):
 * `benchmarks/references.py:143-171`  attention_pair_bias, plus the optional
   key mask semantics of `benchmarks/references.py:273-274` (masked keys are
   filled with -inf before the softmax).
+* `benchmarks/references.py:230-277`  attention_pair_bias_qknorm (the K-Fold
+  variant: Q bias, optional LayerNorm over the full H*D channel of Q and K
+  before the head split, key mask, bias-free gate and output projections).
 
 How each function is pinned (tests/test_oracle.py):
 * every op is compared with the pure-Python loop restatement in
@@ -56,6 +59,8 @@ __all__ = [
     "apb_attention_core",
     "apb_gate_out",
     "attention_pair_bias",
+    "apb_qknorm_qkv",
+    "attention_pair_bias_qknorm",
 ]
 
 
@@ -241,4 +246,44 @@ def attention_pair_bias(X, WQ, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj
         bias = apb_bias(Z, W_ln, B_ln, W_proj_z, B_proj_z, eps, dtype, r)
         o = apb_attention_core(X, WQ, WK, WV, bias, H, D, scale, mask, dtype, r)
         outs.append(apb_gate_out(o, _f(X, dtype)[r], W_proj_g, B_proj_g, W_proj_o, B_proj_o, dtype))
+    return torch.cat(outs, 0)
+
+
+def apb_qknorm_qkv(X, WQ, b_q, WK, WV, H, D, qkn_w_q=None, qkn_b_q=None, qkn_w_k=None, qkn_b_k=None, eps=1e-5,
+                   dtype=torch.float32):
+    """q = X WQ + b_q, k = X WK, v = X WV (M, H*D); with qkn_w_q given, q and k are LayerNormed over
+    the full H*D channel with (qkn_w_q, qkn_b_q) / (qkn_w_k, qkn_b_k) before the head split
+    (references.py:258-264)."""
+    X = _f(X, dtype)
+    q = X @ _f(WQ, dtype)
+    if b_q is not None:
+        q = q + _f(b_q, dtype)
+    k = X @ _f(WK, dtype)
+    v = X @ _f(WV, dtype)
+    if qkn_w_q is not None:
+        q = F.layer_norm(q, (H * D,), _f(qkn_w_q, dtype), _f(qkn_b_q, dtype), eps=eps)
+        k = F.layer_norm(k, (H * D,), _f(qkn_w_k, dtype), _f(qkn_b_k, dtype), eps=eps)
+    return q, k, v
+
+
+def attention_pair_bias_qknorm(X, WQ, b_q, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj_g, W_proj_o, H, D, *,
+                               qkn_w_q=None, qkn_b_q=None, qkn_w_k=None, qkn_b_k=None, key_mask=None, scale=1.0,
+                               eps=1e-5, dtype=torch.float32, rows=None, chunk=256):
+    """Whole K-Fold variant (references.py:230-277).  X (M, C_s), Z (M, M, C_z) -> (M, C_out);
+    gate sigmoid(X W_g^T) and output projection without biases."""
+    M = X.shape[0]
+    q, k, v = apb_qknorm_qkv(X, WQ, b_q, WK, WV, H, D, qkn_w_q, qkn_b_q, qkn_w_k, qkn_b_k, eps, dtype)
+    kh = k.reshape(M, H, D).permute(1, 0, 2)
+    vh = v.reshape(M, H, D).permute(1, 0, 2)
+    rows = torch.arange(M) if rows is None else torch.as_tensor(rows)
+    outs = []
+    for s in range(0, len(rows), chunk):
+        r = rows[s : s + chunk]
+        bias = apb_bias(Z, W_ln, B_ln, W_proj_z, B_proj_z, eps, dtype, r)
+        qh = q[r].reshape(len(r), H, D).permute(1, 0, 2)
+        scores = torch.matmul(qh * scale, kh.transpose(-1, -2)) + bias
+        if key_mask is not None:
+            scores = scores.masked_fill(~(_f(key_mask, dtype) != 0)[None, None, :], float("-inf"))
+        o = torch.matmul(torch.softmax(scores, -1), vh).permute(1, 0, 2).reshape(len(r), H * D)
+        outs.append(apb_gate_out(o, _f(X, dtype)[r], W_proj_g, None, W_proj_o, None, dtype))
     return torch.cat(outs, 0)

@@ -113,6 +113,22 @@ def apb_inputs(M, *, C=128, Cz=128, H=4, D=32, seed=0, dtype=torch.bfloat16, mas
                 B_proj_g=B_pg, W_proj_o=W_po, B_proj_o=B_po, H=H, D=D, scale=D**-0.5, mask=m)
 
 
+def apb_qkn_inputs(M, *, C=128, Cz=128, H=4, D=32, seed=0, dtype=torch.bfloat16, mask="pad", qkn=True):
+    """Inputs of the qk-norm variant (benchmarks/references.py:230-250): apb_inputs plus a Q bias and
+    the qk-norm affine parameters (None when qkn is False); the gate / output projections are
+    bias-free, and the key mask goes by `key_mask`."""
+    d = apb_inputs(M, C=C, Cz=Cz, H=H, D=D, seed=seed, dtype=dtype, mask=mask, biases=True)
+    g = _g(seed + 1000)
+    HD = H * D
+    d["b_q"] = (0.5 * torch.randn(HD, generator=g)).to(dtype)
+    for name, base in (("qkn_w_q", 1.0), ("qkn_b_q", 0.0), ("qkn_w_k", 1.0), ("qkn_b_k", 0.0)):
+        d[name] = (base + 0.2 * torch.randn(HD, generator=g)).to(dtype) if qkn else None
+    d["key_mask"] = d.pop("mask")
+    for k in ("B_proj_g", "B_proj_o"):
+        d.pop(k)
+    return d
+
+
 def to_dev(d, device):
     if isinstance(d, dict):
         return {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in d.items()}

@@ -9,7 +9,8 @@ Large configurations are checked on a sample of output rows (rows are independen
 
 import pytest
 import torch
-from _inputs import TOL_COS, TOL_MAX_ABS, apb_inputs, compare, pad_pair_mask, tmu_inputs, to_dev, tri_inputs
+from _inputs import (TOL_COS, TOL_MAX_ABS, apb_inputs, apb_qkn_inputs, compare, pad_pair_mask, tmu_inputs, to_dev,
+                     tri_inputs)
 
 import triangleops_amd as tops
 from oracle import reference as ref
@@ -387,6 +388,74 @@ def test_apb_config_sizes_sampled_rows(device, M):
     out = _apb_call(inp, device)
     rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
     _check(out[rows].cpu(), _apb_ref(inp, rows=rows), torch.bfloat16, f"apb M={M}")
+
+
+# --------------------------------------------------------------------------- #
+# attention_pair_bias, qk-norm variant (benchmarks/references.py:230-277)
+# --------------------------------------------------------------------------- #
+_QKN_KW = ("qkn_w_q", "qkn_b_q", "qkn_w_k", "qkn_b_k", "key_mask")
+
+
+def _qkn_args(d):
+    return (d["X"], d["WQ"], d["b_q"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"], d["W_proj_z"], d["B_proj_z"],
+            d["W_proj_g"], d["W_proj_o"], d["H"], d["D"])
+
+
+def _qkn_call(inp, device):
+    d = to_dev(inp, device)
+    return tops.attn_pair_bias.attention_pair_bias_qknorm(*_qkn_args(d), scale=d["scale"], eps=1e-5,
+                                                          **{k: d[k] for k in _QKN_KW})
+
+
+def _qkn_ref(inp, rows=None):
+    return ref.attention_pair_bias_qknorm(*_qkn_args(inp), scale=inp["scale"], eps=1e-5, rows=rows,
+                                          **{k: inp[k] for k in _QKN_KW})
+
+
+@pytest.mark.parametrize("M", [40, 128, 200, 512])
+@pytest.mark.parametrize("mask", ["none", "pad", "random"])
+@pytest.mark.parametrize("qkn", [False, True])
+def test_apb_qknorm_matches_oracle(device, M, mask, qkn):
+    inp = apb_qkn_inputs(M, seed=M + 7, mask=mask, qkn=qkn)
+    _check(_qkn_call(inp, device), _qkn_ref(inp), torch.bfloat16, f"apb qk-norm M={M} mask={mask} qkn={qkn}")
+
+
+@pytest.mark.parametrize("M,C,Cz,H,D", [(40, 96, 64, 3, 24), (130, 64, 32, 2, 64), (70, 128, 128, 8, 16)])
+def test_apb_qknorm_any_shape(device, M, C, Cz, H, D):
+    inp = apb_qkn_inputs(M, C=C, Cz=Cz, H=H, D=D, seed=M + C, mask="pad")
+    _check(_qkn_call(inp, device), _qkn_ref(inp), torch.bfloat16, f"apb qk-norm any-shape M={M} C={C} H={H} D={D}")
+
+
+@pytest.mark.parametrize("M", [40, 96])
+def test_apb_qknorm_fp32_io(device, M):
+    inp = apb_qkn_inputs(M, seed=M, mask="pad", dtype=torch.float32)
+    out = _qkn_call(inp, device)
+    assert out.dtype == torch.float32
+    _check(out, _qkn_ref(inp), torch.float32, f"apb qk-norm fp32 M={M}")
+
+
+def test_apb_qknorm_fp16(device):
+    inp = apb_qkn_inputs(160, seed=6, mask="random", dtype=torch.float16)
+    _check(_qkn_call(inp, device), _qkn_ref(inp), torch.float16, "apb qk-norm fp16")
+
+
+def test_apb_qknorm_precompute_forward_matches_oneshot(device):
+    d = to_dev(apb_qkn_inputs(256, seed=2, mask="pad"), device)
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], d["H"], d["D"])
+    a = tops.attn_pair_bias.forward_qknorm(d["X"], d["Z"], pre, b_q=d["b_q"], scale=d["scale"],
+                                           W_proj_g=d["W_proj_g"], W_proj_o=d["W_proj_o"],
+                                           **{k: d[k] for k in _QKN_KW})
+    b = _qkn_call(d, device)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1024, 2048])
+def test_apb_qknorm_config_sizes_sampled_rows(device, M):
+    inp = apb_qkn_inputs(M, seed=0, mask="pad")
+    out = _qkn_call(inp, device)
+    rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
+    _check(out[rows].cpu(), _qkn_ref(inp, rows=rows), torch.bfloat16, f"apb qk-norm M={M}")
 
 
 # --------------------------------------------------------------------------- #

@@ -43,6 +43,10 @@ REF_SIGNATURES = {
     "attn_pair_bias.precompute": "WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D",
     "attn_pair_bias.forward": "X, Z, pre, *, scale=1.0, eps=1e-05, W_proj_g, B_proj_g, W_proj_o, B_proj_o",
     "attn_pair_bias.apb_forward": "X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0, eps=1e-05",
+    # the qk-norm variant, stated by the reference only as a torch function
+    # (benchmarks/references.py:230-250, `torch_attn_pair_bias_qknorm`)
+    "attn_pair_bias.attention_pair_bias_qknorm": "X, WQ, b_q, WK, WV, Z, W_ln, B_ln, W_proj_z, B_proj_z, W_proj_g, "
+    "W_proj_o, H, D, *, qkn_w_q=None, qkn_b_q=None, qkn_w_k=None, qkn_b_k=None, key_mask=None, scale=1.0, eps=1e-05",
 }
 
 

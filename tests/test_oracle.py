@@ -132,6 +132,73 @@ def test_apb_oracle_matches_brute():
     assert _close(part, full[[0, 4]])
 
 
+def _qkn_small(seed=3):
+    d = _apb_small(seed=seed)
+    g = _g(seed + 100)
+    HD = d["H"] * d["D"]
+    r = lambda *s, sd=1.0: torch.randn(*s, generator=g, dtype=F64) * sd  # noqa: E731
+    d.update(b_q=0.5 * r(HD), qkn_w_q=1 + 0.2 * r(HD), qkn_b_q=0.2 * r(HD), qkn_w_k=1 + 0.2 * r(HD),
+             qkn_b_k=0.2 * r(HD))
+    return d
+
+
+def _qkn(d, fn=None, qkn=True, **over):
+    """Call the qk-norm variant (oracle or brute force) on the dict d with overrides."""
+    a = dict(d, **over)
+    fn = fn or (lambda *x, **k: ref.attention_pair_bias_qknorm(*x, dtype=F64, **k))
+    kw = dict(key_mask=a["mask"], scale=a["scale"])
+    if qkn:
+        kw.update(qkn_w_q=a["qkn_w_q"], qkn_b_q=a["qkn_b_q"], qkn_w_k=a["qkn_w_k"], qkn_b_k=a["qkn_b_k"])
+    return fn(a["X"], a["WQ"], a["b_q"], a["WK"], a["WV"], a["Z"], a["W_ln"], a["B_ln"], a["W_proj_z"], a["B_proj_z"],
+              a["W_proj_g"], a["W_proj_o"], a["H"], a["D"], **kw)
+
+
+@pytest.mark.parametrize("qkn", [False, True])
+def test_apb_qknorm_oracle_matches_brute(qkn):
+    d = _qkn_small()
+    for mask in (d["mask"], None):
+        got = _qkn(d, qkn=qkn, mask=mask)
+        assert _close(got, _qkn(d, fn=brute.attention_pair_bias_qknorm, qkn=qkn, mask=mask))
+    part = ref.attention_pair_bias_qknorm(d["X"], d["WQ"], d["b_q"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"],
+                                          d["W_proj_z"], d["B_proj_z"], d["W_proj_g"], d["W_proj_o"], 2, 3,
+                                          key_mask=d["mask"], scale=d["scale"], dtype=F64, rows=[0, 3], chunk=1)
+    full = ref.attention_pair_bias_qknorm(d["X"], d["WQ"], d["b_q"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"],
+                                          d["W_proj_z"], d["B_proj_z"], d["W_proj_g"], d["W_proj_o"], 2, 3,
+                                          key_mask=d["mask"], scale=d["scale"], dtype=F64)
+    assert _close(part, full[[0, 3]])
+
+
+def test_apb_qknorm_without_norm_is_apb():
+    """qk-norm off, no Q bias: the plain op with bias-free gate / output projections (pinned above)."""
+    d = _qkn_small()
+    got = _qkn(d, qkn=False, b_q=None)
+    want = ref.attention_pair_bias(d["X"], d["WQ"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                   d["B_proj_z"], d["W_proj_g"], None, d["W_proj_o"], None, 2, 3, scale=d["scale"],
+                                   mask=d["mask"], dtype=F64)
+    assert _close(got, want)
+
+
+def test_apb_qknorm_norm_spans_all_heads_after_the_bias():
+    """LN over the full H*D channel, applied after the Q bias: a constant added to every channel of
+    b_q cancels; a constant that differs between heads does not (a per-head LN would cancel it)."""
+    d = _qkn_small()
+    base = _qkn(d)
+    assert _close(base, _qkn(d, b_q=d["b_q"] + 0.7))
+    per_head = torch.cat([torch.full((3,), 0.9, dtype=F64), torch.full((3,), -0.4, dtype=F64)])
+    assert not _close(base, _qkn(d, b_q=d["b_q"] + per_head), tol=1e-4)
+    # and without the norm the same per-channel constant is not removed
+    assert not _close(_qkn(d, qkn=False), _qkn(d, qkn=False, b_q=d["b_q"] + 0.7), tol=1e-4)
+
+
+def test_apb_qknorm_key_mask_crop():
+    """Rows of the key-masked op equal the op on the cropped problem (valid keys first)."""
+    d = _qkn_small()
+    m = torch.tensor([True, True, True, False, False])
+    full = _qkn(d, mask=m)
+    crop = dict(d, X=d["X"][:3], Z=d["Z"][:3, :3], mask=None)
+    assert _close(full[:3], _qkn(crop))
+
+
 # --------------------------------------------------------------------------- #
 # golden fixtures (written by brute force at the kernels' real widths)
 # --------------------------------------------------------------------------- #

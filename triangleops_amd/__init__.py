@@ -9,6 +9,9 @@ and a one-shot `<op_name>(...)`:
     triangle_attention             LN + bias proj, Q/K/V proj + attention, then gate + W_o
     triangle_multiplicative_update LN + gated proj, triangle einsum, LN + gated proj
 
+`attn_pair_bias.attention_pair_bias_qknorm` adds the K-Fold variant the reference states only in
+torch (`benchmarks/references.py:230-277`: Q bias, LayerNorm over H*D of Q and K, key mask).
+
 All compute runs in `libtriangleops_amd.so` (HIP, gfx950) through a C ABI
 (`include/triangleops_amd.h`); there is no CPU or fallback path.
 """

@@ -105,3 +105,73 @@ def _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm
     _native.call("tops_apb_generic_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
                  _native.ptr(m8), Og.data_ptr(), M, H, D, float(scale), code, st)
     return Og
+
+
+
+def _io(t, dtype):
+    """A per-channel parameter as a contiguous vector of the I/O dtype (no copy when it already is)."""
+    return None if t is None else t.to(dtype).contiguous()
+
+
+def apb_qkn_prep(X, wqkv_hm, b_q=None, qkn=None, eps=1e-5, qscale=1.0):
+    """q = qscale * (X.Wq + b_q), k = X.Wk, v = X.Wv as (M, H*D) io tensors; with qkn = (w_q, b_q_ln,
+    w_k, b_k_ln) q and k are LayerNormed over the full H*D channel first (before the scale)
+    (benchmarks/references.py:258-264)."""
+    M, C = X.shape
+    H, three, D, C2 = wqkv_hm.shape
+    assert three == 3 and C2 == C, "wqkv_hm must be (H, 3, D, C)"
+    code = any_shape_dtype_code(X.dtype)
+    _native.check_device(X, wqkv_hm, b_q, *(qkn or ()))
+    X = X if X.is_contiguous() else X.contiguous()
+    w = wqkv_hm.to(X.dtype).contiguous()
+    bq = _io(b_q, X.dtype)
+    gq, bqn, gk, bkn = (_io(t, X.dtype) for t in (qkn or (None,) * 4))
+    for t in (bq, gq, bqn, gk, bkn):
+        assert t is None or t.numel() == H * D, "Q bias and qk-norm parameters must have H*D elements"
+    q, k, v = (torch.empty(M, H * D, device=X.device, dtype=X.dtype) for _ in range(3))
+    _native.call("tops_apb_qkn_prep", X.data_ptr(), w.data_ptr(), _native.ptr(bq), 1 if qkn is not None else 0,
+                 _native.ptr(gq), _native.ptr(bqn), _native.ptr(gk), _native.ptr(bkn), q.data_ptr(), k.data_ptr(),
+                 v.data_ptr(), M, C, H, D, float(qscale), float(eps), code, _native.stream_of(X))
+    return q, k, v
+
+
+def apb_forward_qkv(q, k, v, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0, eps=1e-5, *, mask=None):
+    """LN(Z) bias + attention into Og (M, H*D) with q, k, v (M, H*D) given (from `apb_qkn_prep`;
+    pass scale=1.0 when q is already scaled there)."""
+    M, HD = q.shape
+    H = sum_W_combined.shape[0]
+    D = HD // H
+    assert k.shape == v.shape == (M, HD) and Og.shape == (M, HD)
+    assert Z.shape[:2] == (M, M)
+    Cz = Z.shape[2]
+    assert W_combined.shape == (H, Cz) and B_const.shape == (H,)
+    m8 = _native.mask_i8(mask)
+    if m8 is not None:
+        assert m8.numel() == M, "mask must be (M,)"
+    assert Og.is_contiguous()
+    Wc, sWc, Bc = W_combined.float().contiguous(), sum_W_combined.float().contiguous(), B_const.float().contiguous()
+    q, k, v = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
+    _native.check_device(q, k, v, Z, W_combined, Og, mask)
+    st = _native.stream_of(q)
+    if HD == 128 and Cz == 128 and H == 4 and D == 32 and q.dtype != torch.float32:
+        if Z.stride(2) != 1 or Z.stride(0) % 8 or Z.stride(1) % 8:
+            Z = Z.contiguous()
+        nbytes = _native.apb_workspace_bytes(M, H, D)
+        work = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8) if nbytes else None
+        _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), Z.data_ptr(), Z.stride(0),
+                     Z.stride(1), Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), _native.ptr(m8), Og.data_ptr(),
+                     _native.ptr(work), M, HD, Cz, H, D, float(scale), float(eps), io_dtype_code(q.dtype), st)
+        return Og
+    # any shape / fp32: the generic LN(Z) bias (its own Q/K/V outputs are discarded) and attention
+    code = any_shape_dtype_code(q.dtype)
+    if Z.stride(2) != 1:
+        Z = Z.contiguous()
+    wid = torch.eye(HD, device=q.device, dtype=q.dtype).reshape(H, 1, D, HD).expand(H, 3, D, HD).contiguous()
+    scratch = torch.empty(3, M, HD, device=q.device, dtype=q.dtype)
+    bias = torch.empty(H, M, M, device=q.device, dtype=torch.float32)
+    _native.call("tops_apb_generic_prep", q.data_ptr(), wid.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
+                 Wc.data_ptr(), Bc.data_ptr(), scratch[0].data_ptr(), scratch[1].data_ptr(), scratch[2].data_ptr(),
+                 bias.data_ptr(), M, HD, Cz, H, D, float(eps), code, st)
+    _native.call("tops_apb_generic_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
+                 _native.ptr(m8), Og.data_ptr(), M, H, D, float(scale), code, st)
+    return Og

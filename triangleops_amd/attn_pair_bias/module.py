@@ -9,6 +9,14 @@ kernel, and the gate + W_o kernel.
 Additive extension: `forward(..., mask=None)` / `attention_pair_bias(..., mask=None)` take an
 optional (M,) key mask (masked keys -> -inf, as the reference's K-Fold variant does at
 `benchmarks/references.py:273-274`); without it the behaviour is the reference's.
+
+qk-norm variant: `attention_pair_bias_qknorm` has the signature of the reference's
+`torch_attn_pair_bias_qknorm` (`benchmarks/references.py:230-277`: Q bias, optional LayerNorm over
+the full H*D channel of Q and K before the head split, key mask, bias-free gate and output
+projections); `forward_qknorm` is its per-call half over the same `precompute` dict.  Three
+launches plus the gate: the Q/K/V pre-pass (Q bias, qk-norm and the softmax scale applied
+there), the LN(Z) bias + attention kernel fed with those Q/K/V (and its split combine), the
+gate + W_o kernel.
 """
 
 import torch
@@ -16,7 +24,7 @@ import torch
 from .._common.layouts import interleave_qkv, qkv_head_major
 from .._common.ln_absorption import absorb_ln_matmul
 from ..triangle_attn.kernel import gate_out_forward
-from .kernel import apb_forward
+from .kernel import apb_forward, apb_forward_qkv, apb_qkn_prep
 
 
 def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
@@ -90,4 +98,64 @@ def attention_pair_bias(
         W_proj_o=W_proj_o,
         B_proj_o=B_proj_o,
         mask=mask,
+    )
+
+
+def forward_qknorm(X, Z, pre, *, b_q=None, qkn_w_q=None, qkn_b_q=None, qkn_w_k=None, qkn_b_k=None, key_mask=None,
+                   scale=1.0, eps=1e-5, W_proj_g, W_proj_o):
+    """Per-call forward of the qk-norm variant over a `precompute` dict.  X (M, C_s), Z (M, M, C_z) ->
+    (M, C_out).  qk-norm is on when `qkn_w_q` is given (q with (qkn_w_q, qkn_b_q), k with
+    (qkn_w_k, qkn_b_k); a None weight / bias acts as 1 / 0), as in references.py:262-264."""
+    M = X.shape[0]
+    H = pre["sum_W_combined"].shape[0]
+    D = pre["W_QKV"].shape[1] // (3 * H)
+    qkn = None if qkn_w_q is None else (qkn_w_q, qkn_b_q, qkn_w_k, qkn_b_k)
+    q, k, v = apb_qkn_prep(X, pre["wqkv_hm"], b_q, qkn, eps, qscale=scale)
+    Og = torch.empty(M, H * D, device=X.device, dtype=X.dtype)
+    apb_forward_qkv(q, k, v, Z, pre["W_combined"], pre["sum_W_combined"], pre["B_const"], Og, scale=1.0, eps=eps,
+                    mask=key_mask)
+    return gate_out_forward(Og.view(M, 1, H * D), X, W_proj_g, None, W_proj_o, None).view(M, -1)
+
+
+def attention_pair_bias_qknorm(
+    X,
+    WQ,
+    b_q,
+    WK,
+    WV,
+    Z,
+    W_ln,
+    B_ln,
+    W_proj_z,
+    B_proj_z,
+    W_proj_g,
+    W_proj_o,
+    H,
+    D,
+    *,
+    qkn_w_q=None,
+    qkn_b_q=None,
+    qkn_w_k=None,
+    qkn_b_k=None,
+    key_mask=None,
+    scale=1.0,
+    eps=1e-5,
+):
+    """One-shot qk-norm variant (precompute included); arguments as the reference's
+    `torch_attn_pair_bias_qknorm` (benchmarks/references.py:230-250)."""
+    pre = precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D)
+    return forward_qknorm(
+        X,
+        Z,
+        pre,
+        b_q=b_q,
+        qkn_w_q=qkn_w_q,
+        qkn_b_q=qkn_b_q,
+        qkn_w_k=qkn_w_k,
+        qkn_b_k=qkn_b_k,
+        key_mask=key_mask,
+        scale=scale,
+        eps=eps,
+        W_proj_g=W_proj_g,
+        W_proj_o=W_proj_o,
     )

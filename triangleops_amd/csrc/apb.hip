@@ -1,19 +1,29 @@
 // attention_pair_bias core on gfx950.
 //
-// One block per (32-query block, key split).  Z is the dominant HBM stream (M^2 * Cz * 2
-// bytes); every block reads its Z[q-block, key-range, :] exactly once for ALL heads:
+// Two kernels (three when the key range is split):
+//   apb_qkv_kernel: Q = X.Wq^T (+ b_q, scaled), K = X.Wk^T, V = X.Wv^T for all M tokens once,
+//     (M, H*D) rows each, 32 tokens per block and one wave per head (MFMA, fp32 accumulation);
+//     the qk-norm variant (benchmarks/references.py:230-277) also takes the Q bias and a
+//     LayerNorm over the full H*D channel of Q and K (statistics exchanged between the head
+//     waves through LDS) here.
+//   apb_attn_kernel: one block per (32-query block, key split).  Z is the dominant HBM stream
+//     (M^2 * Cz * 2 bytes); every block reads its Z[q-block, key-range, :] exactly once for ALL
+//     heads:
 //   * per (query, 16 keys) the 16 x 128 Z slice is an MFMA A operand loaded straight from HBM;
 //     a 16x16x32 MFMA against [Wc_hi; Wc_lo] (the fp32 LN-folded weight split into two
 //     io-typed terms, accumulated into the same tile) gives z . Wc_h for the 4 heads, and the
 //     LayerNorm statistics are reduced from the same registers (two-pass, fp32);
 //   * bias[h,q,k] = rstd * (z . Wc_h - mean * sum(Wc_h)) + Bc_h goes through LDS to the wave
-//     of head h, which runs S^T = bias + K . Q^T, the online softmax and O^T += V^T . P^T with
-//     K and V projected from X in registers (the D layout of each MFMA is the operand layout of
-//     the next, so no LDS traffic for Q/K/V/P).
+//     of head h, which runs S^T = bias + K . Q^T, the online softmax and O^T += V^T . P^T.  The
+//     wave brings head h's Q, K and V into MFMA operand layout with two MFMA k-steps against a
+//     block-identity operand built in registers (an exact transpose through the matrix core),
+//     so there is no LDS traffic for Q/K/V/P.
 // Split partials (running max m, sum l, unnormalised O) are merged by apb_combine_kernel.
 //
 // Reference: attn_pair_bias/kernel.py:24-202 (`_apb_kernel`), :205-257 (`apb_forward`);
 // the key mask follows benchmarks/references.py:273-274 (masked keys -> -inf).
+#include <type_traits>
+
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -38,7 +48,8 @@ static ApbSplit apb_split(int64_t M) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
+__global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ Qm, const T* __restrict__ Km,
+                                                      const T* __restrict__ Vm,
                                                       const T* __restrict__ Z, int64_t sz0, int64_t sz1,
                                                       const float* __restrict__ Wc, const float* __restrict__ sWc,
                                                       const float* __restrict__ Bc, const int8_t* __restrict__ mask,
@@ -54,7 +65,15 @@ __global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ X, 
   const int hl = lane >> 5, col = lane & 31;
   const int l16 = lane & 15, g16 = lane >> 4;
   const int h = wave;  // attention role: head of this wave
-  const T* wh = wqkv + (int64_t)h * 3 * D * C;
+  // head h's 32 channels are k-steps 2h, 2h + 1 of the (M, 128) rows; `eye` is the matching block of
+  // the identity in operand layout (lane: row col, channels 16 s + 8 hl + e), so A . eye^T and
+  // eye . B^T reproduce the rows exactly in the MFMA output layout
+  const int s0 = 2 * h;
+  V8 eye[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) eye[s][e] = (T)(16 * s + 8 * hl + e == col ? 1.0f : 0.0f);
 
   // ---- Q^T for the block's 32 queries, head h (B operand of S^T = K . Q^T) ----
   const int64_t q0 = (int64_t)qb * 32;
@@ -64,19 +83,12 @@ __global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ X, 
     q = q < M ? q : M - 1;
     f32x16 acc = {};
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      acc = Mma<T>::m32(ldg<V8>(wh + (int64_t)col * C + 16 * s + 8 * hl), ldg<V8>(X + q * C + 16 * s + 8 * hl), acc);
+    for (int s = 0; s < 2; ++s) acc = Mma<T>::m32(eye[s], ldg<V8>(Qm + q * C + 16 * (s0 + s) + 8 * hl), acc);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       qop[0][e] = (T)(acc[e] * scale);
       qop[1][e] = (T)(acc[8 + e] * scale);
     }
-  }
-  V8 wk[8], wv[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    wk[s] = ldg<V8>(wh + (int64_t)(D + col) * C + 16 * s + 8 * hl);
-    wv[s] = ldg<V8>(wh + (int64_t)(2 * D + col) * C + 16 * s + 8 * hl);
   }
   // ---- [Wc_hi; Wc_lo] as the B operand of the bias MFMA (16x16x32: col = head) ----
   V8 whi[4], wlo[4];
@@ -159,10 +171,10 @@ __global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ X, 
       key = key < M ? key : M - 1;
       f32x16 ka = {}, va = {};
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const V8 xk = ldg<V8>(X + key * C + 16 * s + 8 * hl);
-        ka = Mma<T>::m32(wk[s], xk, ka);
-        va = Mma<T>::m32(xk, wv[s], va);
+      for (int s = 0; s < 2; ++s) {
+        const int64_t off = key * C + 16 * (s0 + s) + 8 * hl;
+        ka = Mma<T>::m32(eye[s], ldg<V8>(Km + off), ka);
+        va = Mma<T>::m32(ldg<V8>(Vm + off), eye[s], va);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -269,23 +281,239 @@ __global__ __launch_bounds__(256) void apb_combine_kernel(const float* __restric
   Og[q * (H * D) + hd] = (T)(ot / lt);
 }
 
+// Q / K / V pre-pass at the tuned shape (C = H*D = 128, H = 4, D = 32): 32 tokens per block,
+// wave h computes head h's 32 channels of q, k and v (8 MFMA k-steps each; lane col holds 16 of
+// the 32 channels of token q0 + col, the other 16 in lane col + 32).  With QKN the per-token
+// LayerNorm over all 128 channels of q and k takes its sums from the four head waves through LDS
+// (two passes: mean, then centred squares).  q is scaled by qscale last.
+template <typename T, bool QKN>
+__global__ __launch_bounds__(256) void apb_qkv_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
+                                                     const T* __restrict__ bq, const T* __restrict__ gq,
+                                                     const T* __restrict__ bqn, const T* __restrict__ gk,
+                                                     const T* __restrict__ bkn, T* __restrict__ qo,
+                                                     T* __restrict__ ko, T* __restrict__ vo, int64_t M, float qscale,
+                                                     float eps) {
+  constexpr int C = 128, D = 32, H = 4, HD = H * D;
+  using V8 = vec<T, 8>;
+  using V4 = vec<T, 4>;
+  __shared__ float red[2][4][32];  // [q / k][head][token]: per-head partial sums
+  const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int64_t q0 = (int64_t)blockIdx.x * 32;
+  int64_t tok = q0 + col;
+  tok = tok < M ? tok : M - 1;
+  V8 xs[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) xs[s] = ldg<V8>(X + tok * C + 16 * s + 8 * hl);
+  const T* wh = wqkv + (int64_t)h * 3 * D * C;
+  f32x16 acc[3];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    acc[t] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc[t] = Mma<T>::m32(ldg<V8>(wh + (int64_t)(t * D + col) * C + 16 * s + 8 * hl), xs[s], acc[t]);
+  }
+  // slot v of acc[t]: channel h*D + dch(v) of token q0 + col
+  auto dch = [&](int v) { return 8 * (v >> 2) + 4 * hl + (v & 3); };
+  if (bq) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][v] += (float)bq[h * D + dch(v)];
+  }
+  if constexpr (QKN) {
+    float mean[2], rstd[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float s1 = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s1 += acc[t][v];
+      s1 += __shfl_xor(s1, 32);
+      if (hl == 0) red[t][h][col] = s1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) mean[t] = (red[t][0][col] + red[t][1][col] + red[t][2][col] + red[t][3][col]) * (1.0f / HD);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float s2 = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float d = acc[t][v] - mean[t];
+        s2 += d * d;
+      }
+      s2 += __shfl_xor(s2, 32);
+      if (hl == 0) red[t][h][col] = s2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      rstd[t] = rsqrtf((red[t][0][col] + red[t][1][col] + red[t][2][col] + red[t][3][col]) * (1.0f / HD) + eps);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const T* g = t == 0 ? gq : gk;
+      const T* b = t == 0 ? bqn : bkn;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int c = h * D + dch(v);
+        float y = (acc[t][v] - mean[t]) * rstd[t];
+        if (g) y *= (float)g[c];
+        if (b) y += (float)b[c];
+        acc[t][v] = y;
+      }
+    }
+  }
+  if (q0 + col >= M) return;
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    T* dst = (t == 0 ? qo : t == 1 ? ko : vo) + (q0 + col) * HD + h * D;
+    const float f = t == 0 ? qscale : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      V4 r = {(T)(acc[t][4 * g] * f), (T)(acc[t][4 * g + 1] * f), (T)(acc[t][4 * g + 2] * f),
+              (T)(acc[t][4 * g + 3] * f)};
+      stg<V4>(dst + 8 * g + 4 * hl, r);
+    }
+  }
+}
+
+// Bytes of the Q / K / V region at the head of the apb workspace (16-bit I/O, 256-byte aligned).
+static int64_t apb_qkv_bytes(int64_t M) { return ((3 * M * 128 * 2) + 255) / 256 * 256; }
+
 template <typename T>
-static int apb_forward_t(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
-                         const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M,
-                         float scale, float eps, hipStream_t st) {
+static int apb_qkv_t(const void* X, const void* wqkv, const void* bq, int qkn, const void* gq, const void* bqn,
+                     const void* gk, const void* bkn, void* q, void* k, void* v, int64_t M, float qscale, float eps,
+                     hipStream_t st) {
+  const int64_t blocks = (M + 31) / 32;
+  if (blocks == 0) return TOPS_OK;
+  if (qkn)
+    hipLaunchKernelGGL((apb_qkv_kernel<T, true>), dim3((unsigned)blocks), dim3(256), 0, st, (const T*)X,
+                       (const T*)wqkv, (const T*)bq, (const T*)gq, (const T*)bqn, (const T*)gk, (const T*)bkn, (T*)q,
+                       (T*)k, (T*)v, M, qscale, eps);
+  else
+    hipLaunchKernelGGL((apb_qkv_kernel<T, false>), dim3((unsigned)blocks), dim3(256), 0, st, (const T*)X,
+                       (const T*)wqkv, (const T*)bq, (const T*)gq, (const T*)bqn, (const T*)gk, (const T*)bkn, (T*)q,
+                       (T*)k, (T*)v, M, qscale, eps);
+  return launched("apb_qkv_kernel");
+}
+
+template <typename T>
+static int apb_attention_t(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0, int64_t sz1,
+                           const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og, void* part,
+                           int64_t M, float scale, float eps, hipStream_t st) {
   if (M == 0) return TOPS_OK;
   const ApbSplit sp = apb_split(M);
   const int64_t qblocks = (M + 31) / 32;
   const int64_t grid = qblocks * sp.nsplit;
-  hipLaunchKernelGGL((apb_attn_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)X, (const T*)wqkv,
-                     (const T*)Z, sz0, sz1, Wc, sWc, Bc, (const int8_t*)mask, (T*)Og, (float*)work, M, sp.nsplit,
-                     sp.keys_per_split, scale, eps);
-  int rc = launched("tops_apb_forward");
+  hipLaunchKernelGGL((apb_attn_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Q, (const T*)K,
+                     (const T*)V, (const T*)Z, sz0, sz1, Wc, sWc, Bc, (const int8_t*)mask, (T*)Og, (float*)part, M,
+                     sp.nsplit, sp.keys_per_split, scale, eps);
+  int rc = launched("apb_attn_kernel");
   if (rc != TOPS_OK || sp.nsplit == 1) return rc;
   const int64_t n = M * 128;
   hipLaunchKernelGGL((apb_combine_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                     (const float*)work, (T*)Og, M, sp.nsplit);
-  return launched("tops_apb_forward(combine)");
+                     (const float*)part, (T*)Og, M, sp.nsplit);
+  return launched("apb_combine_kernel");
+}
+
+// ---------------------------------------------------------------------------------------------
+// qk-norm pre-pass (benchmarks/references.py:258-264), any C, H, D: per token m
+//   q = X[m] . Wq^T + b_q,  k = X[m] . Wk^T,  v = X[m] . Wv^T          (fp32 accumulation)
+//   with qkn: q <- LN(q) * g_q + b_q', k <- LN(k) * g_k + b_k' over the full H*D channel
+// written as (M, H*D) rows in the I/O type.  kQknTok tokens per block: the weight rows are read
+// once per block, the token rows are LDS broadcasts.
+// ---------------------------------------------------------------------------------------------
+constexpr int kQknTok = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void apb_qkn_prep_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
+                                                          const T* __restrict__ bq, int qkn, const T* __restrict__ gq,
+                                                          const T* __restrict__ bqn, const T* __restrict__ gk,
+                                                          const T* __restrict__ bkn,
+                                                          T* __restrict__ qo, T* __restrict__ ko, T* __restrict__ vo,
+                                                          int64_t M, int C, int H, int D, float qscale, float eps) {
+  extern __shared__ float sm[];
+  const int HD = H * D, F = 3 * HD;
+  float* xs = sm;                    // [kQknTok][C]
+  float* raw = xs + kQknTok * C;     // [kQknTok][3][HD]: q, k, v
+  float* stat = raw + kQknTok * F;   // [kQknTok][2][2]: (mean, rstd) of q and k
+  const int tid = threadIdx.x;
+  const int64_t m0 = (int64_t)blockIdx.x * kQknTok;
+  for (int e = tid; e < kQknTok * C; e += 256) {
+    const int64_t m = m0 + e / C;
+    xs[e] = m < M ? (float)X[m * C + e % C] : 0.f;
+  }
+  __syncthreads();
+  for (int f = tid; f < F; f += 256) {  // f: row of the (H, 3, D, C) weight
+    const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+    const T* w = wqkv + (int64_t)f * C;
+    float acc[kQknTok];
+#pragma unroll
+    for (int t = 0; t < kQknTok; ++t) acc[t] = 0.f;
+    for (int c = 0; c < C; ++c) {
+      const float wc = (float)w[c];
+#pragma unroll
+      for (int t = 0; t < kQknTok; ++t) acc[t] = fmaf(xs[t * C + c], wc, acc[t]);
+    }
+    const int ch = h * D + d;
+    const float add = (which == 0 && bq) ? (float)bq[ch] : 0.f;
+#pragma unroll
+    for (int t = 0; t < kQknTok; ++t) raw[(t * 3 + which) * HD + ch] = acc[t] + add;
+  }
+  __syncthreads();
+  if (qkn) {
+    // one wave per (token, q / k) row: two-pass mean and variance over H*D
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int r = wave; r < 2 * kQknTok; r += 4) {
+      const float* row = raw + ((r >> 1) * 3 + (r & 1)) * HD;
+      float sum = 0.f;
+      for (int c = lane; c < HD; c += 64) sum += row[c];
+      for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+      const float mean = sum / (float)HD;
+      float sq = 0.f;
+      for (int c = lane; c < HD; c += 64) {
+        const float dv = row[c] - mean;
+        sq += dv * dv;
+      }
+      for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+      if (lane == 0) {
+        stat[r * 2] = mean;
+        stat[r * 2 + 1] = rsqrtf(sq / (float)HD + eps);
+      }
+    }
+    __syncthreads();
+  }
+  for (int e = tid; e < kQknTok * F; e += 256) {
+    const int t = e / F, which = (e / HD) % 3, ch = e % HD;
+    const int64_t m = m0 + t;
+    if (m >= M) continue;
+    float val = raw[e];
+    if (qkn && which < 2) {
+      const int r = t * 2 + which;
+      val = (val - stat[r * 2]) * stat[r * 2 + 1];
+      const T* g = which == 0 ? gq : gk;
+      const T* b = which == 0 ? bqn : bkn;
+      if (g) val *= (float)g[ch];
+      if (b) val += (float)b[ch];
+    }
+    T* dst = which == 0 ? qo : which == 1 ? ko : vo;
+    dst[m * HD + ch] = (T)(which == 0 ? val * qscale : val);
+  }
+}
+
+template <typename T>
+static int apb_qkn_prep_t(const void* X, const void* wqkv, const void* bq, int qkn, const void* gq, const void* bqn,
+                          const void* gk, const void* bkn, void* q, void* k, void* v, int64_t M, int C, int H, int D,
+                          float qscale, float eps, hipStream_t st) {
+  if constexpr (!std::is_same_v<T, float>) {
+    if (C == 128 && H == 4 && D == 32) return apb_qkv_t<T>(X, wqkv, bq, qkn, gq, bqn, gk, bkn, q, k, v, M, qscale, eps, st);
+  }
+  const int64_t blocks = (M + kQknTok - 1) / kQknTok;
+  if (blocks == 0) return TOPS_OK;
+  const size_t lds = ((size_t)kQknTok * C + (size_t)kQknTok * 3 * H * D + 4 * kQknTok) * sizeof(float);
+  hipLaunchKernelGGL((apb_qkn_prep_kernel<T>), dim3((unsigned)blocks), dim3(256), lds, st, (const T*)X,
+                     (const T*)wqkv, (const T*)bq, qkn, (const T*)gq, (const T*)bqn, (const T*)gk, (const T*)bkn,
+                     (T*)q, (T*)k, (T*)v, M, C, H, D, qscale, eps);
+  return launched("tops_apb_qkn_prep");
 }
 
 }  // namespace tops
@@ -295,8 +523,8 @@ using namespace tops;
 extern "C" int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D) {
   if (M <= 0) return 0;
   const ApbSplit sp = apb_split(M);
-  if (sp.nsplit == 1) return 0;
-  return (int64_t)sp.nsplit * M * H * (D + 2) * 4;
+  const int64_t part = sp.nsplit == 1 ? 0 : (int64_t)sp.nsplit * M * H * (D + 2) * 4;
+  return apb_qkv_bytes(M) + part;
 }
 
 extern "C" int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
@@ -308,11 +536,60 @@ extern "C" int tops_apb_forward(const void* X, const void* wqkv, const void* Z, 
                "tops_apb_forward: supports C == Cz == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld D=%lld)",
                (long long)C, (long long)Cz, (long long)H, (long long)D);
   TOPS_REQUIRE(M >= 0, "tops_apb_forward: bad M");
-  TOPS_REQUIRE(work || tops_apb_workspace_bytes(M, H, D) == 0, "tops_apb_forward: workspace required");
+  TOPS_REQUIRE(work || M == 0, "tops_apb_forward: workspace of tops_apb_workspace_bytes(M, H, D) bytes required");
+  if (M == 0) return TOPS_OK;
+  hipStream_t st = (hipStream_t)stream;
+  char* w = (char*)work;
+  char *q = w, *k = w + M * 128 * 2, *v = w + 2 * M * 128 * 2, *part = w + apb_qkv_bytes(M);
+  int rc;
+  if (dtype == TOPS_DTYPE_BF16) {
+    rc = apb_qkv_t<__bf16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
+    return rc != TOPS_OK ? rc : apb_attention_t<__bf16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st);
+  }
+  if (dtype == TOPS_DTYPE_F16) {
+    rc = apb_qkv_t<_Float16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
+    return rc != TOPS_OK ? rc : apb_attention_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st);
+  }
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_forward: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_apb_forward_qkv(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0,
+                                    int64_t sz1, const float* Wc, const float* sWc, const float* Bc, const void* mask,
+                                    void* Og, void* work, int64_t M, int64_t HD, int64_t Cz, int64_t H, int64_t D,
+                                    float scale, float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(Q && K && V && Z && Wc && sWc && Bc && Og, "tops_apb_forward_qkv: null pointer argument");
+  TOPS_REQUIRE(HD == 128 && Cz == 128 && H == 4 && D == 32,
+               "tops_apb_forward_qkv: supports H*D == Cz == 128, H == 4, D == 32 (got H*D=%lld Cz=%lld H=%lld D=%lld)",
+               (long long)HD, (long long)Cz, (long long)H, (long long)D);
+  TOPS_REQUIRE(M >= 0, "tops_apb_forward_qkv: bad M");
+  TOPS_REQUIRE(work || M == 0, "tops_apb_forward_qkv: workspace of tops_apb_workspace_bytes(M, H, D) bytes required");
+  if (M == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return apb_forward_t<__bf16>(X, wqkv, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
+    return apb_attention_t<__bf16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
   if (dtype == TOPS_DTYPE_F16)
-    return apb_forward_t<_Float16>(X, wqkv, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
-  return fail(TOPS_EUNSUPPORTED, "tops_apb_forward: unsupported dtype code %d", dtype);
+    return apb_attention_t<_Float16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_forward_qkv: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_apb_qkn_prep(const void* X, const void* wqkv, const void* bq, int qkn, const void* gq,
+                                 const void* bqn, const void* gk, const void* bkn, void* q, void* k, void* v,
+                                 int64_t M, int64_t C, int64_t H, int64_t D, float qscale, float eps, int dtype,
+                                 void* stream) {
+  TOPS_REQUIRE(X && wqkv && q && k && v, "tops_apb_qkn_prep: null pointer argument");
+  // generic shapes: LDS of kQknTok rows of C + 3 H D floats (plus the statistics) within 64 KiB
+  TOPS_REQUIRE(M >= 0 && M <= (1LL << 31) && C >= 1 && H >= 1 && D >= 1 && C + 3 * H * D <= 2040,
+               "tops_apb_qkn_prep: supports C + 3 * H * D <= 2040 (got M=%lld C=%lld H=%lld D=%lld)", (long long)M,
+               (long long)C, (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return apb_qkn_prep_t<__bf16>(X, wqkv, bq, qkn, gq, bqn, gk, bkn, q, k, v, M, (int)C, (int)H, (int)D, qscale, eps,
+                                  st);
+  if (dtype == TOPS_DTYPE_F16)
+    return apb_qkn_prep_t<_Float16>(X, wqkv, bq, qkn, gq, bqn, gk, bkn, q, k, v, M, (int)C, (int)H, (int)D, qscale,
+                                    eps, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return apb_qkn_prep_t<float>(X, wqkv, bq, qkn, gq, bqn, gk, bkn, q, k, v, M, (int)C, (int)H, (int)D, qscale, eps,
+                                 st);
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_qkn_prep: unsupported dtype code %d", dtype);
 }
