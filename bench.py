@@ -15,7 +15,7 @@ Prints ONE JSON line with the contract fields plus:
   kernels       the same figures for each kernel of the step;
   torch_path_ms the reference's pure-torch bf16 formulation on the same GPU;
   cpu_baseline  the fp32 CPU oracle on this host (one full outgoing call at the same size).
-`--sweep FILE` additionally times all three ops and the apb qk-norm variant at sizes 128..2048 (ours, the torch path and
+`--sweep FILE` additionally times all three ops, the apb qk-norm variant and a Pairformer pair stack at sizes 128..2048 (ours, the torch path and
 per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
 """
 
@@ -203,6 +203,15 @@ def torch_apb_qknorm(d, p, eps=1e-5):
     o = torch.matmul(torch.softmax(scores, -1), v).permute(1, 0, 2).reshape(M, H * D)
     g = torch.sigmoid(F.linear(X, d["W_proj_g"]))
     return F.linear(g * o, d["W_proj_o"])
+
+
+def torch_pair_stack(z, m, w_out, w_in, ts, te, eps=1e-5):
+    """The four residual pair updates of a Pairformer block over the torch formulations above."""
+    z = z + torch_tmu(z[None], "outgoing", m[None], eps, **w_out)[0]
+    z = z + torch_tmu(z[None], "incoming", m[None], eps, **w_in)[0]
+    z = z + torch_tri(dict(ts, X=z, mask=m), eps)
+    zt = z.transpose(0, 1).contiguous()
+    return z + torch_tri(dict(te, X=zt, mask=m.T.contiguous()), eps).transpose(0, 1)
 
 
 # --------------------------------------------------------------------------- #
@@ -477,6 +486,40 @@ def sweep(path, sizes, dev):
             f.flush()
             rows.append(r)
             del d, pre, p
+        # Pairformer pair stack (z += tmu_out, tmu_in, tri_start, tri_end): fused residual adds vs
+        # the same ops with separate adds vs the torch formulation
+        for N in [n for n in sizes if n <= 1024]:
+            torch.cuda.empty_cache()
+            x, m, w_out = tmu_inputs(N)
+            _, _, w_in = tmu_inputs(N, seed=1)
+            ts, te = tri_inputs(N, seed=2), tri_inputs(N, seed=3)
+            keys = ("W_ln", "B_ln", "WQ", "WK", "WV", "W_proj_z", "B_proj_z", "W_proj_g", "W_proj_o")
+            ts, te = ({k: t[k].to(dev) for k in keys} for t in (ts, te))
+            z, pm = x[0].to(dev), m[0].to(dev)
+            w_out, w_in = ({k: v.to(dev) for k, v in w.items()} for w in (w_out, w_in))
+            pre = tops.pairformer.precompute(w_out, w_in, ts, te, H=H, D=D)
+            it = 20 if N <= 512 else 8
+            ms = time_ms(lambda: tops.pairformer.pair_stack(z, pre, pair_mask=pm), it, 3)
+
+            def unfused():
+                m3 = pm[None]
+                z1 = z + tops.triangle_mul.forward(z[None], pre["tmu_out"], direction="outgoing", mask=m3)[0]
+                z2 = z1 + tops.triangle_mul.forward(z1[None], pre["tmu_in"], direction="incoming", mask=m3)[0]
+                z3 = z2 + tops.triangle_attn.forward(z2, pre["tri_start"], mask=pm, scale=D**-0.5, W_proj_g=ts["W_proj_g"],
+                                                     B_proj_g=None, W_proj_o=ts["W_proj_o"], B_proj_o=None)
+                e = tops.triangle_attn.forward(z3.transpose(0, 1), pre["tri_end"], mask=pm.T, scale=D**-0.5,
+                                               W_proj_g=te["W_proj_g"], B_proj_g=None, W_proj_o=te["W_proj_o"],
+                                               B_proj_o=None)
+                return z3 + e.transpose(0, 1)
+
+            ms_unf = time_ms(unfused, it, 3)
+            tms = time_ms(lambda: torch_pair_stack(z, pm, w_out, w_in, ts, te), max(3, it // 4), 1)
+            r = {"op": "pairformer_pair_stack", "size": N, "ms": round(ms, 4), "ms_unfused_adds": round(ms_unf, 4),
+                 "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": {}}
+            f.write(json.dumps(r) + "\n")
+            f.flush()
+            rows.append(r)
+            del x, m, z, pm, pre, w_out, w_in, ts, te
     return rows
 
 

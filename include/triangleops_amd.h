@@ -124,6 +124,35 @@ int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, int6
                   void* stream);
 
 /*
+ * Residual-fused output kernels for composing a Pairformer block (z <- z + op(z)); the
+ * reference has no block composition, these serve the step after each of its ops (no
+ * counterpart in the reference):
+ * tops_tmu_output_phase_residual: as tops_tmu_output_phase with out = res + result, res io
+ *   (B, L, L, C_out) contiguous (16-byte aligned at the tuned shape).
+ * tops_gate_out_residual / tops_gate_out_generic_residual: as tops_gate_out /
+ *   tops_gate_out_generic with out[m1, m2] = res[m1, m2] + result, token (m1, m2) of res at
+ *   res[m1*sr0 + m2*sr1 + c] and of out at out[m1*sd0 + m2*sd1 + c] (the ending node writes
+ *   straight into the untransposed pair tensor); the tuned kernel needs strides that are
+ *   multiples of 8 and 16-byte aligned bases.
+ * Each sum is rounded once to the I/O type, from the result already rounded, as a separate
+ * `res + result` in the I/O type would be.
+ */
+int tops_tmu_output_phase_residual(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
+                                   const float* sWg, const float* Bp, const float* Bg, const void* res, void* out,
+                                   int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype,
+                                   void* stream);
+int tops_gate_out_residual(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
+                           const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg,
+                           const void* bg, const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1,
+                           void* out, int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int64_t C, int dtype,
+                           void* stream);
+int tops_gate_out_generic_residual(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
+                                   int64_t sg1, const void* w_ln, const void* b_ln, float ln_eps, int apply_ln,
+                                   const void* Wg, const void* bg, const void* Wo, const void* bo, const void* res,
+                                   int64_t sr0, int64_t sr1, void* out, int64_t sd0, int64_t sd1, int64_t M1,
+                                   int64_t M2, int64_t Cin, int64_t HD, int64_t Cout, int dtype, void* stream);
+
+/*
  * attention_pair_bias core.  Replaces `apb_forward` + `_apb_kernel`
  * (attn_pair_bias/kernel.py:205-257, :24-202).
  *   X      io   (M, C) contiguous, C == 128

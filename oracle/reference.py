@@ -22,6 +22,10 @@ Reference files followed (paths relative to the reference repository root):
 * `benchmarks/references.py:230-277`  attention_pair_bias_qknorm (the K-Fold
   variant: Q bias, optional LayerNorm over the full H*D channel of Q and K
   before the head split, key mask, bias-free gate and output projections).
+* Pairformer-block composition (no counterpart in the reference, which ships
+  the ops only): the pair stack z += tmu_out(z), z += tmu_in(z),
+  z += tri_start(z), z += tri_end(z) = tri(z^T)^T, and the single update
+  s += apb(s, z), composed from the functions above.
 
 How each function is pinned (tests/test_oracle.py):
 * every op is compared with the pure-Python loop restatement in
@@ -61,6 +65,8 @@ __all__ = [
     "attention_pair_bias",
     "apb_qknorm_qkv",
     "attention_pair_bias_qknorm",
+    "pair_stack",
+    "single_update",
 ]
 
 
@@ -287,3 +293,34 @@ def attention_pair_bias_qknorm(X, WQ, b_q, WK, WV, Z, W_ln, B_ln, W_proj_z, B_pr
         o = torch.matmul(torch.softmax(scores, -1), vh).permute(1, 0, 2).reshape(len(r), H * D)
         outs.append(apb_gate_out(o, _f(X, dtype)[r], W_proj_g, None, W_proj_o, None, dtype))
     return torch.cat(outs, 0)
+
+
+def pair_stack(z, tmu_out, tmu_in, tri_start, tri_end, H, D, pair_mask=None, eps=1e-5, scale=None,
+               dtype=torch.float32):
+    """The four pair updates with residuals; z (N, N, C).  tmu_* are the 8-weight keyword dicts of
+    triangle_multiplicative_update, tri_* dicts with W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z,
+    W_proj_g, W_proj_o (bias-free gate / output).  The ending node is the op on z^T, transposed back."""
+    z = _f(z, dtype)
+    N = z.shape[0]
+    scale = D**-0.5 if scale is None else scale
+    m3 = None if pair_mask is None else pair_mask.reshape(1, N, N)
+    z = z + triangle_multiplicative_update(z[None], direction="outgoing", mask=m3, eps=eps, dtype=dtype, **tmu_out)[0]
+    z = z + triangle_multiplicative_update(z[None], direction="incoming", mask=m3, eps=eps, dtype=dtype, **tmu_in)[0]
+
+    def tri(x, w, mask):
+        return triangle_attention(x, w["W_ln"], w["B_ln"], w["WQ"], w["WK"], w["WV"], w["W_proj_z"], w["B_proj_z"],
+                                  w["W_proj_g"], None, w["W_proj_o"], None, H, D, scale=scale, eps=eps, mask=mask,
+                                  dtype=dtype)
+
+    z = z + tri(z, tri_start, pair_mask)
+    z = z + tri(z.transpose(0, 1), tri_end, None if pair_mask is None else pair_mask.T).transpose(0, 1)
+    return z
+
+
+def single_update(s, z, apb, H, D, key_mask=None, eps=1e-5, scale=None, dtype=torch.float32):
+    """s + attention_pair_bias(s, z); apb: dict of the op's weights (gate / output biases optional)."""
+    scale = D**-0.5 if scale is None else scale
+    out = attention_pair_bias(s, apb["WQ"], apb["WK"], apb["WV"], z, apb["W_ln"], apb["B_ln"], apb["W_proj_z"],
+                              apb["B_proj_z"], apb["W_proj_g"], apb.get("B_proj_g"), apb["W_proj_o"],
+                              apb.get("B_proj_o"), H, D, scale=scale, eps=eps, mask=key_mask, dtype=dtype)
+    return _f(s, dtype) + out

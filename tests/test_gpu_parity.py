@@ -7,6 +7,8 @@ padded+masked problem restricted to its valid block equals the cropped problem b
 Large configurations are checked on a sample of output rows (rows are independent).
 """
 
+import math
+
 import pytest
 import torch
 from _inputs import (TOL_COS, TOL_MAX_ABS, apb_inputs, apb_qkn_inputs, compare, pad_pair_mask, tmu_inputs, to_dev,
@@ -456,6 +458,110 @@ def test_apb_qknorm_config_sizes_sampled_rows(device, M):
     out = _qkn_call(inp, device)
     rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
     _check(out[rows].cpu(), _qkn_ref(inp, rows=rows), torch.bfloat16, f"apb qk-norm M={M}")
+
+
+# --------------------------------------------------------------------------- #
+# Pairformer block composition (residual adds fused into the output kernels)
+# --------------------------------------------------------------------------- #
+_TRI_KEYS = ("W_ln", "B_ln", "WQ", "WK", "WV", "W_proj_z", "B_proj_z", "W_proj_g", "W_proj_o")
+
+
+def _block_inputs(N, *, C=128, H=4, D=32, seed=0, dtype=torch.bfloat16, mask="pad"):
+    x, m, tmu_o = tmu_inputs(N, C=C, seed=seed, dtype=dtype, mask=mask)
+    _, _, tmu_i = tmu_inputs(N, C=C, seed=seed + 1, dtype=dtype, mask="none")
+    ts = tri_inputs(N, C=C, H=H, D=D, seed=seed + 2, dtype=dtype, mask="none", bias_z=True)
+    te = tri_inputs(N, C=C, H=H, D=D, seed=seed + 3, dtype=dtype, mask="none", bias_z=True)
+    return (x[0], None if m is None else m[0], tmu_o, tmu_i, {k: ts[k] for k in _TRI_KEYS},
+            {k: te[k] for k in _TRI_KEYS}, H, D)
+
+
+def _bf16_ulp(v):
+    return 2.0 ** (math.floor(math.log2(max(v, 1e-30))) - 7)
+
+
+def _unfused_pair_stack(z, pm, pre, dev):
+    """The same four updates from the ops without residual fusion and torch adds in the I/O type."""
+    N = z.shape[0]
+    m3 = None if pm is None else pm.reshape(1, N, N)
+    sc = pre["D"] ** -0.5
+    z = z + tops.triangle_mul.forward(z[None], pre["tmu_out"], direction="outgoing", mask=m3)[0]
+    z = z + tops.triangle_mul.forward(z[None], pre["tmu_in"], direction="incoming", mask=m3)[0]
+    wg, wo = pre["tri_start_proj"]
+    z = z + tops.triangle_attn.forward(z, pre["tri_start"], mask=pm, scale=sc, W_proj_g=wg, B_proj_g=None,
+                                       W_proj_o=wo, B_proj_o=None)
+    wg, wo = pre["tri_end_proj"]
+    e = tops.triangle_attn.forward(z.transpose(0, 1), pre["tri_end"], mask=None if pm is None else pm.T, scale=sc,
+                                   W_proj_g=wg, B_proj_g=None, W_proj_o=wo, B_proj_o=None)
+    return z + e.transpose(0, 1)
+
+
+def _check_block(out, expect, dtype, what):
+    """Budget of four residual updates: the per-op bar four times, plus one rounding of the residual
+    stream per update (half an ulp of its largest magnitude) in a 16-bit I/O type."""
+    diff, cos = compare(out, expect)
+    big = float(expect.abs().max())
+    ulp = {torch.bfloat16: _bf16_ulp(big), torch.float16: _bf16_ulp(big) / 8, torch.float32: 0.0}[dtype]
+    tol = 4 * TOL_MAX_ABS[dtype] + 4 * 0.5 * ulp
+    assert torch.isfinite(out.float()).all(), f"{what}: non-finite output"
+    assert diff <= tol and cos >= TOL_COS, f"{what}: max|d|={diff:.3e} (budget {tol:.3e}) cos={cos:.6f}"
+
+
+@pytest.mark.parametrize("N", [64, 130])
+@pytest.mark.parametrize("mask", ["none", "pad"])
+def test_pair_stack_fused_equals_unfused(device, N, mask):
+    z, pm, tmu_o, tmu_i, ts, te, H, D = _block_inputs(N, seed=N, mask=mask)
+    d = lambda t: None if t is None else t.to(device)  # noqa: E731
+    dd = lambda w: {k: d(v) for k, v in w.items()}  # noqa: E731
+    pre = tops.pairformer.precompute(dd(tmu_o), dd(tmu_i), dd(ts), dd(te), H=H, D=D)
+    fused = tops.pairformer.pair_stack(d(z), pre, pair_mask=d(pm))
+    assert fused.is_contiguous() and fused.shape == z.shape
+    assert torch.equal(fused, _unfused_pair_stack(d(z), d(pm), pre, device)), f"pair stack N={N} mask={mask}"
+
+
+@pytest.mark.parametrize("N,C,H,D,dtype", [(64, 128, 4, 32, torch.bfloat16), (130, 128, 4, 32, torch.bfloat16),
+                                           (48, 64, 4, 16, torch.bfloat16), (40, 128, 4, 32, torch.float32)])
+def test_pair_stack_matches_oracle(device, N, C, H, D, dtype):
+    z, pm, tmu_o, tmu_i, ts, te, H, D = _block_inputs(N, C=C, H=H, D=D, seed=N + C, dtype=dtype)
+    d = lambda t: None if t is None else t.to(device)  # noqa: E731
+    dd = lambda w: {k: d(v) for k, v in w.items()}  # noqa: E731
+    pre = tops.pairformer.precompute(dd(tmu_o), dd(tmu_i), dd(ts), dd(te), H=H, D=D)
+    out = tops.pairformer.pair_stack(d(z), pre, pair_mask=d(pm))
+    expect = ref.pair_stack(z, tmu_o, tmu_i, ts, te, H, D, pair_mask=pm)
+    _check_block(out, expect, dtype, f"pair stack N={N} C={C} H={H} D={D} {dtype}")
+
+
+@pytest.mark.parametrize("M", [96, 256])
+def test_single_update_fused_and_oracle(device, M):
+    inp = apb_inputs(M, seed=M, mask="pad", biases=True)
+    apb = {k: inp[k] for k in ("WQ", "WK", "WV", "W_ln", "B_ln", "W_proj_z", "B_proj_z", "W_proj_g", "B_proj_g",
+                               "W_proj_o", "B_proj_o")}
+    d = to_dev(inp, device)
+    _, _, tmu_o = tmu_inputs(4)  # the pair-stack weights are not used by the single update
+    tri = {k: v for k, v in tri_inputs(4).items() if k in _TRI_KEYS}
+    pre = tops.pairformer.precompute(to_dev(tmu_o, device), to_dev(tmu_o, device), to_dev(tri, device),
+                                     to_dev(tri, device), to_dev(apb, device), H=4, D=32)
+    s = tops.pairformer.single_update(d["X"], d["Z"], pre, key_mask=d["mask"])
+    plain = d["X"] + tops.attention_pair_bias(d["X"], d["WQ"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"],
+                                              d["W_proj_z"], d["B_proj_z"], d["W_proj_g"], d["B_proj_g"],
+                                              d["W_proj_o"], d["B_proj_o"], 4, 32, scale=32**-0.5, mask=d["mask"])
+    assert torch.equal(s, plain), f"single update M={M}: fused != unfused"
+    expect = ref.single_update(inp["X"], inp["Z"], apb, 4, 32, key_mask=inp["mask"])
+    diff, cos = compare(s, expect)
+    tol = TOL_MAX_ABS[torch.bfloat16] + 0.5 * _bf16_ulp(float(expect.abs().max()))
+    assert diff <= tol and cos >= TOL_COS, f"single update M={M}: max|d|={diff:.3e} (budget {tol:.3e}) cos={cos}"
+
+
+def test_pairformer_block(device):
+    z, pm, tmu_o, tmu_i, ts, te, H, D = _block_inputs(96, seed=5)
+    inp = apb_inputs(96, seed=6, mask="none", biases=True)
+    apb = {k: inp[k] for k in ("WQ", "WK", "WV", "W_ln", "B_ln", "W_proj_z", "B_proj_z", "W_proj_g", "B_proj_g",
+                               "W_proj_o", "B_proj_o")}
+    d = lambda t: None if t is None else t.to(device)  # noqa: E731
+    dd = lambda w: {k: d(v) for k, v in w.items()}  # noqa: E731
+    pre = tops.pairformer.precompute(dd(tmu_o), dd(tmu_i), dd(ts), dd(te), dd(apb), H=H, D=D)
+    zo, so = tops.pairformer.pairformer_block(d(z), d(inp["X"]), pre, pair_mask=d(pm))
+    assert torch.equal(zo, tops.pairformer.pair_stack(d(z), pre, pair_mask=d(pm)))
+    assert torch.equal(so, tops.pairformer.single_update(d(inp["X"]), zo, pre))
 
 
 # --------------------------------------------------------------------------- #

@@ -199,6 +199,59 @@ def test_apb_qknorm_key_mask_crop():
     assert _close(full[:3], _qkn(crop))
 
 
+def _block_small(N=4, C=4, H=2, D=2, seed=11):
+    """Weights of a tiny Pairformer pair stack (C = H*D so the attention output feeds the residual)."""
+    _, _, tmu_out = _tmu_small(L=N, C=C, seed=seed)
+    _, _, tmu_in = _tmu_small(L=N, C=C, seed=seed + 1)
+    tri = []
+    for k in (2, 3):
+        d = _tri_small(N=N, C=C, H=H, D=D, seed=seed + k)
+        tri.append({n: d[n] for n in ("W_ln", "B_ln", "WQ", "WK", "WV", "W_proj_z", "B_proj_z", "W_proj_g",
+                                      "W_proj_o")})
+    z = torch.randn(N, N, C, generator=_g(seed + 9), dtype=F64)
+    m = torch.rand(N, N, generator=_g(seed + 10)) < 0.75
+    m[:, 0] = True
+    return z, m, tmu_out, tmu_in, tri[0], tri[1], H, D
+
+
+def test_pair_stack_oracle_matches_brute_composition():
+    """The oracle's pair stack == the same four residual updates built from the loop restatements
+    (ending node = the op on z^T, transposed back)."""
+    z, m, tmu_out, tmu_in, t0, t1, H, D = _block_small()
+    got = ref.pair_stack(z, tmu_out, tmu_in, t0, t1, H, D, pair_mask=m, scale=0.5, dtype=F64)
+    N = z.shape[0]
+    zb = z.clone()
+    zb = zb + torch.tensor(brute.triangle_multiplicative_update(zb[None], direction="outgoing",
+                                                                mask=m.reshape(1, N, N).double(), **tmu_out),
+                           dtype=F64)[0]
+    zb = zb + torch.tensor(brute.triangle_multiplicative_update(zb[None], direction="incoming",
+                                                                mask=m.reshape(1, N, N).double(), **tmu_in),
+                           dtype=F64)[0]
+
+    def tri(x, w, mask):
+        return torch.tensor(brute.triangle_attention(x, w["W_ln"], w["B_ln"], w["WQ"], w["WK"], w["WV"],
+                                                     w["W_proj_z"], w["B_proj_z"], w["W_proj_g"], None,
+                                                     w["W_proj_o"], None, H, D, scale=0.5, mask=mask),
+                            dtype=F64)
+
+    zb = zb + tri(zb, t0, m)
+    zb = zb + tri(zb.transpose(0, 1), t1, m.T).transpose(0, 1)
+    assert _close(got, zb)
+    # the ending node is not the starting node: swapping the transposes changes the result
+    wrong = ref.pair_stack(z, tmu_out, tmu_in, t0, t0, H, D, pair_mask=m, scale=0.5, dtype=F64)
+    assert not _close(got, wrong, tol=1e-6)
+
+
+def test_single_update_oracle_is_residual_of_apb():
+    d = _apb_small()
+    apb = {k: d[k] for k in ("WQ", "WK", "WV", "W_ln", "B_ln", "W_proj_z", "B_proj_z", "W_proj_g", "B_proj_g",
+                             "W_proj_o", "B_proj_o")}
+    s = d["X"]
+    got = ref.single_update(s, d["Z"], apb, 2, 3, key_mask=d["mask"], scale=d["scale"], dtype=F64)
+    want = s + torch.tensor(brute.attention_pair_bias(*_apb_args(d), scale=d["scale"], mask=d["mask"]), dtype=F64)
+    assert _close(got, want)
+
+
 # --------------------------------------------------------------------------- #
 # golden fixtures (written by brute force at the kernels' real widths)
 # --------------------------------------------------------------------------- #

@@ -42,6 +42,17 @@ _SIGNATURES = {
     "tops_apb_qkn_prep": [
         _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],
+    "tops_tmu_output_phase_residual": [
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p,
+    ],
+    "tops_gate_out_residual": [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64,
+        _i64, _i64, _i32, _p,
+    ],
+    "tops_gate_out_generic_residual": [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64,
+        _i64, _i64, _i64, _i64, _i32, _p,
+    ],
     "tops_tri_generic_prep": [
         _p, _i64, _i64, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p,
     ],

@@ -43,8 +43,9 @@ def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
     }
 
 
-def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, mask=None):
-    """Per-call forward.  X (M, C_s), Z (M, M, C_z) -> (M, C_out)."""
+def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, mask=None, residual=None):
+    """Per-call forward.  X (M, C_s), Z (M, M, C_z) -> (M, C_out); `residual` (M, C_out) returns
+    residual + result, the add fused into the gate kernel's store (Pairformer single update)."""
     M = X.shape[0]
     H = pre["sum_W_combined"].shape[0]
     D = pre["W_QKV"].shape[1] // (3 * H)
@@ -62,7 +63,9 @@ def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_p
         mask=mask,
         wqkv_hm=pre.get("wqkv_hm"),
     )
-    return gate_out_forward(Og.view(M, 1, H * D), X, W_proj_g, B_proj_g, W_proj_o, B_proj_o).view(M, -1)
+    res = None if residual is None else residual.view(M, 1, -1)
+    return gate_out_forward(Og.view(M, 1, H * D), X, W_proj_g, B_proj_g, W_proj_o, B_proj_o,
+                            residual=res).view(M, -1)
 
 
 def attention_pair_bias(

@@ -20,14 +20,17 @@
 
 namespace tops {
 
-template <typename T, bool LN>
+// RES: out[m1, m2] = res[m1, m2] + result, both at their own token strides (the residual add of
+// a Pairformer block fused into the store; the sum is rounded once, as a separate add would be).
+template <typename T, bool LN, bool RES>
 __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
                                                       const T* __restrict__ gin, int64_t sg0, int64_t sg1,
                                                       const T* __restrict__ w_ln, const T* __restrict__ b_ln,
                                                       float ln_eps, const T* __restrict__ Wg,
                                                       const T* __restrict__ bg, const T* __restrict__ Wo,
-                                                      const T* __restrict__ bo, T* __restrict__ out, FastDiv M2,
-                                                      uint32_t M, uint32_t ntiles) {
+                                                      const T* __restrict__ bo, const T* __restrict__ res,
+                                                      int64_t sr0, int64_t sr1, T* __restrict__ out, int64_t sd0,
+                                                      int64_t sd1, FastDiv M2, uint32_t M, uint32_t ntiles) {
   constexpr int C = 128, ROW = C * 2, KS = C / 16;
   constexpr int NL = 256;  // loader threads (waves 0-3); writers are waves 4-7
   constexpr int PD = 2;    // register stages in flight
@@ -190,7 +193,17 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
         const int ci = k * NL + wt;  // token ci / 16, chunk ci % 16
         const int tk = ci >> 4, c = ci & 15;
         const uint32_t m = t * 64 + tk;
-        if (m < M) stg<V8>(out + (int64_t)m * C + 8 * c, *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ (tk & 15)) << 3)]));
+        if (m >= M) continue;
+        V8 v = *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ (tk & 15)) << 3)]);
+        if constexpr (RES) {
+          const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
+          const V8 r = ldg<V8>(res + m1 * sr0 + m2 * sr1 + 8 * c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (T)((float)r[e] + (float)v[e]);
+          stg<V8>(out + m1 * sd0 + m2 * sd1 + 8 * c, v);
+        } else {
+          stg<V8>(out + (int64_t)m * C + 8 * c, v);
+        }
       }
     }
   }
@@ -199,16 +212,19 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
 template <typename T>
 static int gate_out_t(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
                       const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg, const void* bg,
-                      const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2, hipStream_t st) {
+                      const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
+                      int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, hipStream_t st) {
   const int64_t M = M1 * M2;
   const int64_t ntiles = (M + 63) / 64;
   if (ntiles == 0) return TOPS_OK;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
-  auto kern = apply_ln ? gate_out_kernel<T, true> : gate_out_kernel<T, false>;
+  auto kern = apply_ln ? (res ? gate_out_kernel<T, true, true> : gate_out_kernel<T, true, false>)
+                       : (res ? gate_out_kernel<T, false, true> : gate_out_kernel<T, false, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), 0, st, (const T*)o, so0, so1, (const T*)gin, sg0, sg1,
                      (const T*)w_ln, (const T*)b_ln, ln_eps, (const T*)Wg, (const T*)bg, (const T*)Wo,
-                     (const T*)bo, (T*)out, FastDiv((uint32_t)M2), (uint32_t)M, (uint32_t)ntiles);
-  return launched("tops_gate_out");
+                     (const T*)bo, (const T*)res, sr0, sr1, (T*)out, sd0, sd1, FastDiv((uint32_t)M2), (uint32_t)M,
+                     (uint32_t)ntiles);
+  return launched(res ? "tops_gate_out_residual" : "tops_gate_out");
 }
 
 }  // namespace tops
@@ -229,10 +245,35 @@ extern "C" int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void
                "tops_gate_out: o, gin and out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1, M2,
-                              st);
+    return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0, 0,
+                              out, 0, 0, M1, M2, st);
   if (dtype == TOPS_DTYPE_F16)
-    return gate_out_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1,
-                                M2, st);
+    return gate_out_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0,
+                                0, out, 0, 0, M1, M2, st);
   return fail(TOPS_EUNSUPPORTED, "tops_gate_out: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_gate_out_residual(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
+                                      int64_t sg1, const void* w_ln, const void* b_ln, float ln_eps, int apply_ln,
+                                      const void* Wg, const void* bg, const void* Wo, const void* bo, const void* res,
+                                      int64_t sr0, int64_t sr1, void* out, int64_t sd0, int64_t sd1, int64_t M1,
+                                      int64_t M2, int64_t C, int dtype, void* stream) {
+  TOPS_REQUIRE(o && gin && Wg && Wo && res && out, "tops_gate_out_residual: null pointer argument");
+  TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out_residual: w_ln is required when apply_ln != 0");
+  TOPS_REQUIRE(C == 128, "tops_gate_out_residual: C must be 128 (got %lld)", (long long)C);
+  TOPS_REQUIRE(M1 >= 0 && M2 >= 0 && M1 * M2 < (1LL << 31), "tops_gate_out_residual: bad sizes");
+  TOPS_REQUIRE(so0 % 8 == 0 && so1 % 8 == 0 && sg0 % 8 == 0 && sg1 % 8 == 0 && sr0 % 8 == 0 && sr1 % 8 == 0 &&
+                   sd0 % 8 == 0 && sd1 % 8 == 0,
+               "tops_gate_out_residual: token strides must be multiples of 8 elements");
+  TOPS_REQUIRE((uintptr_t)o % 16 == 0 && (uintptr_t)gin % 16 == 0 && (uintptr_t)res % 16 == 0 &&
+                   (uintptr_t)out % 16 == 0,
+               "tops_gate_out_residual: o, gin, res and out must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TOPS_DTYPE_BF16)
+    return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0, sr1,
+                              out, sd0, sd1, M1, M2, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return gate_out_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0,
+                                sr1, out, sd0, sd1, M1, M2, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_gate_out_residual: unsupported dtype code %d", dtype);
 }

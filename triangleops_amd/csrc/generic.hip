@@ -162,8 +162,10 @@ __global__ __launch_bounds__(256) void gate_generic_kernel(const T* __restrict__
                                                           const T* __restrict__ w_ln, const T* __restrict__ b_ln,
                                                           float eps, int apply_ln, const T* __restrict__ Wg,
                                                           const T* __restrict__ bg, const T* __restrict__ Wo,
-                                                          const T* __restrict__ bo, T* __restrict__ out, int64_t M1,
-                                                          int64_t M2, int Cin, int HD, int Cout) {
+                                                          const T* __restrict__ bo, const T* __restrict__ res,
+                                                          int64_t sr0, int64_t sr1, T* __restrict__ out, int64_t sd0,
+                                                          int64_t sd1, int64_t M1, int64_t M2, int Cin, int HD,
+                                                          int Cout) {
   extern __shared__ float sm[];
   float* gs = sm;                   // [kGenTok][Cin]  gate input (normalised)
   float* ys = sm + kGenTok * Cin;   // [kGenTok][HD]   o, then the gated activations
@@ -201,7 +203,9 @@ __global__ __launch_bounds__(256) void gate_generic_kernel(const T* __restrict__
     const T* w = Wo + (int64_t)c * HD;
     float acc = bo ? (float)bo[c] : 0.f;
     for (int j = 0; j < HD; ++j) acc = fmaf(y[j], (float)w[j], acc);
-    out[tok * Cout + c] = (T)acc;
+    const int64_t m1 = tok / M2, m2 = tok % M2;
+    // with a residual: out = res + result, the result rounded first as a separate add would see it
+    out[m1 * sd0 + m2 * sd1 + c] = res ? (T)((float)res[m1 * sr0 + m2 * sr1 + c] + (float)(T)acc) : (T)acc;
   }
 }
 
@@ -241,15 +245,16 @@ static int tri_generic_attention_t(const void* q, const void* k, const void* v, 
 template <typename T>
 static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
                           const void* w_ln, const void* b_ln, float eps, int apply_ln, const void* Wg, const void* bg,
-                          const void* Wo, const void* bo, void* out, int64_t M1, int64_t M2, int Cin, int HD, int Cout,
+                          const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
+                          int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int Cin, int HD, int Cout,
                           hipStream_t st) {
   const int64_t blocks = (M1 * M2 + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   hipLaunchKernelGGL((gate_generic_kernel<T>), dim3((unsigned)blocks), dim3(256),
                      (size_t)kGenTok * (Cin + HD) * sizeof(float), st, (const T*)o, so0, so1, (const T*)gin, sg0, sg1,
                      (const T*)w_ln, (const T*)b_ln, eps, apply_ln, (const T*)Wg, (const T*)bg, (const T*)Wo,
-                     (const T*)bo, (T*)out, M1, M2, Cin, HD, Cout);
-  return launched("tops_gate_out_generic");
+                     (const T*)bo, (const T*)res, sr0, sr1, (T*)out, sd0, sd1, M1, M2, Cin, HD, Cout);
+  return launched(res ? "tops_gate_out_generic_residual" : "tops_gate_out_generic");
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -434,9 +439,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
                                                              const T* __restrict__ Wp, const T* __restrict__ Wg,
                                                              const float* __restrict__ Bp,
-                                                             const float* __restrict__ Bg, T* __restrict__ out,
-                                                             int64_t B, int64_t L, int C, int Cout, int64_t ldy,
-                                                             float eps) {
+                                                             const float* __restrict__ Bg, const T* __restrict__ res,
+                                                             T* __restrict__ out, int64_t B, int64_t L, int C,
+                                                             int Cout, int64_t ldy, float eps) {
   extern __shared__ float sm[];
   float* ys = sm;                 // [kGenTok][C]  y of the tile's tokens (token-major)
   float* xs = sm + kGenTok * C;   // [kGenTok][C]  x
@@ -475,7 +480,8 @@ __global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restric
       p = fmaf(yr[c], (float)wp[c], p);
       g = fmaf(xr[c], (float)wg[c], g);
     }
-    out[tok * Cout + f] = (T)(p * sigmoid(g));
+    const T r = (T)(p * sigmoid(g));
+    out[tok * Cout + f] = res ? (T)((float)res[tok * Cout + f] + (float)r) : r;
   }
 }
 
@@ -515,15 +521,15 @@ int tmu_generic_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_
 }
 
 int tmu_generic_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* Bp,
-                             const float* Bg, void* out, int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ldy,
-                             float eps, int dtype, hipStream_t st) {
+                             const float* Bg, const void* res, void* out, int64_t B, int64_t L, int64_t C,
+                             int64_t C_out, int64_t ldy, float eps, int dtype, hipStream_t st) {
   TOPS_REQUIRE(C >= 1 && C <= 512 && C_out >= 1 && C_out <= 4096,
                "tops_tmu_output_phase: supports C <= 512, C_out <= 4096 (got %lld, %lld)", (long long)C,
                (long long)C_out);
   const int64_t blocks = (B * L * L + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   const size_t lds = (size_t)2 * kGenTok * C * sizeof(float);
-#define TOPS_GEN_OUT(TT)                                                                                        hipLaunchKernelGGL((tmu_generic_out_kernel<TT>), dim3((unsigned)blocks), dim3(256), lds, st, (const TT*)y,                      (const TT*)x, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (TT*)out, B, L, (int)C, (int)C_out, ldy, eps)
+#define TOPS_GEN_OUT(TT)                                                                                        hipLaunchKernelGGL((tmu_generic_out_kernel<TT>), dim3((unsigned)blocks), dim3(256), lds, st, (const TT*)y,                      (const TT*)x, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (const TT*)res, (TT*)out, B, L, (int)C, (int)C_out, ldy, eps)
   if (dtype == TOPS_DTYPE_BF16)
     TOPS_GEN_OUT(__bf16);
   else if (dtype == TOPS_DTYPE_F16)
@@ -623,6 +629,23 @@ extern "C" int tops_apb_generic_attention(const void* q, const void* k, const vo
   return fail(TOPS_EUNSUPPORTED, "tops_apb_generic_attention: unsupported dtype code %d", dtype);
 }
 
+static int gate_generic_dispatch(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
+                                 const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg,
+                                 const void* bg, const void* Wo, const void* bo, const void* res, int64_t sr0,
+                                 int64_t sr1, void* out, int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int64_t Cin,
+                                 int64_t HD, int64_t Cout, int dtype, hipStream_t st) {
+  if (dtype == TOPS_DTYPE_BF16)
+    return gate_generic_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0,
+                                  sr1, out, sd0, sd1, M1, M2, (int)Cin, (int)HD, (int)Cout, st);
+  if (dtype == TOPS_DTYPE_F16)
+    return gate_generic_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res,
+                                    sr0, sr1, out, sd0, sd1, M1, M2, (int)Cin, (int)HD, (int)Cout, st);
+  if (dtype == TOPS_DTYPE_F32)
+    return gate_generic_t<float>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0,
+                                 sr1, out, sd0, sd1, M1, M2, (int)Cin, (int)HD, (int)Cout, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_gate_out_generic: unsupported dtype code %d", dtype);
+}
+
 extern "C" int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
                                      int64_t sg1, const void* w_ln, const void* b_ln, float ln_eps, int apply_ln,
                                      const void* Wg, const void* bg, const void* Wo, const void* bo, void* out,
@@ -634,15 +657,22 @@ extern "C" int tops_gate_out_generic(const void* o, int64_t so0, int64_t so1, co
   TOPS_REQUIRE(Cin >= 1 && HD >= 1 && Cout >= 1 && Cin + HD <= 1024 && Cout <= 4096,
                "tops_gate_out_generic: supports C_in + H*D <= 1024, C_out <= 4096 (got %lld, %lld, %lld)",
                (long long)Cin, (long long)HD, (long long)Cout);
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == TOPS_DTYPE_BF16)
-    return gate_generic_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1,
-                                  M2, (int)Cin, (int)HD, (int)Cout, st);
-  if (dtype == TOPS_DTYPE_F16)
-    return gate_generic_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out,
-                                    M1, M2, (int)Cin, (int)HD, (int)Cout, st);
-  if (dtype == TOPS_DTYPE_F32)
-    return gate_generic_t<float>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, out, M1, M2,
-                                 (int)Cin, (int)HD, (int)Cout, st);
-  return fail(TOPS_EUNSUPPORTED, "tops_gate_out_generic: unsupported dtype code %d", dtype);
+  return gate_generic_dispatch(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0, 0,
+                               out, M2 * Cout, Cout, M1, M2, Cin, HD, Cout, dtype, (hipStream_t)stream);
+}
+
+extern "C" int tops_gate_out_generic_residual(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0,
+                                              int64_t sg1, const void* w_ln, const void* b_ln, float ln_eps,
+                                              int apply_ln, const void* Wg, const void* bg, const void* Wo,
+                                              const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
+                                              int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int64_t Cin,
+                                              int64_t HD, int64_t Cout, int dtype, void* stream) {
+  TOPS_REQUIRE(o && gin && Wg && Wo && res && out, "tops_gate_out_generic_residual: null pointer argument");
+  TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out_generic_residual: w_ln is required when apply_ln != 0");
+  TOPS_REQUIRE(M1 >= 0 && M2 >= 0, "tops_gate_out_generic_residual: bad sizes");
+  TOPS_REQUIRE(Cin >= 1 && HD >= 1 && Cout >= 1 && Cin + HD <= 1024 && Cout <= 4096,
+               "tops_gate_out_generic_residual: supports C_in + H*D <= 1024, C_out <= 4096 (got %lld, %lld, %lld)",
+               (long long)Cin, (long long)HD, (long long)Cout);
+  return gate_generic_dispatch(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0, sr1,
+                               out, sd0, sd1, M1, M2, Cin, HD, Cout, dtype, (hipStream_t)stream);
 }

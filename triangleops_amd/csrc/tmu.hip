@@ -563,11 +563,14 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
 //   whole 256-byte rows per 16 lanes, after the barrier of tile n + 1, when every writer has
 //   finished it.  One barrier per tile.
 // ---------------------------------------------------------------------------------------------
-template <typename T>
+// RES: out = res + result (res in out's layout; the Pairformer residual add fused into the store,
+// the sum rounded once, as a separate add would be).
+template <typename T, bool RES>
 __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
                                                      const T* __restrict__ Wp, const T* __restrict__ Wg,
                                                      const float* __restrict__ sWp, const float* __restrict__ Bp,
-                                                     const float* __restrict__ Bg, T* __restrict__ out, int64_t L,
+                                                     const float* __restrict__ Bg, const T* __restrict__ res,
+                                                     T* __restrict__ out, int64_t L,
                                                      int64_t ldy, int64_t cstride, float eps, uint32_t ntiles,
                                                      FastDiv tpr, FastDiv Ld) {
   constexpr int C = 128, COUT = 128;
@@ -693,12 +696,17 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
     auto store = [&](uint32_t tt, int ob) {
       const GridTile g = grid_tile_fast(tt, tpr, Ld);
       const int64_t tok0 = (g.b * L + g.r) * L + g.c0;
-#pragma unroll
+#pragma unroll(RES ? 1 : 2)
       for (int k = 0; k < 2; ++k) {
         const int ci = k * 512 + wt;  // token ci / 16, chunk ci % 16
         const int tk = ci >> 4, c = ci & 15;
         if (g.c0 + tk < L) {
-          const V8 v = *reinterpret_cast<const V8*>(&os[ob][tk * COUT + ((c ^ (tk & 15)) << 3)]);
+          V8 v = *reinterpret_cast<const V8*>(&os[ob][tk * COUT + ((c ^ (tk & 15)) << 3)]);
+          if constexpr (RES) {
+            const V8 r = ldg<V8>(res + (tok0 + tk) * COUT + 8 * c);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (T)((float)r[e] + (float)v[e]);
+          }
           stg<V8>(out + (tok0 + tk) * COUT + 8 * c, v);
         }
       }
@@ -802,18 +810,23 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
 
 template <typename T>
 static int tmu_output_phase_t(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
-                              const float* Bp, const float* Bg, void* out, int64_t B, int64_t L, int64_t ldy,
-                              float eps, hipStream_t st) {
+                              const float* Bp, const float* Bg, const void* res, void* out, int64_t B, int64_t L,
+                              int64_t ldy, float eps, hipStream_t st) {
   const int64_t tpr = (L + 63) / 64;
   const int64_t ntiles = B * L * tpr;
   if (ntiles == 0) return TOPS_OK;
   const int64_t cstride = B * L * ldy;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
   const FastDiv tdiv((uint32_t)tpr), ldiv((uint32_t)L);
-  hipLaunchKernelGGL((tmu_out_kernel<T>), dim3((unsigned)grid), dim3(768), 0, st, (const T*)y, (const T*)x,
-                     (const T*)Wp, (const T*)Wg, sWp, Bp, Bg, (T*)out, L, ldy, cstride, eps, (uint32_t)ntiles, tdiv,
-                     ldiv);
-  return launched("tops_tmu_output_phase");
+  if (res)
+    hipLaunchKernelGGL((tmu_out_kernel<T, true>), dim3((unsigned)grid), dim3(768), 0, st, (const T*)y, (const T*)x,
+                       (const T*)Wp, (const T*)Wg, sWp, Bp, Bg, (const T*)res, (T*)out, L, ldy, cstride, eps,
+                       (uint32_t)ntiles, tdiv, ldiv);
+  else
+    hipLaunchKernelGGL((tmu_out_kernel<T, false>), dim3((unsigned)grid), dim3(768), 0, st, (const T*)y, (const T*)x,
+                       (const T*)Wp, (const T*)Wg, sWp, Bp, Bg, (const T*)nullptr, (T*)out, L, ldy, cstride, eps,
+                       (uint32_t)ntiles, tdiv, ldiv);
+  return launched(res ? "tops_tmu_output_phase_residual" : "tops_tmu_output_phase");
 }
 
 }  // namespace tops
@@ -856,22 +869,39 @@ extern "C" int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_einsum: unsupported dtype code %d", dtype);
 }
 
-extern "C" int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
-                                     const float* sWg, const float* Bp, const float* Bg, void* out, int64_t B,
-                                     int64_t L, int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype,
-                                     void* stream) {
+static int tmu_output_phase_any(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
+                                const float* sWg, const float* Bp, const float* Bg, const void* res, void* out,
+                                int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype,
+                                void* stream) {
   TOPS_REQUIRE(y && x && Wp && Wg && sWp && sWg && Bp && Bg && out, "tops_tmu_output_phase: null pointer argument");
   TOPS_REQUIRE(B >= 0 && L >= 0 && ldy >= L && ldy % 64 == 0,
                "tops_tmu_output_phase: bad sizes B=%lld L=%lld ldy=%lld (ldy must be a multiple of 64)",
                (long long)B, (long long)L, (long long)ldy);
   TOPS_REQUIRE(B * L * ((L + 63) / 64) < (1LL << 31), "tops_tmu_output_phase: too many tokens");
   if (C != 128 || C_out != 128 || dtype == TOPS_DTYPE_F32)  // any-shape kernels
-    return tmu_generic_output_phase(y, x, Wp, Wg, Bp, Bg, out, B, L, C, C_out, ldy, eps, dtype, (hipStream_t)stream);
+    return tmu_generic_output_phase(y, x, Wp, Wg, Bp, Bg, res, out, B, L, C, C_out, ldy, eps, dtype,
+                                    (hipStream_t)stream);
   (void)sWg;  // x is normalised before its GEMM: the column sums of Wg_c are not needed
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return tmu_output_phase_t<__bf16>(y, x, Wp, Wg, sWp, Bp, Bg, out, B, L, ldy, eps, st);
+    return tmu_output_phase_t<__bf16>(y, x, Wp, Wg, sWp, Bp, Bg, res, out, B, L, ldy, eps, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tmu_output_phase_t<_Float16>(y, x, Wp, Wg, sWp, Bp, Bg, out, B, L, ldy, eps, st);
+    return tmu_output_phase_t<_Float16>(y, x, Wp, Wg, sWp, Bp, Bg, res, out, B, L, ldy, eps, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_output_phase: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* sWp,
+                                     const float* sWg, const float* Bp, const float* Bg, void* out, int64_t B,
+                                     int64_t L, int64_t C, int64_t C_out, int64_t ldy, float eps, int dtype,
+                                     void* stream) {
+  return tmu_output_phase_any(y, x, Wp, Wg, sWp, sWg, Bp, Bg, nullptr, out, B, L, C, C_out, ldy, eps, dtype, stream);
+}
+
+extern "C" int tops_tmu_output_phase_residual(const void* y, const void* x, const void* Wp, const void* Wg,
+                                              const float* sWp, const float* sWg, const float* Bp, const float* Bg,
+                                              const void* res, void* out, int64_t B, int64_t L, int64_t C,
+                                              int64_t C_out, int64_t ldy, float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(res, "tops_tmu_output_phase_residual: null residual");
+  TOPS_REQUIRE((uintptr_t)res % 16 == 0 || C != 128, "tops_tmu_output_phase_residual: res must be 16-byte aligned");
+  return tmu_output_phase_any(y, x, Wp, Wg, sWp, sWg, Bp, Bg, res, out, B, L, C, C_out, ldy, eps, dtype, stream);
 }

@@ -236,17 +236,36 @@ def triangle_attn_forward(
     return attention_core(Qp, KV, bias, out, N=N, ldn=ldn, mask=mask)
 
 
-def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
+def _residual_views(o, residual, out, Cout, aligned):
+    """The residual and destination of a fused residual add: (N1, N2, C_out) views with unit channel
+    stride (`out` defaults to a new contiguous tensor; a residual that does not meet the kernel's
+    stride / alignment rules is copied)."""
+    N1, N2 = o.shape[0], o.shape[1]
+    assert residual.shape == (N1, N2, Cout), "residual must be (N1, N2, C_out)"
+    _native.check_device(o, residual, out)
+    if residual.dtype != o.dtype or not aligned(residual):
+        residual = residual.to(o.dtype).contiguous()
+    if out is None:
+        out = torch.empty(N1, N2, Cout, device=o.device, dtype=o.dtype)
+    assert out.shape == (N1, N2, Cout) and out.dtype == o.dtype, "out must be (N1, N2, C_out) of the I/O dtype"
+    assert aligned(out), "out must have unit channel stride (and, at the tuned shape, 16-byte aligned tokens)"
+    return residual, out
+
+
+def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None, residual=None, out=None):
     """out = ((o * sigmoid(g W_g^T + b_g)) -> io) W_o^T + b_o over (N1, N2, C) tokens.
 
     g = gin, or LN(gin) with ln = (w_ln, b_ln, eps).  o and gin may be strided views with unit
-    channel stride.
+    channel stride.  With `residual` ((N1, N2, C_out), any token strides, unit channel stride) the
+    result is residual + out, the add fused into the store; `out` (optional, with `residual`)
+    is the destination view, e.g. a transposed view of a contiguous tensor.
     """
     N1, N2, C = o.shape
     _native.check_device(o, gin, W_g, W_o)
     Cin = gin.shape[-1]
+    assert out is None or residual is not None, "out= is supported together with residual="
     if not (C == 128 and Cin == 128 and W_o.shape[0] == 128) or o.dtype == torch.float32:
-        return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln)
+        return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln, residual=residual, out=out)
     if o.stride(2) != 1 or o.stride(0) % 8 or o.stride(1) % 8 or o.data_ptr() % 16:
         o = o.contiguous()
     gin = gin.reshape(N1, N2, C) if gin.dim() != 3 else gin
@@ -256,35 +275,25 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
     eps = 1e-5
     if ln is not None:
         w_ln, b_ln, eps = ln
-    out = torch.empty(N1, N2, C, device=o.device, dtype=o.dtype)
-    _native.call(
-        "tops_gate_out",
-        o.data_ptr(),
-        o.stride(0),
-        o.stride(1),
-        gin.data_ptr(),
-        gin.stride(0),
-        gin.stride(1),
-        _native.ptr(_as(o, w_ln)),
-        _native.ptr(_as(o, b_ln)),
-        float(eps),
-        1 if ln is not None else 0,
-        _as(o, W_g).data_ptr(),
-        _native.ptr(_as(o, b_g)),
-        _as(o, W_o).data_ptr(),
-        _native.ptr(_as(o, b_o)),
-        out.data_ptr(),
-        N1,
-        N2,
-        C,
-        io_dtype_code(o.dtype),
-        _native.stream_of(o),
-    )
+    args = [o.data_ptr(), o.stride(0), o.stride(1), gin.data_ptr(), gin.stride(0), gin.stride(1),
+            _native.ptr(_as(o, w_ln)), _native.ptr(_as(o, b_ln)), float(eps), 1 if ln is not None else 0,
+            _as(o, W_g).data_ptr(), _native.ptr(_as(o, b_g)), _as(o, W_o).data_ptr(), _native.ptr(_as(o, b_o))]
+    if residual is None:
+        out = torch.empty(N1, N2, C, device=o.device, dtype=o.dtype)
+        _native.call("tops_gate_out", *args, out.data_ptr(), N1, N2, C, io_dtype_code(o.dtype), _native.stream_of(o))
+        return out
+
+    def aligned(t):
+        return t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0
+
+    residual, out = _residual_views(o, residual, out, C, aligned)
+    _native.call("tops_gate_out_residual", *args, residual.data_ptr(), residual.stride(0), residual.stride(1),
+                 out.data_ptr(), out.stride(0), out.stride(1), N1, N2, C, io_dtype_code(o.dtype), _native.stream_of(o))
     return out
 
 
-def _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
-    """gate_out_forward for any (C_in, H*D, C_out) (tops_gate_out_generic)."""
+def _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, *, ln=None, residual=None, out=None):
+    """gate_out_forward for any (C_in, H*D, C_out) (tops_gate_out_generic[_residual])."""
     N1, N2, HD = o.shape
     Cin, Cout = gin.shape[-1], W_o.shape[0]
     assert W_g.shape == (HD, Cin) and W_o.shape == (Cout, HD), "W_g (H*D, C_in) and W_o (C_out, H*D) expected"
@@ -297,32 +306,17 @@ def _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, *, ln=None):
     eps = 1e-5
     if ln is not None:
         w_ln, b_ln, eps = ln
-    out = torch.empty(N1, N2, Cout, device=o.device, dtype=o.dtype)
-    _native.call(
-        "tops_gate_out_generic",
-        o.data_ptr(),
-        o.stride(0),
-        o.stride(1),
-        gin.data_ptr(),
-        gin.stride(0),
-        gin.stride(1),
-        _native.ptr(_as(o, w_ln)),
-        _native.ptr(_as(o, b_ln)),
-        float(eps),
-        1 if ln is not None else 0,
-        _as(o, W_g).data_ptr(),
-        _native.ptr(_as(o, b_g)),
-        _as(o, W_o).data_ptr(),
-        _native.ptr(_as(o, b_o)),
-        out.data_ptr(),
-        N1,
-        N2,
-        Cin,
-        HD,
-        Cout,
-        any_shape_dtype_code(o.dtype),
-        _native.stream_of(o),
-    )
+    args = [o.data_ptr(), o.stride(0), o.stride(1), gin.data_ptr(), gin.stride(0), gin.stride(1),
+            _native.ptr(_as(o, w_ln)), _native.ptr(_as(o, b_ln)), float(eps), 1 if ln is not None else 0,
+            _as(o, W_g).data_ptr(), _native.ptr(_as(o, b_g)), _as(o, W_o).data_ptr(), _native.ptr(_as(o, b_o))]
+    code = any_shape_dtype_code(o.dtype)
+    if residual is None:
+        out = torch.empty(N1, N2, Cout, device=o.device, dtype=o.dtype)
+        _native.call("tops_gate_out_generic", *args, out.data_ptr(), N1, N2, Cin, HD, Cout, code, _native.stream_of(o))
+        return out
+    residual, out = _residual_views(o, residual, out, Cout, lambda t: t.stride(2) == 1)
+    _native.call("tops_gate_out_generic_residual", *args, residual.data_ptr(), residual.stride(0), residual.stride(1),
+                 out.data_ptr(), out.stride(0), out.stride(1), N1, N2, Cin, HD, Cout, code, _native.stream_of(o))
     return out
 
 

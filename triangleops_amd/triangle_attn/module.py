@@ -44,8 +44,13 @@ def precompute(W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, H, D):
     }
 
 
-def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, pad_to=32):
-    """Per-call forward.  X (N, N, C_in) -> (N, N, C_out); mask (N, N), nonzero = valid key."""
+def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, pad_to=32,
+            residual=None, out=None):
+    """Per-call forward.  X (N, N, C_in) -> (N, N, C_out); mask (N, N), nonzero = valid key.
+
+    Optional extras for composing a Pairformer block: `residual` (N, N, C_out) returns
+    residual + result with the add fused into the gate kernel's store; `out` is then the
+    destination view (for the ending node, a transposed view of the untransposed pair tensor)."""
     assert B_proj_g is None and B_proj_o is None, (
         "fused gate path assumes bias-free linear_g / linear_o (K-Fold LinearNoBias)"
     )
@@ -59,12 +64,13 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
         xln, q, k, v, bias = generic_prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], eps=eps)
         O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
         generic_attention(q, k, v, bias, O, scale=scale, mask=mask)
-        return gate_out_forward(O, xln, W_proj_g, None, W_proj_o, None)
+        return gate_out_forward(O, xln, W_proj_g, None, W_proj_o, None, residual=residual, out=out)
     Qp, KV, bias, ldn = prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], scale=scale, eps=eps)
     O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
     attention_core(Qp, KV, bias, O, N=N, ldn=ldn, mask=mask)
     # the gate reads LN(X); it is recomputed from X inside the gate kernel
-    return gate_out_forward(O, X, W_proj_g, None, W_proj_o, None, ln=(pre["W_ln"], pre["B_ln"], eps))
+    return gate_out_forward(O, X, W_proj_g, None, W_proj_o, None, ln=(pre["W_ln"], pre["B_ln"], eps),
+                            residual=residual, out=out)
 
 
 def triangle_attention(

@@ -114,11 +114,14 @@ def output_phase(
     eps,
     *,
     ldy=None,
+    residual=None,
 ):
     """sigmoid(g_out(LN_in x)) * p_out(LN_out y) -> (B, L, L, C_out); y channel-major (C, B, L, ldy).
 
     The kernel reads y rows padded to a multiple of 64 (`ldy`); with the default (y as the
     reference's (C, B, L, L) tensor) a padded copy is made when L is not a multiple of 64.
+    `residual` (B, L, L, C_out): returns residual + result, the add fused into the kernel's store
+    (each sum rounded once, as `residual + result` would be).
     """
     B, L, _, C = x.shape
     C_out = p_out_combined.shape[0]
@@ -139,8 +142,13 @@ def output_phase(
     Wp, Wg = _prep_weights(x, p_out_combined, g_out_combined)
     sWp, sWg, Bp, Bg = _f32(sum_W_p_out, sum_W_g_out, B_p_out_const, B_g_out_const)
     out = torch.empty(B, L, L, C_out, device=x.device, dtype=x.dtype)
+    res = []
+    if residual is not None:
+        assert residual.shape == out.shape, "residual must have the output's shape (B, L, L, C_out)"
+        _native.check_device(x, residual)
+        res = [residual.to(x.dtype).contiguous()]
     _native.call(
-        "tops_tmu_output_phase",
+        "tops_tmu_output_phase_residual" if res else "tops_tmu_output_phase",
         y_t.data_ptr(),
         x.data_ptr(),
         Wp.data_ptr(),
@@ -149,6 +157,7 @@ def output_phase(
         sWg.data_ptr(),
         Bp.data_ptr(),
         Bg.data_ptr(),
+        *[r.data_ptr() for r in res],
         out.data_ptr(),
         B,
         L,

@@ -53,8 +53,11 @@ def precompute(
     }
 
 
-def forward(x, pre, *, direction, mask=None, eps=1e-5):
-    """Per-call forward with precomputed weights.  x (B, L, L, C) -> (B, L, L, C)."""
+def forward(x, pre, *, direction, mask=None, eps=1e-5, residual=None):
+    """Per-call forward with precomputed weights.  x (B, L, L, C) -> (B, L, L, C).
+
+    `residual` (optional extra, e.g. x itself in a Pairformer block): returns residual + result
+    with the add fused into the output phase's store."""
     if direction not in _DIRECTIONS:
         raise ValueError(f"unknown direction: {direction!r} (expected 'outgoing'/'incoming')")
     B, L, _, C = x.shape
@@ -84,6 +87,7 @@ def forward(x, pre, *, direction, mask=None, eps=1e-5):
         pre["B_g_out_const"],
         eps,
         ldy=ld,
+        residual=residual,
     )
 
 
