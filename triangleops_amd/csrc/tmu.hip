@@ -61,7 +61,10 @@ __device__ inline GridTile grid_tile_fast(uint32_t t, const FastDiv& tpr, const 
 //   with whole 128-byte rows (8 features x 64 tokens per store instruction).
 // No wave has loads and stores in flight together; one barrier per tile, and the loaders'
 // LayerNorm of tile n + 1 overlaps the writers' GEMM of tile n.  The LN affine is folded into
-// the weights, so the GEMM of the normalised x gives LN(x) . W^T directly.
+// the weights, so the GEMM of the normalised x gives LN(x) . W^T directly.  The loaders also
+// publish per tile whether every token is masked (the writers then store zeros without the
+// GEMM: padded rows / columns) or every token is valid (no mask multiply); the kernel is
+// bound by the writers' vector work (two transcendentals per output for the gate).
 // ---------------------------------------------------------------------------------------------
 template <typename T, int NWR>
 __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
@@ -76,6 +79,8 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x tiles
   __shared__ __attribute__((aligned(16))) float smask[2][64];
+  // per tile and loader wave: bit 0 = some token of the wave's quarter masked, bit 1 = some valid
+  __shared__ __attribute__((aligned(16))) int tstate[2][4];
   __shared__ __attribute__((aligned(16))) T os[NWR][FW * 64];   // per writer wave: [feature][token]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -107,6 +112,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
     };
     auto step = [&](uint32_t tt, int bb, Stage& sg) {
       const GridTile g = grid_tile_fast(tt, tpr, Ld);
+      uint64_t zero = 0, valid = 0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int tk = 16 * k + tq;
@@ -126,8 +132,12 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
         for (int e = 0; e < 8; ++e) o[e] = (T)((v[e] - mean) * rstd);
         *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ key(tk)) << 4)]) = o;
         // every lane of the token stores the same value: no divergent branch in the loop
-        smask[bb][tk] = g.c0 + tk < L ? (mask ? (float)(sg.mb[k] != 0) : 1.f) : 0.f;
+        const float mv = g.c0 + tk < L ? (mask ? (float)(sg.mb[k] != 0) : 1.f) : 0.f;
+        smask[bb][tk] = mv;
+        zero |= __ballot(mv == 0.f);
+        valid |= __ballot(mv != 0.f);
       }
+      if (lane == 0) tstate[bb][wave] = (zero ? 1 : 0) | (valid ? 2 : 0);
       __syncthreads();  // tile tt staged; the writers are done with the tile before tt - 1
       fetch(tt + PD * G, sg);  // refill this stage
       __builtin_amdgcn_sched_barrier(0);
@@ -174,28 +184,44 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
     int bb = 0;
     for (; t < ntiles; t += G) {
       __syncthreads();  // tile t staged
+      // tile state from the loader waves: every token masked (the outputs are exact zeros, no
+      // GEMM needed), every token valid (no mask multiply) or mixed
+      const int4 ts = *reinterpret_cast<const int4*>(&tstate[bb][0]);
+      const int st = ts.x | ts.y | ts.z | ts.w;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const int tok = sub * 32 + prow;
         const int tb = sub * 32 + 16 * hl;  // first of this lane's 16 tokens
         {
-          f32x16 accP = {}, accG = {};
-#pragma unroll
-          for (int k = 0; k < KS; ++k) {
-            const V8 xa = *reinterpret_cast<const V8*>(&xs[bb][tok * ROW + (((2 * k + hl) ^ key(tok)) << 4)]);
-            accP = Mma<T>::m32(xa, wp[k], accP);
-            accG = Mma<T>::m32(xa, wg[k], accG);
-          }
           V8 o[2];
+          if (st == 1) {
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) {
-            const f32x4 rm = *reinterpret_cast<const f32x4*>(&smask[bb][tb + 4 * gq]);
+            for (int e = 0; e < 8; ++e) o[0][e] = o[1][e] = (T)0.0f;
+          } else {
+            f32x16 accP = {}, accG = {};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int v = 4 * gq + j;
-              const float P = accP[v] + cbp;
-              const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
-              o[v / 8][v % 8] = (T)(P * gate * rm[j]);
+            for (int k = 0; k < KS; ++k) {
+              const V8 xa = *reinterpret_cast<const V8*>(&xs[bb][tok * ROW + (((2 * k + hl) ^ key(tok)) << 4)]);
+              accP = Mma<T>::m32(xa, wp[k], accP);
+              accG = Mma<T>::m32(xa, wg[k], accG);
+            }
+            if (st == 2) {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+                o[v / 8][v % 8] = (T)((accP[v] + cbp) * gate);
+              }
+            } else {
+#pragma unroll
+              for (int gq = 0; gq < 4; ++gq) {
+                const f32x4 rm = *reinterpret_cast<const f32x4*>(&smask[bb][tb + 4 * gq]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  const int v = 4 * gq + j;
+                  const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+                  o[v / 8][v % 8] = (T)((accP[v] + cbp) * gate * rm[j]);
+                }
+              }
             }
           }
           // 16-byte chunks c = tb / 8 + {0, 1} of local feature row ff, XOR-swizzled by (ff >> 1) & 7
