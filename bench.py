@@ -390,6 +390,12 @@ def run_phases(phase_lists, names, iters, warmup):
     return {n: statistics.fmean(a[n] for a in avgs) for n in names}
 
 
+def graph_ms(call, *args, iters=50):
+    """ms per replay of `call(*args)` captured as one HIP graph (triangleops_amd.graph)."""
+    g = tops.graph.capture(call, *args)
+    return time_ms(g.replay, iters, 3)
+
+
 # --------------------------------------------------------------------------- #
 # CPU baseline (fp32 oracle on this host)
 # --------------------------------------------------------------------------- #
@@ -427,6 +433,9 @@ def sweep(path, sizes, dev):
                 kern = {n: kernel_entry(n, ph[n], *tmu_work(L)[n]) for n in ph}
                 r = {"op": "triangle_multiplicative_update", "direction": direction, "size": L, "ms": round(ms, 4),
                      "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": kern}
+                if L <= 512:  # launch-bound sizes: the same call replayed as one HIP graph
+                    r["ms_graph"] = round(graph_ms(
+                        lambda xx: tops.triangle_mul.forward(xx, pre, direction=direction, mask=m), x), 4)
                 f.write(json.dumps(r) + "\n")
                 f.flush()
                 rows.append(r)
@@ -449,6 +458,10 @@ def sweep(path, sizes, dev):
             kern = {n: kernel_entry(n, ph[n], *tri_work(N)[n]) for n in ph}
             r = {"op": "triangle_attention", "size": N, "ms": round(ms, 4), "ms_ending_node": round(ms_end, 4),
                  "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": kern}
+            if N <= 512:
+                r["ms_graph"] = round(graph_ms(lambda X: tops.triangle_attn.forward(
+                    X, pre, mask=d["mask"], scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=None,
+                    W_proj_o=d["W_proj_o"], B_proj_o=None), d["X"]), 4)
             f.write(json.dumps(r) + "\n")
             f.flush()
             rows.append(r)
@@ -467,6 +480,10 @@ def sweep(path, sizes, dev):
             kern = {n: kernel_entry(n, ph[n], *apb_work(M)[n]) for n in ph}
             r = {"op": "attention_pair_bias", "size": M, "ms": round(ms, 4), "calls_per_s": round(1e3 / ms, 1),
                  "torch_path_ms": round(tms, 4), "kernels": kern}
+            if M <= 512:
+                r["ms_graph"] = round(graph_ms(lambda X, Z: tops.attn_pair_bias.forward(
+                    X, Z, pre, scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"],
+                    B_proj_o=d["B_proj_o"], mask=d["mask"]), d["X"], d["Z"]), 4)
             f.write(json.dumps(r) + "\n")
             f.flush()
             rows.append(r)
@@ -516,6 +533,8 @@ def sweep(path, sizes, dev):
             tms = time_ms(lambda: torch_pair_stack(z, pm, w_out, w_in, ts, te), max(3, it // 4), 1)
             r = {"op": "pairformer_pair_stack", "size": N, "ms": round(ms, 4), "ms_unfused_adds": round(ms_unf, 4),
                  "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4), "kernels": {}}
+            if N <= 512:
+                r["ms_graph"] = round(graph_ms(lambda zz: tops.pairformer.pair_stack(zz, pre, pair_mask=pm), z), 4)
             f.write(json.dumps(r) + "\n")
             f.flush()
             rows.append(r)

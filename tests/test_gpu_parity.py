@@ -565,6 +565,77 @@ def test_pairformer_block(device):
 
 
 # --------------------------------------------------------------------------- #
+# HIP graph replay of whole calls (launch-bound small sizes)
+# --------------------------------------------------------------------------- #
+def _graph_check(device, call, fresh, n_replays=3):
+    """Capture call(*inputs), then per replay: copy fresh values into the captured inputs, replay,
+    run the same call eagerly (work between the replays) and compare bitwise."""
+    inputs = fresh(0)
+    g = tops.graph.capture(call, *inputs)
+    for r in range(1, n_replays + 1):
+        new = fresh(r)
+        for dst, src in zip(g.inputs, new):
+            dst.copy_(src)
+        out = g.replay().clone()
+        torch.cuda.synchronize()
+        eager = call(*new)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r} differs from the eager call"
+
+
+def test_graph_replay_tmu(device):
+    x, m, w = tmu_inputs(96, mask="pad")
+    w = to_dev(w, device)
+    pre = tops.triangle_mul.precompute(*(w[k] for k in ("norm_in_weight", "norm_in_bias", "p_in_weight",
+                                                        "g_in_weight", "norm_out_weight", "norm_out_bias",
+                                                        "p_out_weight", "g_out_weight")))
+    m = m.to(device)
+
+    def call(xx):
+        return tops.triangle_mul.forward(xx, pre, direction="incoming", mask=m)
+
+    _graph_check(device, call, lambda r: [tmu_inputs(96, seed=100 + r)[0].to(device)])
+
+
+def test_graph_replay_tri_and_apb(device):
+    d = to_dev(tri_inputs(80, mask="pad"), device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], d["H"], d["D"])
+
+    def tri(X):
+        return tops.triangle_attn.forward(X, pre, mask=d["mask"], scale=d["scale"], W_proj_g=d["W_proj_g"],
+                                          B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None)
+
+    _graph_check(device, tri, lambda r: [tri_inputs(80, seed=200 + r)["X"].to(device)])
+    a = to_dev(apb_inputs(96, mask="pad", biases=True), device)
+    pa = tops.attn_pair_bias.precompute(a["WQ"], a["WK"], a["WV"], a["W_ln"], a["B_ln"], a["W_proj_z"],
+                                        a["B_proj_z"], a["H"], a["D"])
+
+    def apb(X, Z):
+        return tops.attn_pair_bias.forward(X, Z, pa, scale=a["scale"], W_proj_g=a["W_proj_g"],
+                                           B_proj_g=a["B_proj_g"], W_proj_o=a["W_proj_o"], B_proj_o=a["B_proj_o"],
+                                           mask=a["mask"])
+
+    def fresh(r):
+        f = apb_inputs(96, seed=300 + r)
+        return [f["X"].to(device), f["Z"].to(device)]
+
+    _graph_check(device, apb, fresh)
+
+
+def test_graph_replay_pair_stack(device):
+    z, pm, tmu_o, tmu_i, ts, te, H, D = _block_inputs(64, seed=9)
+    dd = lambda w: {k: v.to(device) for k, v in w.items()}  # noqa: E731
+    pre = tops.pairformer.precompute(dd(tmu_o), dd(tmu_i), dd(ts), dd(te), H=H, D=D)
+    pm = pm.to(device)
+
+    def call(zz):
+        return tops.pairformer.pair_stack(zz, pre, pair_mask=pm)
+
+    _graph_check(device, call, lambda r: [_block_inputs(64, seed=40 + r)[0].to(device)])
+
+
+# --------------------------------------------------------------------------- #
 # golden fixtures (brute-force float64 expected outputs, tests/golden)
 # --------------------------------------------------------------------------- #
 def _golden(name):

@@ -12,13 +12,14 @@ and a one-shot `<op_name>(...)`:
 `attn_pair_bias.attention_pair_bias_qknorm` adds the K-Fold variant the reference states only in
 torch (`benchmarks/references.py:230-277`: Q bias, LayerNorm over H*D of Q and K, key mask), and
 `pairformer` composes the ops into a Pairformer block's pair stack and single update with the
-residual adds fused into the output kernels.
+residual adds fused into the output kernels, and `graph.capture` replays a fixed-shape call as
+one HIP graph (for the launch-bound small sizes).
 
 All compute runs in `libtriangleops_amd.so` (HIP, gfx950) through a C ABI
 (`include/triangleops_amd.h`); there is no CPU or fallback path.
 """
 
-from . import attn_pair_bias, pairformer, triangle_attn, triangle_mul
+from . import attn_pair_bias, graph, pairformer, triangle_attn, triangle_mul
 from .attn_pair_bias import attention_pair_bias
 from .triangle_attn import triangle_attention
 from .triangle_mul import triangle_multiplicative_update
