@@ -48,7 +48,7 @@ static ApbSplit apb_split(int64_t M) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ Qm, const T* __restrict__ Km,
+__global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ Qm, const T* __restrict__ Km,
                                                       const T* __restrict__ Vm,
                                                       const T* __restrict__ Z, int64_t sz0, int64_t sz1,
                                                       const float* __restrict__ Wc, const float* __restrict__ sWc,
@@ -120,17 +120,20 @@ __global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ Qm,
     if (kbits == 0) continue;  // block-uniform
 
     // ---- pair bias for the 32 x 32 (query, key) tile: wave w -> queries 8w .. 8w+7 ----
-#pragma unroll 1
-    for (int u = 0; u < 16; ++u) {
+    // step u covers query 8w + u / 2 and keys 16 (u % 2) .. +15; the Z slice of step u + 1 is
+    // loaded while step u is reduced (two register sets, so a load is always in flight)
+    auto zload = [&](int u, V8* za) {
       const int lq = 8 * wave + (u >> 1), kh = u & 1;
       int64_t q = q0 + lq;
       q = q < M ? q : M - 1;
       int64_t key = k0 + 16 * kh + l16;
       key = key < M ? key : M - 1;
       const T* zr = Z + q * sz0 + key * sz1 + 8 * g16;
-      V8 za[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) za[s] = ldg<V8>(zr + 32 * s);
+    };
+    auto zbias = [&](int u, const V8* za) {
+      const int lq = 8 * wave + (u >> 1), kh = u & 1;
       float sum = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
@@ -161,6 +164,17 @@ __global__ __launch_bounds__(256) void apb_attn_kernel(const T* __restrict__ Qm,
         const float mu = __shfl(mean, 4 * g16 + v);
         const float rs = __shfl(rstd, 4 * g16 + v);
         if (l16 < H) bias_s[l16][lq * kApbBRow + 16 * kh + 4 * g16 + v] = rs * (acc[v] - mu * my_swc) + my_bc;
+      }
+    };
+    {
+      V8 za[4], zb[4];
+      zload(0, za);
+#pragma unroll 1
+      for (int u = 0; u < 16; u += 2) {
+        zload(u + 1, zb);
+        zbias(u, za);
+        if (u + 2 < 16) zload(u + 2, za);
+        zbias(u + 1, zb);
       }
     }
 
