@@ -161,6 +161,30 @@ def test_tmu_config_sizes_sampled_rows(device, L, direction):
     _check(out[:, rows].cpu(), expect, torch.bfloat16, f"tmu L={L} {direction}")
 
 
+@pytest.mark.parametrize("L,nslab,dtype", [(400, 8, torch.bfloat16), (600, 64, torch.bfloat16),
+                                           (768, 4, torch.bfloat16), (1000, 32, torch.bfloat16),
+                                           (1024, 40, torch.bfloat16), (600, 64, torch.float16)])
+def test_tmu_einsum_large_kernels(device, L, nslab, dtype):
+    """The L > 384 einsum kernels against a torch fp32 product of the same 16-bit operands: odd
+    k-tile counts (L = 400), rows past L in the last block tile (L = 600, 1000), fewer block tiles
+    than CUs (L = 768) and several block tiles per persistent block with an uneven split
+    (L = 600, 1024).  Each output is the fp32 sum rounded once: within half an ulp of the 16-bit
+    type plus the fp32 summation-order difference."""
+    ld = (L + 63) // 64 * 64
+    g = torch.Generator().manual_seed(L + nslab)
+    ab = torch.zeros(2 * nslab, 1, L, ld, dtype=dtype)
+    ab[..., :L] = torch.randn(2 * nslab, 1, L, L, generator=g).to(dtype)
+    ab = ab.to(device)
+    y = tops.triangle_mul.triangle_einsum(ab, L, ld, nslab, 1)
+    a, b = ab[:nslab, 0].float(), ab[nslab:, 0].float()
+    expect = torch.bmm(a, b.transpose(1, 2).contiguous())  # fp32 on the GPU
+    half_ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err = (y[:, 0, :, :L].float() - expect[:, :, :L]).abs()
+    bound = half_ulp * expect[:, :, :L].abs() + 1e-5 * expect.abs().max()
+    assert bool((err <= bound).all()), f"L={L} nslab={nslab}: max excess {float((err - bound).max()):.3e}"
+    assert bool(torch.isfinite(y[..., L:].float()).all()), "padding columns must be finite"
+
+
 # --------------------------------------------------------------------------- #
 # triangle_attention
 # --------------------------------------------------------------------------- #
