@@ -577,6 +577,192 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------------------------------------
+// Einsum, large L, persistent: the k-tile pipeline of tmu_einsum_large_kernel (the same LDS
+// layout, loads and fragment reads) run by one block per CU over the block tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... without draining between tiles: the last two k-tiles of a tile load
+// the next tile's first two, and the tile's output stores are issued while those loads are in
+// flight, so neither the next tile's first load nor a block launch is waited for (each cost
+// ~2.4 / ~0.6 us per 256 x 256 tile, against ~32 us of k-loop at L = 1024).  The first k-step of
+// a tile starts from zero accumulators.  Requires L % 256 == 0 (no row of a block tile lies past
+// L) and an even k-tile count (two static stages per tile); with gridDim.x a multiple of 8 block
+// tile t stays on XCD t % 8 under the XCD-major tile order.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+                                                                T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
+                                                                int64_t nslab, int tiles) {
+  constexpr int BM = 256, BK = 64, MI = 4, NJ = 4;
+  constexpr int TILE = BM * BK;
+  using V8 = vec<T, 8>;
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+
+  __shared__ __attribute__((aligned(16))) T As0[TILE], As1[TILE];
+  __shared__ __attribute__((aligned(16))) T Bs0[TILE], Bs1[TILE];
+  auto abuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? As0 : As1; };
+  auto bbuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? Bs0 : Bs1; };
+
+  // tile counts fit 32 bits (checked by the launcher): 32-bit index arithmetic
+  const uint32_t total = (uint32_t)(nslab * tiles * tiles);
+  const uint32_t tt = (uint32_t)tiles * (uint32_t)tiles;
+  // block tile t -> (slab, tm, tn), XCD-major (tiles of one XCD contiguous)
+  auto coords = [&](uint32_t t, int64_t& slab, int& tm, int& tn) {
+    uint32_t id = t;
+    if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+    slab = (int64_t)(id / tt);
+    const uint32_t rem = id % tt;
+    tm = (int)(rem / (uint32_t)tiles);
+    tn = (int)(rem % (uint32_t)tiles);
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hl = lane >> 5, col = lane & 31;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+  auto swa = [](int row) { return (row >> 1) & 7; };
+  auto swb = [](int row) { return ((row >> 1) & 3) | ((row >> 2) & 4); };
+
+  const int nk = (int)(ld / BK);
+  // loads: wave w, instruction j < 8 fills LDS bytes [(8 w + j) KB, +1 KB) of an operand's tile,
+  // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + i / 8, physical chunk i % 8 <-
+  // logical chunk (i % 8) ^ swz(r).  L % 256 == 0, so every block tile's rows lie inside its
+  // slab: the lane offsets are the same for every tile, only the scalar bases change.
+  uint32_t aoff[8], boff[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = 8 * (8 * wave + j) + (lane >> 3), cp = lane & 7;
+    aoff[j] = (uint32_t)((r * ld + 8 * (cp ^ swa(r))) * (int64_t)sizeof(T));
+    boff[j] = (uint32_t)((r * ld + 8 * (cp ^ swb(r))) * (int64_t)sizeof(T));
+  }
+  const char* abase;
+  const char* bbase;
+  auto setup = [&](uint32_t t) {
+    int64_t slab;
+    int tm, tn;
+    coords(t, slab, tm, tn);
+    abase = reinterpret_cast<const char*>(A + (slab * L + (int64_t)tm * BM) * ld);
+    bbase = reinterpret_cast<const char*>(Bmat + (slab * L + (int64_t)tn * BM) * ld);
+  };
+  auto gload = [&](int kt, auto S) {
+    const char* ak = abase + (int64_t)kt * BK * sizeof(T);
+    const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
+    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 8 * 1024);
+    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 8 * 1024);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t va = aoff[j], vb = boff[j], ma = as + 1024 * j, mb = bs + 1024 * j;
+      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
+      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
+    }
+  };
+  struct Frags {
+    V8 a[MI], b[NJ];
+  };
+  auto frags = [&](auto S, int ks, Frags& f) {
+    const T* as = abuf(S);
+    const T* bs = bbuf(S);
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int row = wm * 128 + 32 * i + col;
+      f.a[i] = *reinterpret_cast<const V8*>(&as[row * BK + (((2 * ks + hl) ^ swa(row)) << 3)]);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int row = wn * 128 + 32 * j + prow;
+      f.b[j] = *reinterpret_cast<const V8*>(&bs[row * BK + (((2 * ks + hl) ^ swb(row)) << 3)]);
+    }
+  };
+
+  f32x16 acc[NJ][MI];
+  auto mfmas = [&](const Frags& f, auto first) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        acc[j][i] = Mma<T>::m32(f.b[j], f.a[i], decltype(first)::value ? f32x16{} : acc[j][i]);
+  };
+  auto interleave = [] {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  const uint32_t G = gridDim.x;
+  Frags fa, fb;
+  uint32_t t = blockIdx.x;
+  bool has_next = false;
+  auto ktile = [&](int kt, auto S, auto first) {
+    using N = std::integral_constant<int, 1 - decltype(S)::value>;
+    using NO = std::false_type;
+    mfmas(fa, first);
+    frags(S, 1, fb);
+    interleave();
+    mfmas(fb, NO{});
+    frags(S, 2, fa);
+    interleave();
+    mfmas(fa, NO{});
+    frags(S, 3, fb);
+    interleave();
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 2 < nk) {
+      gload(kt + 2, S);
+    } else if (has_next) {  // the next block tile's k-tiles 0 and 1
+      if (kt + 2 == nk) setup(t + G);
+      gload(kt + 2 - nk, S);
+    }
+    mfmas(fb, NO{});
+    frags(N{}, 0, fa);  // after the block's last k-tile: stale contents, never used
+    interleave();
+  };
+
+  setup(t);
+  gload(0, S0{});
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (1 < nk) gload(1, S1{});
+  frags(S0{}, 0, fa);
+  for (; t < total; t += G) {
+    has_next = t + G < total;
+    ktile(0, S0{}, std::true_type{});
+    ktile(1, S1{}, std::false_type{});
+    for (int kt = 2; kt < nk; kt += 2) {
+      ktile(kt, S0{}, std::false_type{});
+      ktile(kt + 1, S1{}, std::false_type{});
+    }
+    // ---- Y[i][j0 .. j0 + 15] per lane: two 16-byte stores (columns [L, ldy) get finite filler) ----
+    int64_t slab;
+    int tm, tn;
+    coords(t, slab, tm, tn);
+    T* Yb = Y + slab * L * ldy;
+    unsigned t2 = threadIdx.x;
+    asm volatile("" : "+v"(t2));
+    const int ecol = (int)(t2 & 31), ehl = (int)((t2 >> 5) & 1);
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int64_t ii = (int64_t)tm * BM + wm * 128 + i * 32 + ecol;
+      if (ii < L) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * ehl;
+          if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
+          V8 o0, o1;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            o0[e] = (T)acc[j][i][e];
+            o1[e] = (T)acc[j][i][8 + e];
+          }
+          stg<V8>(Yb + ii * ldy + j0, o0);
+          stg<V8>(Yb + ii * ldy + j0 + 8, o1);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Output phase (C = C_out = 128).  64-token tiles, 12 waves in two roles:
 //   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
@@ -823,8 +1009,16 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
   if (L > 384) {
     const int t = (int)((L + 255) / 256);
     const int64_t grid = nslab * t * t;
-    hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld, ldy,
-                       nslab, t);
+    const int64_t cus = num_cus() / 8 * 8;
+    if (L % 256 == 0 && (ld / 64) % 2 == 0 && grid < (1LL << 31) && cus >= 8) {
+      // persistent: one block per CU (a multiple of 8 blocks, so each block stays on one XCD's tiles)
+      const int64_t pg = grid < cus ? grid : cus;
+      hipLaunchKernelGGL((tmu_einsum_persist_kernel<T>), dim3((unsigned)pg), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
+                         ldy, nslab, t);
+    } else {
+      hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
+                         ldy, nslab, t);
+    }
   } else {
     const int t = (int)((L + 127) / 128);
     const int64_t grid = nslab * t * t;
