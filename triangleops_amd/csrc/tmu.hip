@@ -482,19 +482,16 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   struct Frags {
     V8 a[MI], b[NJ];
   };
+  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 128 + 32 j + prow); neither swizzle
+  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all four
+  // fragments, which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
-    const T* as = abuf(S);
-    const T* bs = bbuf(S);
+    const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
+    const T* bs = bbuf(S) + (wn * 128 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int row = wm * 128 + 32 * i + col;
-      f.a[i] = *reinterpret_cast<const V8*>(&as[row * BK + (((2 * ks + hl) ^ swa(row)) << 3)]);
-    }
+    for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(as + 32 * i * BK);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int row = wn * 128 + 32 * j + prow;
-      f.b[j] = *reinterpret_cast<const V8*>(&bs[row * BK + (((2 * ks + hl) ^ swb(row)) << 3)]);
-    }
+    for (int j = 0; j < NJ; ++j) f.b[j] = *reinterpret_cast<const V8*>(bs + 32 * j * BK);
   };
 
   f32x16 acc[NJ][MI];
@@ -658,19 +655,16 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
   struct Frags {
     V8 a[MI], b[NJ];
   };
+  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 128 + 32 j + prow); neither swizzle
+  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all four
+  // fragments, which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
-    const T* as = abuf(S);
-    const T* bs = bbuf(S);
+    const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
+    const T* bs = bbuf(S) + (wn * 128 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
-      const int row = wm * 128 + 32 * i + col;
-      f.a[i] = *reinterpret_cast<const V8*>(&as[row * BK + (((2 * ks + hl) ^ swa(row)) << 3)]);
-    }
+    for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(as + 32 * i * BK);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int row = wn * 128 + 32 * j + prow;
-      f.b[j] = *reinterpret_cast<const V8*>(&bs[row * BK + (((2 * ks + hl) ^ swb(row)) << 3)]);
-    }
+    for (int j = 0; j < NJ; ++j) f.b[j] = *reinterpret_cast<const V8*>(bs + 32 * j * BK);
   };
 
   f32x16 acc[NJ][MI];
