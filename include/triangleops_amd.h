@@ -48,10 +48,11 @@ int tops_tmu_input_phase(const void* x, const void* mask, const void* Wp, const 
 /*
  * triangle_multiplicative_update, triangle einsum (replaces the torch.einsum calls at
  * triangle_mul/module.py:80-84).  For every channel-batch slab s < nslab:
- *   y[s*L*ldy + i*ldy + j] = sum_{k < ld} a[s*L*ld + i*ld + k] * b[s*L*ld + j*ld + k]
+ *   y[s*L*ldy + i*ldy + j] = sum_{k < L} a[s*L*ld + i*ld + k] * b[s*L*ld + j*ld + k]
  * with a = ab, b = ab + nslab*L*ld, for i, j < L.  ld and ldy must be multiples of 64 and
- * the columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them); columns
- * [L, ldy) of y receive unspecified finite values.  Outgoing feeds the natural token grid,
+ * the columns k in [L, ld) must hold zeros (tops_tmu_input_phase writes them; the product
+ * reads k < round_up(L, 64) only, so ld may exceed that as a row padding); columns [L, ldy) of
+ * y receive unspecified finite values.  Outgoing feeds the natural token grid,
  * incoming the transposed one (transpose=1 above).  fp32 I/O runs an fp32 VALU product.
  */
 int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,

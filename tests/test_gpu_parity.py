@@ -163,12 +163,13 @@ def test_tmu_config_sizes_sampled_rows(device, L, direction):
 
 @pytest.mark.parametrize("L,nslab,dtype", [(400, 8, torch.bfloat16), (600, 64, torch.bfloat16),
                                            (768, 4, torch.bfloat16), (1000, 32, torch.bfloat16),
-                                           (1024, 40, torch.bfloat16), (600, 64, torch.float16)])
+                                           (1024, 40, torch.bfloat16), (600, 64, torch.float16),
+                                           (768, 4, torch.float16)])
 def test_tmu_einsum_large_kernels(device, L, nslab, dtype):
     """The L > 384 einsum kernels against a torch fp32 product of the same 16-bit operands: odd
-    k-tile counts (L = 400), rows past L in the last block tile (L = 600, 1000), fewer block tiles
-    than CUs (L = 768) and several block tiles per persistent block with an uneven split
-    (L = 600, 1024).  Each output is the fp32 sum rounded once: within half an ulp of the 16-bit
+    k-tile counts (L = 400), rows past L in the last block tile (L = 600, 1000), and the
+    persistent kernel (L % 256 == 0) with fewer block tiles than CUs (L = 768) and with several
+    block tiles per block in an uneven split (L = 1024, 640 tiles).  Each output is the fp32 sum rounded once: within half an ulp of the 16-bit
     type plus the fp32 summation-order difference."""
     ld = (L + 63) // 64 * 64
     g = torch.Generator().manual_seed(L + nslab)
@@ -183,6 +184,24 @@ def test_tmu_einsum_large_kernels(device, L, nslab, dtype):
     bound = half_ulp * expect[:, :, :L].abs() + 1e-5 * expect.abs().max()
     assert bool((err <= bound).all()), f"L={L} nslab={nslab}: max excess {float((err - bound).max()):.3e}"
     assert bool(torch.isfinite(y[..., L:].float()).all()), "padding columns must be finite"
+
+
+@pytest.mark.parametrize("L,nslab,pad,dtype", [(1024, 8, 128, torch.bfloat16), (600, 16, 64, torch.bfloat16),
+                                               (200, 8, 64, torch.float16), (100, 4, 64, torch.float32)])
+def test_tmu_einsum_row_padding_not_read(device, L, nslab, pad, dtype):
+    """The product reads k < round_up(L, 64) only: a row stride ld beyond that is pure padding,
+    here filled with NaN, and the result equals the one with ld = round_up(L, 64) bit for bit
+    (persistent, large, small and fp32 kernels)."""
+    lr = (L + 63) // 64 * 64
+    g = torch.Generator().manual_seed(L)
+    vals = torch.randn(2 * nslab, 1, L, L, generator=g).to(dtype)
+    tight = torch.zeros(2 * nslab, 1, L, lr, dtype=dtype)
+    tight[..., :L] = vals
+    padded = torch.full((2 * nslab, 1, L, lr + pad), float("nan"), dtype=dtype)
+    padded[..., :lr] = tight
+    y0 = tops.triangle_mul.triangle_einsum(tight.to(device), L, lr, nslab, 1)
+    y1 = tops.triangle_mul.triangle_einsum(padded.to(device), L, lr + pad, nslab, 1)
+    assert torch.equal(y0[..., :L], y1[..., :L])
 
 
 # --------------------------------------------------------------------------- #

@@ -386,7 +386,8 @@ __global__ __launch_bounds__(256) void tmu_generic_in_kernel(const T* __restrict
   }
 }
 
-// fp32 batched product: per slab s, Y[i][j] = sum_k A[i][k] B[j][k], k < ld (A, B zero-padded).
+// fp32 batched product: per slab s, Y[i][j] = sum_k A[i][k] B[j][k] over k < round_up(L, 64)
+// (the columns [L, ld) are zero; those past round_up(L, 64) are row padding and not read).
 __global__ __launch_bounds__(256) void tmu_generic_einsum_kernel(const float* __restrict__ A,
                                                                 const float* __restrict__ Bm, float* __restrict__ Y,
                                                                 int64_t L, int64_t ld, int64_t ldy, int tiles) {
@@ -399,7 +400,8 @@ __global__ __launch_bounds__(256) void tmu_generic_einsum_kernel(const float* __
   const float* Bb = Bm + slab * L * ld;
   const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
   float acc[4][4] = {};
-  for (int64_t k0 = 0; k0 < ld; k0 += TK) {
+  const int64_t kend = (L + 63) / 64 * 64;  // <= ld
+  for (int64_t k0 = 0; k0 < kend; k0 += TK) {
     for (int e = tid; e < TM * TK; e += 256) {
       const int r = e / TK, k = e % TK;
       const int64_t ia = (int64_t)tm * TM + r, ib = (int64_t)tn * TM + r;

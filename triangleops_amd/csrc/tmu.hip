@@ -349,7 +349,7 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 
   // Branch-free k-tile body (the last k-tile reloads itself into the unused buffer), scheduled
   // explicitly: fragments of k-step ks + 1 are read from LDS before the MFMAs of ks issue.
-  const int nk = (int)(ld / BK);
+  const int nk = (int)((L + BK - 1) / BK);  // k-tiles holding a k < L (the rest of the row is zero)
   gload(0);
   sstore(0);
   __syncthreads();
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + lane / 8, physical chunk lane % 8
   // <- logical chunk (lane % 8) ^ swz(r).  Rows past L reload row L - 1 (their products are never
   // stored).
-  const int nk = (int)(ld / BK);
+  const int nk = (int)((L + BK - 1) / BK);  // k-tiles holding a k < L (the rest of the row is zero)
   const char* abase = reinterpret_cast<const char*>(Ab + (int64_t)tm * BM * ld);
   const char* bbase = reinterpret_cast<const char*>(Bb + (int64_t)tn * BM * ld);
   uint32_t aoff[8], boff[8];
@@ -619,7 +619,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
   auto swa = [](int row) { return (row >> 1) & 7; };
   auto swb = [](int row) { return ((row >> 1) & 3) | ((row >> 2) & 4); };
 
-  const int nk = (int)(ld / BK);
+  const int nk = (int)((L + BK - 1) / BK);  // k-tiles holding a k < L (the rest of the row is zero)
   // loads: wave w, instruction j < 8 fills LDS bytes [(8 w + j) KB, +1 KB) of an operand's tile,
   // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + i / 8, physical chunk i % 8 <-
   // logical chunk (i % 8) ^ swz(r).  L % 256 == 0, so every block tile's rows lie inside its
@@ -1004,7 +1004,7 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
     const int t = (int)((L + 255) / 256);
     const int64_t grid = nslab * t * t;
     const int64_t cus = num_cus() / 8 * 8;
-    if (L % 256 == 0 && (ld / 64) % 2 == 0 && grid < (1LL << 31) && cus >= 8) {
+    if (L % 256 == 0 && (L / 64) % 2 == 0 && grid < (1LL << 31) && cus >= 8) {
       // persistent: one block per CU (a multiple of 8 blocks, so each block stays on one XCD's tiles)
       const int64_t pg = grid < cus ? grid : cus;
       hipLaunchKernelGGL((tmu_einsum_persist_kernel<T>), dim3((unsigned)pg), dim3(256), 0, st, A, Bm, (T*)y, L, ld,

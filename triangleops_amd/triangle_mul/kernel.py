@@ -85,7 +85,8 @@ def triangle_einsum(ab, L, ld, C, B):
     """y[d, b, i, j] = sum_k a[d, b, i, k] b[d, b, j, k] over the (2C, B, L, ld) tensor ab.
 
     `ld` must be a multiple of 64 with zero columns [L, ld) (as `input_phase(..., ld=ld)`
-    writes them).  Returns y as (C, B, L, ld); columns [L, ld) are left unwritten.
+    writes them); only k < round_up(L, 64) is read, so ld may carry extra row padding.
+    Returns y as (C, B, L, ld); columns [L, ld) are left unspecified.
     """
     y = torch.empty(C, B, L, ld, device=ab.device, dtype=ab.dtype)
     _native.call(
