@@ -4,7 +4,9 @@
 //                    ("D-major") so every channel is an L x L matrix for the einsum.
 //                    Incoming writes the token grid transposed, so the einsum is always
 //                    y = A . B^T with k contiguous in both operands.
-//   tmu_einsum       batched bf16/f16 MFMA GEMM, one slab per channel: y = A . B^T.
+//   tmu_einsum       batched bf16/f16 MFMA GEMM, one slab per channel: y = A . B^T
+//                    (256 x 256 tiles for L > 384, persistent when L % 256 == 0; 128 x 128
+//                    tiles below).
 //   tmu_out_kernel   LN_out(y) . Wp^T gated by sigmoid(LN_in(x) . Wg^T), token-major output.
 //
 // Reference: triangle_mul/kernel.py:54-162 (fused LN + gated projection), :235-326 (phase
@@ -402,7 +404,8 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 }
 
 // ---------------------------------------------------------------------------------------------
-// Einsum, large L: 256 x 256 block tile, 4 waves of 128 x 128 (accumulators in AGPRs), k-tile 64,
+// Einsum, large L (L > 384; the persistent variant below runs the same pipeline when L % 256 == 0):
+// 256 x 256 block tile, 4 waves of 128 x 128 (accumulators in AGPRs), k-tile 64,
 // operands copied from HBM / L2 straight into LDS with global_load_lds (no staging registers, no
 // LDS store instructions), double-buffered.  One load instruction fills 1 KB of LDS in lane order
 // and covers 8 rows x 128 bytes, i.e. 8 whole cache lines: a footprint of half lines (k-tile 32)
