@@ -578,7 +578,9 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
 
 // ---------------------------------------------------------------------------------------------
 // Einsum, large L, persistent: the k-tile pipeline of tmu_einsum_large_kernel (the same LDS
-// layout, loads and fragment reads) run by one block per CU over the block tiles blockIdx.x,
+// layout, loads and fragment swizzles) with 8 waves of 128 x 64 (2 x 4; accumulators in VGPRs,
+// 218 registers, so two waves share each SIMD and one issues MFMAs while the other waits on its
+// fragment reads or loads), run by one block per CU over the block tiles blockIdx.x,
 // blockIdx.x + gridDim.x, ... without draining between tiles: the last two k-tiles of a tile load
 // the next tile's first two, and the tile's output stores are issued while those loads are in
 // flight, so neither the next tile's first load nor a block launch is waited for (each cost
@@ -588,10 +590,10 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
 // tile t stays on XCD t % 8 under the XCD-major tile order.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+__global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
                                                                 T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
                                                                 int64_t nslab, int tiles) {
-  constexpr int BM = 256, BK = 64, MI = 4, NJ = 4;
+  constexpr int BM = 256, BK = 64, MI = 4, NJ = 2;
   constexpr int TILE = BM * BK;
   using V8 = vec<T, 8>;
   using S0 = std::integral_constant<int, 0>;
@@ -617,20 +619,20 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5, col = lane & 31;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;  // 8 waves: 2 x 4 of 128 x 64
   const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
   auto swa = [](int row) { return (row >> 1) & 7; };
   auto swb = [](int row) { return ((row >> 1) & 3) | ((row >> 2) & 4); };
 
   const int nk = (int)((L + BK - 1) / BK);  // k-tiles holding a k < L (the rest of the row is zero)
-  // loads: wave w, instruction j < 8 fills LDS bytes [(8 w + j) KB, +1 KB) of an operand's tile,
-  // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + i / 8, physical chunk i % 8 <-
-  // logical chunk (i % 8) ^ swz(r).  L % 256 == 0, so every block tile's rows lie inside its
+  // loads: wave w < 8, instruction j < 4 fills LDS bytes [(4 w + j) KB, +1 KB) of an operand's
+  // tile, lane i writing 16 bytes at m0 + 16 i: row r = 8 (4 w + j) + i / 8, physical chunk i % 8
+  // <- logical chunk (i % 8) ^ swz(r).  L % 256 == 0, so every block tile's rows lie inside its
   // slab: the lane offsets are the same for every tile, only the scalar bases change.
-  uint32_t aoff[8], boff[8];
+  uint32_t aoff[4], boff[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = 8 * (8 * wave + j) + (lane >> 3), cp = lane & 7;
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * (4 * wave + j) + (lane >> 3), cp = lane & 7;
     aoff[j] = (uint32_t)((r * ld + 8 * (cp ^ swa(r))) * (int64_t)sizeof(T));
     boff[j] = (uint32_t)((r * ld + 8 * (cp ^ swb(r))) * (int64_t)sizeof(T));
   }
@@ -646,10 +648,10 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
   auto gload = [&](int kt, auto S) {
     const char* ak = abase + (int64_t)kt * BK * sizeof(T);
     const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
-    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 8 * 1024);
-    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 8 * 1024);
+    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 4 * 1024);
+    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 4 * 1024);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const uint32_t va = aoff[j], vb = boff[j], ma = as + 1024 * j, mb = bs + 1024 * j;
       asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
       asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
@@ -663,7 +665,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
   // fragments, which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
     const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
-    const T* bs = bbuf(S) + (wn * 128 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
+    const T* bs = bbuf(S) + (wn * 64 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
 #pragma unroll
     for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(as + 32 * i * BK);
 #pragma unroll
@@ -680,11 +682,11 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
   };
   auto interleave = [] {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < 6; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -743,7 +745,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_persist_kernel(const T* __rest
       if (ii < L) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * ehl;
+          const int64_t j0 = (int64_t)tn * BM + wn * 64 + j * 32 + 16 * ehl;
           if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
           V8 o0, o1;
 #pragma unroll
@@ -1008,9 +1010,10 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
     const int64_t grid = nslab * t * t;
     const int64_t cus = num_cus() / 8 * 8;
     if (L % 256 == 0 && (L / 64) % 2 == 0 && grid < (1LL << 31) && cus >= 8) {
-      // persistent: one block per CU (a multiple of 8 blocks, so each block stays on one XCD's tiles)
+      // persistent: one 8-wave block per CU (a multiple of 8 blocks, so each block stays on one
+      // XCD's tiles)
       const int64_t pg = grid < cus ? grid : cus;
-      hipLaunchKernelGGL((tmu_einsum_persist_kernel<T>), dim3((unsigned)pg), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
+      hipLaunchKernelGGL((tmu_einsum_persist_kernel<T>), dim3((unsigned)pg), dim3(512), 0, st, A, Bm, (T*)y, L, ld,
                          ldy, nslab, t);
     } else {
       hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
