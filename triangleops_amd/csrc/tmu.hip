@@ -405,7 +405,8 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 
 // ---------------------------------------------------------------------------------------------
 // Einsum, large L (L > 384; the persistent variant below runs the same pipeline when L % 256 == 0):
-// 256 x 256 block tile, 4 waves of 128 x 128 (accumulators in AGPRs), k-tile 64,
+// 256 x 256 block tile, 8 waves of 128 x 64 (2 x 4; accumulators in VGPRs, 214 registers, so two
+// waves share each SIMD and one issues MFMAs while the other waits), k-tile 64,
 // operands copied from HBM / L2 straight into LDS with global_load_lds (no staging registers, no
 // LDS store instructions), double-buffered.  One load instruction fills 1 KB of LDS in lane order
 // and covers 8 rows x 128 bytes, i.e. 8 whole cache lines: a footprint of half lines (k-tile 32)
@@ -419,10 +420,10 @@ __global__ __launch_bounds__(NW * 64) void tmu_einsum_kernel(const T* __restrict
 // the loads are inline asm, so the compiler adds no waits of its own for them.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
+__global__ __launch_bounds__(512) void tmu_einsum_large_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
                                                          T* __restrict__ Y, int64_t L, int64_t ld, int64_t ldy,
                                                          int64_t nslab, int tiles) {
-  constexpr int BM = 256, BK = 64, MI = 4, NJ = 4;
+  constexpr int BM = 256, BK = 64, MI = 4, NJ = 2;
   constexpr int TILE = BM * BK;  // elements of one operand's k-tile (32 KB)
   using V8 = vec<T, 8>;
 
@@ -454,17 +455,17 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   auto swa = [](int row) { return (row >> 1) & 7; };
   auto swb = [](int row) { return ((row >> 1) & 3) | ((row >> 2) & 4); };
 
-  // loads: wave w, instruction j < 8 fills LDS bytes [(8 w + j) KB, +1 KB) of an operand's tile,
-  // lane i writing 16 bytes at m0 + 16 i: row r = 8 (8 w + j) + lane / 8, physical chunk lane % 8
-  // <- logical chunk (lane % 8) ^ swz(r).  Rows past L reload row L - 1 (their products are never
-  // stored).
+  // loads: wave w < 8, instruction j < 4 fills LDS bytes [(4 w + j) KB, +1 KB) of an operand's
+  // tile, lane i writing 16 bytes at m0 + 16 i: row r = 8 (4 w + j) + lane / 8, physical chunk
+  // lane % 8 <- logical chunk (lane % 8) ^ swz(r).  Rows past L reload row L - 1 (their products
+  // are never stored).
   const int nk = (int)((L + BK - 1) / BK);  // k-tiles holding a k < L (the rest of the row is zero)
   const char* abase = reinterpret_cast<const char*>(Ab + (int64_t)tm * BM * ld);
   const char* bbase = reinterpret_cast<const char*>(Bb + (int64_t)tn * BM * ld);
-  uint32_t aoff[8], boff[8];
+  uint32_t aoff[4], boff[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int r = 8 * (8 * wave + j) + (lane >> 3), cp = lane & 7;
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * (4 * wave + j) + (lane >> 3), cp = lane & 7;
     const int ra = (int64_t)tm * BM + r < L ? r : (int)(L - 1 - (int64_t)tm * BM);
     const int rb = (int64_t)tn * BM + r < L ? r : (int)(L - 1 - (int64_t)tn * BM);
     aoff[j] = (uint32_t)((ra * ld + 8 * (cp ^ swa(r))) * (int64_t)sizeof(T));
@@ -473,10 +474,10 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   auto gload = [&](int kt, auto S) {
     const char* ak = abase + (int64_t)kt * BK * sizeof(T);
     const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
-    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 8 * 1024);
-    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 8 * 1024);
+    const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 4 * 1024);
+    const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 4 * 1024);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const uint32_t va = aoff[j], vb = boff[j], ma = as + 1024 * j, mb = bs + 1024 * j;
       asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
       asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
@@ -490,7 +491,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   // fragments, which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
     const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
-    const T* bs = bbuf(S) + (wn * 128 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
+    const T* bs = bbuf(S) + (wn * 64 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
 #pragma unroll
     for (int i = 0; i < MI; ++i) f.a[i] = *reinterpret_cast<const V8*>(as + 32 * i * BK);
 #pragma unroll
@@ -510,11 +511,11 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
   };
   auto interleave = [] {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < 6; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(256) void tmu_einsum_large_kernel(const T* __restri
     if (ii < L) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const int64_t j0 = (int64_t)tn * BM + wn * 128 + j * 32 + 16 * ehl;
+        const int64_t j0 = (int64_t)tn * BM + wn * 64 + j * 32 + 16 * ehl;
         if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
         V8 o0, o1;
 #pragma unroll
@@ -1016,7 +1017,7 @@ static int tmu_einsum_t(const void* ab, void* y, int64_t nslab, int64_t L, int64
       hipLaunchKernelGGL((tmu_einsum_persist_kernel<T>), dim3((unsigned)pg), dim3(512), 0, st, A, Bm, (T*)y, L, ld,
                          ldy, nslab, t);
     } else {
-      hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, A, Bm, (T*)y, L, ld,
+      hipLaunchKernelGGL((tmu_einsum_large_kernel<T>), dim3((unsigned)grid), dim3(512), 0, st, A, Bm, (T*)y, L, ld,
                          ldy, nslab, t);
     }
   } else {
