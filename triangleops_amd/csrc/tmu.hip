@@ -186,6 +186,10 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
     int bb = 0;
     for (; t < ntiles; t += G) {
       __syncthreads();  // tile t staged
+      // the second writer on each SIMD (waves 8-11 share SIMDs with waves 4-7) starts ~384 cycles
+      // later, so one wave's MFMA phase meets the other's gate arithmetic instead of its MFMAs
+      // (measured 7-9 % faster at L = 1024, 2-4 % at 2048; a store-phase offset did not help)
+      if (w >= 4) __builtin_amdgcn_s_sleep(6);
       // tile state from the loader waves: every token masked (the outputs are exact zeros, no
       // GEMM needed), every token valid (no mask multiply) or mixed
       const int4 ts = *reinterpret_cast<const int4*>(&tstate[bb][0]);
