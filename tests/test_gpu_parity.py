@@ -86,6 +86,19 @@ def test_tmu_batch(device):
         _check(out, expect, torch.bfloat16, f"tmu B=3 {direction}")
 
 
+def test_tmu_batch_large(device):
+    """B = 2 at L = 512: the persistent einsum over C * B slabs and the phases' batch indexing,
+    on sampled output rows of both batch elements."""
+    L = 512
+    x, m, w = tmu_inputs(L, B=2, seed=13, mask="random")
+    rows = torch.tensor([0, 77, L // 2, L - 1])
+    for direction in ("outgoing", "incoming"):
+        out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                                  **to_dev(w, device))
+        expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, rows=rows, **w)
+        _check(out[:, rows].cpu(), expect, torch.bfloat16, f"tmu B=2 L={L} {direction}")
+
+
 @pytest.mark.parametrize("transpose", [False, True])
 def test_tmu_input_phase_and_mask_zeros(device, transpose):
     """Gated projection vs oracle; masked tokens are exactly zero (bit-exact masking)."""
