@@ -490,9 +490,9 @@ __global__ __launch_bounds__(512) void tmu_einsum_large_kernel(const T* __restri
   struct Frags {
     V8 a[MI], b[NJ];
   };
-  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 128 + 32 j + prow); neither swizzle
-  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all four
-  // fragments, which sit 4 KiB apart (immediate offsets)
+  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 64 + 32 j + prow); neither swizzle
+  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all its
+  // fragments (four of A, two of B), which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
     const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
     const T* bs = bbuf(S) + (wn * 64 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
@@ -665,9 +665,9 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
   struct Frags {
     V8 a[MI], b[NJ];
   };
-  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 128 + 32 j + prow); neither swizzle
-  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all four
-  // fragments, which sit 4 KiB apart (immediate offsets)
+  // fragment i (j) of k-step ks: row wm 128 + 32 i + col (wn 64 + 32 j + prow); neither swizzle
+  // sees the 32 i / 32 j part of the row, so one address per k-step and operand serves all its
+  // fragments (four of A, two of B), which sit 4 KiB apart (immediate offsets)
   auto frags = [&](auto S, int ks, Frags& f) {
     const T* as = abuf(S) + (wm * 128 + col) * BK + (((2 * ks + hl) ^ swa(col)) << 3);
     const T* bs = bbuf(S) + (wn * 64 + prow) * BK + (((2 * ks + hl) ^ swb(prow)) << 3);
