@@ -639,8 +639,9 @@ def _graph_check(device, call, fresh, n_replays=3):
         assert torch.equal(out, eager), f"replay {r} differs from the eager call"
 
 
-def test_graph_replay_tmu(device):
-    x, m, w = tmu_inputs(96, mask="pad")
+@pytest.mark.parametrize("L", [96, 512])  # 512: the persistent einsum kernel
+def test_graph_replay_tmu(device, L):
+    x, m, w = tmu_inputs(L, mask="pad")
     w = to_dev(w, device)
     pre = tops.triangle_mul.precompute(*(w[k] for k in ("norm_in_weight", "norm_in_bias", "p_in_weight",
                                                         "g_in_weight", "norm_out_weight", "norm_out_bias",
@@ -650,7 +651,7 @@ def test_graph_replay_tmu(device):
     def call(xx):
         return tops.triangle_mul.forward(xx, pre, direction="incoming", mask=m)
 
-    _graph_check(device, call, lambda r: [tmu_inputs(96, seed=100 + r)[0].to(device)])
+    _graph_check(device, call, lambda r: [tmu_inputs(L, seed=100 + r)[0].to(device)])
 
 
 def test_graph_replay_tri_and_apb(device):
