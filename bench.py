@@ -14,7 +14,13 @@ Prints ONE JSON line with the contract fields plus:
                 (bf16 dense MFMA 2.5 PFLOP/s, HBM 8 TB/s);
   kernels       the same figures for each kernel of the step;
   torch_path_ms the reference's pure-torch bf16 formulation on the same GPU;
-  cpu_baseline  the fp32 CPU oracle on this host (one full outgoing call at the same size).
+  cpu_baseline  the fp32 CPU oracle on this host (one full outgoing call at the same size);
+  ops           the metric's other two ops at size 1024 (BASELINE.json configs 2 and 4):
+                triangle_attention (starting and ending node) and attention_pair_bias, each with
+                ms per call, per-kernel figures, the dominant kernel's roofline (the attention
+                kernel's MFMA fraction; apb's HBM fraction), the torch path on the same GPU and
+                its own CPU baseline (the fp32 oracle; triangle attention timed on sampled rows
+                and scaled, rows being independent).
 `--sweep FILE` additionally times all three ops, the apb qk-norm variant and a Pairformer pair stack at sizes 128..2048 (ours, the torch path and
 per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
 """
@@ -399,21 +405,123 @@ def graph_ms(call, *args, iters=50):
 # --------------------------------------------------------------------------- #
 # CPU baseline (fp32 oracle on this host)
 # --------------------------------------------------------------------------- #
-def cpu_baseline_tmu(x, m, w, L, min_s=10.0):
-    from oracle import reference as oracle  # the checker, timed here as the CPU baseline
+CPU_SHARE = 16  # host cores of one GPU's share on the GPU boxes (OMP_NUM_THREADS there)
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    threads = max(1, min(threads, 16))
+
+def _cpu_threads():
+    """(threads used, CPUs in this process's affinity mask): the oracle runs on the GPU's CPU share."""
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, min(aff, int(os.environ.get("OMP_NUM_THREADS", CPU_SHARE) or CPU_SHARE), CPU_SHARE))
     torch.set_num_threads(threads)
+    return threads, aff
+
+
+def _repeat(fn, min_s):
     calls, t0 = 0, time.perf_counter()
-    while True:  # repeat whole calls until at least min_s of CPU work has been timed
-        oracle.triangle_multiplicative_update(x, direction="outgoing", mask=m, **w)
+    while True:  # whole calls until at least min_s of CPU work has been timed
+        fn()
         calls += 1
         dt = time.perf_counter() - t0
         if dt >= min_s:
-            break
-    return {"value": round(calls / dt, 5), "unit": "calls/s", "cores": threads, "kind": "port",
+            return calls, dt
+
+
+def cpu_baseline_tmu(x, m, w, L, min_s=10.0):
+    from oracle import reference as oracle  # the checker, timed here as the CPU baseline
+
+    threads, aff = _cpu_threads()
+    calls, dt = _repeat(lambda: oracle.triangle_multiplicative_update(x, direction="outgoing", mask=m, **w), min_s)
+    return {"value": round(calls / dt, 5), "unit": "calls/s", "cores": threads, "affinity_cpus": aff, "kind": "port",
             "sample": f"{calls} full outgoing call(s) at L={L} (fp32 torch oracle), {dt:.1f} s"}
+
+
+def cpu_baseline_tri(d, N, min_s=8.0):
+    """fp32 oracle triangle attention on sampled rows: rows are independent, so a call over R rows
+    costs a + b R (a: LayerNorm and pair bias of the whole grid, b: one row's projections, attention
+    and gate); a and b come from timing R and 2R rows, and the whole call is estimated as a + b N."""
+    from oracle import reference as oracle
+
+    threads, aff = _cpu_threads()
+    R = 16
+    args = (d["X"], d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"], d["B_proj_z"], d["W_proj_g"],
+            None, d["W_proj_o"], None, H, D)
+    t = {}
+    for r in (R, 2 * R):
+        rows = torch.arange(r) * (N // (2 * R))
+        calls, dt = _repeat(lambda: oracle.triangle_attention(*args, scale=D**-0.5, mask=d["mask"], rows=rows),
+                            min_s / 2)
+        t[r] = dt / calls
+    b = max(t[2 * R] - t[R], 1e-9) / R
+    a = max(t[R] - b * R, 0.0)
+    est = a + b * N
+    return {"value": round(1.0 / est, 6), "unit": "calls/s", "cores": threads, "affinity_cpus": aff, "kind": "port",
+            "sample": f"starting node at N={N} (fp32 torch oracle) timed on {R} and {2 * R} sampled rows "
+                      f"({t[R]:.2f} s / {t[2 * R]:.2f} s per call); whole call estimated as "
+                      f"{a:.3g} s + {N} x {b:.4g} s = {est:.4g} s"}
+
+
+def cpu_baseline_apb(d, M, min_s=6.0):
+    from oracle import reference as oracle
+
+    threads, aff = _cpu_threads()
+    args = (d["X"], d["WQ"], d["WK"], d["WV"], d["Z"], d["W_ln"], d["B_ln"], d["W_proj_z"], d["B_proj_z"],
+            d["W_proj_g"], d["B_proj_g"], d["W_proj_o"], d["B_proj_o"], H, D)
+    calls, dt = _repeat(lambda: oracle.attention_pair_bias(*args, scale=D**-0.5, mask=d["mask"]), min_s)
+    return {"value": round(calls / dt, 5), "unit": "calls/s", "cores": threads, "affinity_cpus": aff, "kind": "port",
+            "sample": f"{calls} full call(s) at M={M} (fp32 torch oracle), {dt:.1f} s"}
+
+
+def op_entry_tri(N, dev, iters, warmup, cpu):
+    """triangle_attention at N: starting and ending node per call, per-kernel
+    HIP-event times of the starting node, the attention kernel's MFMA fraction, the torch path."""
+    d_c = tri_inputs(N)
+    d = to_dev(d_c, dev)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], H, D)
+    kw = dict(scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None)
+    ms = time_ms(lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], **kw), iters, warmup)
+    ms_end = time_ms(lambda: tops.triangle_attn.forward(d["X"].transpose(0, 1), pre, mask=d["mask"].T, **kw), iters,
+                     warmup)
+    work = tri_work(N)
+    ph = run_phases([tri_phases(d, pre)], list(work), iters, warmup)
+    kern = {n: kernel_entry(n, ph[n], *work[n]) for n in ph}
+    ka = kern["tri_attention"]
+    e = {"config": f"triangle_attention bf16, N={N}, H={H}, D={D}, C={C}, pad mask (last 10% rows/cols)",
+         "ms_per_call": round(ms, 4), "ms_per_call_ending_node": round(ms_end, 4), "calls_per_s": round(1e3 / ms, 2),
+         "roofline": {"kernel": "tri_attention", "bound": "mfma", "achieved": ka["achieved"], "peak": ka["peak"],
+                      "unit": ka["unit"], "frac": ka["frac"], "traffic": None},
+         "kernels": kern}
+    e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), 3, 1), 4)
+    del d, pre
+    torch.cuda.empty_cache()
+    e["cpu_baseline"] = cpu_baseline_tri(d_c, N) if cpu else None
+    return e
+
+
+def op_entry_apb(M, dev, iters, warmup, cpu):
+    """attention_pair_bias at M: per-kernel times, the attention kernel's HBM
+    fraction (Z is read once: 2 M^2 C bytes), the torch path."""
+    d_c = apb_inputs(M)
+    d = to_dev(d_c, dev)
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], H, D)
+    ms = time_ms(lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5, W_proj_g=d["W_proj_g"],
+                                                      B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"],
+                                                      B_proj_o=d["B_proj_o"], mask=d["mask"]), iters, warmup)
+    work = apb_work(M)
+    ph = run_phases([apb_phases(d, pre)], list(work), iters, warmup)
+    kern = {n: kernel_entry(n, ph[n], *work[n]) for n in ph}
+    ka = kern["apb_attention"]
+    e = {"config": f"attention_pair_bias bf16, M={M}, H={H}, D={D}, C_s=C_z={C}, key mask (last 5% padded)",
+         "ms_per_call": round(ms, 4), "calls_per_s": round(1e3 / ms, 2),
+         "roofline": {"kernel": "apb_attention", "bound": "hbm", "achieved": ka["achieved"], "peak": ka["peak"],
+                      "unit": ka["unit"], "frac": ka["frac"], "traffic": None},
+         "kernels": kern}
+    e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)
+    del d, pre
+    torch.cuda.empty_cache()
+    e["cpu_baseline"] = cpu_baseline_apb(d_c, M) if cpu else None
+    return e
 
 
 # --------------------------------------------------------------------------- #
@@ -581,6 +689,36 @@ def traffic_run(L):
     print("traffic run done", flush=True)
 
 
+def op_run(op, n):
+    """Workload of the counter runs (no timing): 5 calls of one op at size n after 2 warmup calls
+    (`tri`: starting-node triangle attention; `apb`: attention_pair_bias; `tmu`: outgoing tmu)."""
+    dev = torch.device("cuda:0")
+    if op == "tri":
+        d = to_dev(tri_inputs(n), dev)
+        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                            d["B_proj_z"], H, D)
+        fn = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=D**-0.5,  # noqa: E731
+                                                W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
+                                                B_proj_o=None)
+    elif op == "apb":
+        d = to_dev(apb_inputs(n), dev)
+        pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                             d["B_proj_z"], H, D)
+        fn = lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5,  # noqa: E731
+                                                 W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"],
+                                                 W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"], mask=d["mask"])
+    else:
+        x_c, m_c, w_c = tmu_inputs(n)
+        x, m = x_c.to(dev), m_c.to(dev)
+        w = {k: v.to(dev) for k, v in w_c.items()}
+        pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+        fn = lambda: tops.triangle_mul.forward(x, pre, direction="outgoing", mask=m)  # noqa: E731
+    for _ in range(7):
+        fn()
+    torch.cuda.synchronize()
+    print(f"op run {op} n={n} done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -591,6 +729,10 @@ def main():
     ap.add_argument("--sweep-sizes", default="128,256,512,1024,2048")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-path reference timing")
+    ap.add_argument("--no-ops", action="store_true", help="skip the triangle_attention / attention_pair_bias entries")
+    ap.add_argument("--ops-size", type=int, default=1024, help="N = M of the triangle_attention / apb entries")
+    ap.add_argument("--op-run", choices=("tri", "apb", "tmu"), default=None,
+                    help="only run 7 calls of one op at --size (workload of rocprofv3 counter runs)")
     ap.add_argument("--traffic-run", action="store_true",
                     help="only run the workload of the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -606,6 +748,9 @@ def main():
     L = args.size
     if args.traffic_run:
         traffic_run(L)
+        return
+    if args.op_run:
+        op_run(args.op_run, L)
         return
 
     x_c, m_c, w_c = tmu_inputs(L)
@@ -669,12 +814,16 @@ def main():
     }
     del x, m, w, pre, steps, timers
     torch.cuda.empty_cache()
+    cpu = not args.no_cpu_baseline
+    # the other two ops of the metric at their BASELINE configurations (size 1024)
+    if not args.no_ops:
+        out["ops"] = {
+            "triangle_attention": op_entry_tri(args.ops_size, dev, 10, 3, cpu),
+            "attention_pair_bias": op_entry_apb(args.ops_size, dev, 20, 5, cpu),
+        }
     if args.sweep:
         sweep(args.sweep, [int(s) for s in args.sweep_sizes.split(",")], dev)
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L)
-    else:
-        out["cpu_baseline"] = None
+    out["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L) if cpu else None
     print(json.dumps(out), flush=True)
 
 

@@ -82,7 +82,7 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
  *   w_ln, b_ln  io (C,) LayerNorm affine (b_ln may be NULL)
  *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T
  *   WZ     io   (H, C);  BZ fp32 (H,) or NULL
- *   ldn         N rounded up to a multiple of 64
+ *   ldn         max(64, N rounded up to a multiple of 64); any other value is rejected (TOPS_EINVAL)
  *   Qp     io   (N, H, ldn, D): scale * log2(e) * Q, d permuted within each 32 as
  *               [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]
  *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x D, d permuted) then
@@ -90,7 +90,7 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
  *   bias   io   (H, ceil(N/32), ldn/32, 1024): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]) per
  *               32 x 32 (query, key) tile; (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e) at
  *               element (64 j + 32 hl + c) * 8 + e of tile (qt, kt); zeros for k >= N
- * C == 128, H == 4, D == 32.
+ * C == 128, H == 4, D == 32, N <= 16384 (tops_tri_generic_prep serves larger N).
  */
 int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                   const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
@@ -102,7 +102,8 @@ int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, con
  *   mask   int8 (N, N) with strides (sm0, sm1), nonzero = valid key, or NULL
  *   out    io   O[i, q, h*D + d] at out[i*so0 + q*so1 + h*D + d]
  * out[i,q,h] = softmax_k(scale * Q.K + bias[h,q,k] - 1e9 * (mask[i,k] == 0)) V; a row with no
- * valid key is the uniform average of V over all N keys (what the -1e9 add gives).  D == 32.
+ * valid key is the uniform average of V over all N keys (what the -1e9 add gives).  D == 32,
+ * N <= 16384, ldn as in tops_tri_prep (any other value is rejected).
  */
 int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0, int64_t sm1,
                        void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H, int64_t D, int dtype,

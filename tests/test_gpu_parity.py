@@ -44,6 +44,17 @@ def test_tmu_matches_oracle(device, L, direction, mask):
     _check(out, expect, torch.bfloat16, f"tmu L={L} {direction} mask={mask}")
 
 
+def test_tmu_config0_all_ones_mask(device):
+    """BASELINE config 0 through the HIP path: outgoing, L = 128, all-ones mask, seed 0, the whole
+    output against the fp32 oracle; and an all-ones mask gives the same bits as no mask."""
+    x, m, w = tmu_inputs(128, seed=0, mask="ones")
+    xd, wd = to_dev(x, device), to_dev(w, device)
+    out = tops.triangle_multiplicative_update(xd, direction="outgoing", mask=m.to(device), **wd)
+    expect = ref.triangle_multiplicative_update(x, direction="outgoing", mask=m, **w)
+    _check(out, expect, torch.bfloat16, "tmu config 0")
+    assert torch.equal(out, tops.triangle_multiplicative_update(xd, direction="outgoing", mask=None, **wd))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_tmu_fp16(device, dtype, direction):
@@ -287,16 +298,61 @@ def test_tri_low_level_entry_points(device):
 
 @pytest.mark.parametrize("N", [512, 1024, 2048])
 def test_tri_config_sizes_sampled_rows(device, N):
-    """BASELINE configs 3/4 sizes (pad mask): starting node on sampled rows; ending node at N <= 1024."""
+    """BASELINE configs 3/4 sizes (pad mask): starting and ending node on sampled rows."""
     inp = tri_inputs(N, seed=0, mask="pad")
     out = _tri_call(inp, device)
     rows = torch.tensor([0, N // 2, N - N // 10 - 1, N - 1])
     _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} start")
-    if N <= 1024:
-        Xd = inp["X"].to(device)
-        out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
-        exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T, rows=rows)
-        _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri N={N} end")
+    del out
+    Xd = inp["X"].to(device)
+    out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
+    exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T, rows=rows)
+    _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri N={N} end")
+
+
+@pytest.mark.parametrize("N", [100, 384])
+def test_tri_masked_keys_bitwise_invariant(device, N):
+    """Masked keys contribute exactly nothing (weight exactly 0, benchmarks/references.py:198-201 with
+    the reference kernel's -1e9 add, triangle_attn/kernel.py:230-238).
+    (a) Kernel level, random pair mask: the attention core fed with K/V projected from x perturbed at
+        every masked (i, k) returns the same bits as with the original K/V.
+    (b) Op level, a key mask shared by all rows (mask[i, k] = valid[k]): perturbing x[:, k] at every
+        masked k changes only output columns k (their own query, gate input and bias entries are
+        perturbed); every other output element is bitwise unchanged."""
+    from triangleops_amd.triangle_attn.kernel import attention_core, prep_forward
+
+    inp = tri_inputs(N, seed=N + 3, mask="random", bias_z=True)
+    d = to_dev(inp, device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], 4, 32)
+    m = d["mask"]
+    g = torch.Generator().manual_seed(N)
+    noise = torch.randn(N, N, 128, generator=g).to(torch.bfloat16).to(device)
+    X2 = torch.where(m[..., None], d["X"], d["X"] + 3 * noise)
+    args = (pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"])
+    Qp, KV, bias, ldn = prep_forward(d["X"], *args, scale=inp["scale"])
+    _, KV2, _, _ = prep_forward(X2, *args, scale=inp["scale"])
+    o1 = torch.empty(N, N, 128, device=device, dtype=torch.bfloat16)
+    o2 = torch.empty_like(o1)
+    attention_core(Qp, KV, bias, o1, N=N, ldn=ldn, mask=m)
+    attention_core(Qp, KV2, bias, o2, N=N, ldn=ldn, mask=m)
+    rows = m.any(dim=1)  # a row without valid keys averages every key (uniform path)
+    assert not torch.equal(KV, KV2)
+    assert torch.equal(o1[rows], o2[rows]), "masked keys changed valid rows (kernel level)"
+
+    valid = torch.rand(N, generator=g) < 0.8
+    valid[0] = False
+    km = valid[None, :].expand(N, N).contiguous().to(device)
+    X3 = d["X"].clone()
+    X3[:, ~valid.to(device)] += 3 * noise[:, ~valid.to(device)]
+    kw = dict(mask=km, scale=inp["scale"], W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
+              B_proj_o=None)
+    a = tops.triangle_attn.forward(d["X"], pre, **kw)
+    b = tops.triangle_attn.forward(X3, pre, **kw)
+    cols = valid.to(device)
+    assert not torch.equal(a[:, ~cols], b[:, ~cols])
+    assert torch.equal(a[:, cols], b[:, cols]), "masked keys changed the output (op level)"
+    _check(a, _tri_ref(inp, mask=km.cpu()), torch.bfloat16, f"tri key mask N={N}")
 
 
 @pytest.mark.parametrize("N", [257, 300, 520])
@@ -438,6 +494,54 @@ def test_apb_precompute_forward_matches_oneshot(device):
                                  inp["W_proj_z"], inp["B_proj_z"], inp["W_proj_g"], inp["B_proj_g"], inp["W_proj_o"],
                                  inp["B_proj_o"], inp["H"], inp["D"], scale=1.0)
     assert torch.equal(a, b)
+
+
+def _apb_perturbed(inp, kmask, seed):
+    """inputs with X rows and Z key columns replaced at the masked keys"""
+    g = torch.Generator().manual_seed(seed)
+    X, Z = inp["X"].clone(), inp["Z"].clone()
+    bad = ~kmask
+    X[bad] = torch.randn(int(bad.sum()), X.shape[1], generator=g).to(X.dtype) * 3
+    Z[:, bad] = torch.randn(Z.shape[0], int(bad.sum()), Z.shape[2], generator=g).to(Z.dtype) * 3
+    return dict(inp, X=X, Z=Z, mask=kmask)
+
+
+@pytest.mark.parametrize("M,shape,dtype", [(128, "tuned", torch.bfloat16), (200, "tuned", torch.bfloat16),
+                                           (1024, "tuned", torch.bfloat16), (300, "tuned", torch.float16),
+                                           (70, (96, 64, 3, 24), torch.bfloat16), (64, "tuned", torch.float32)])
+@pytest.mark.parametrize("mask", ["pad", "random", "first"])
+def test_apb_masked_keys_bitwise_invariant(device, M, shape, dtype, mask):
+    """Masked keys contribute exactly nothing (-inf before the softmax, benchmarks/references.py:273-274):
+    replacing the X rows and Z columns of every masked key leaves every unmasked query row of the output
+    bitwise unchanged (tuned kernels incl. the split-key combine at M = 1024, the any-shape kernels and
+    fp32 I/O); "first" masks key 0, the key every online softmax starts from."""
+    C, Cz, H, D = (128, 128, 4, 32) if shape == "tuned" else shape
+    inp = apb_inputs(M, C=C, Cz=Cz, H=H, D=D, seed=M + 11, mask="none", biases=True, dtype=dtype)
+    g = torch.Generator().manual_seed(M)
+    if mask == "pad":
+        km = torch.arange(M) < M - M // 20
+    elif mask == "random":
+        km = torch.rand(M, generator=g) < 0.7
+    else:
+        km = torch.ones(M, dtype=torch.bool)
+        km[0] = False
+        km[M // 2] = False
+    a_inp, b_inp = dict(inp, mask=km), _apb_perturbed(inp, km, M + 1)
+    a, b = _apb_call(a_inp, device), _apb_call(b_inp, device)
+    assert not torch.equal(a[~km.to(device)], b[~km.to(device)])
+    assert torch.equal(a[km.to(device)], b[km.to(device)]), f"apb M={M} {shape} {dtype} mask={mask}"
+    _check(a, _apb_ref(a_inp), dtype, f"apb M={M} {shape} {dtype} mask={mask}")
+
+
+@pytest.mark.parametrize("M,shape,dtype", [(96, "tuned", torch.bfloat16), (70, (96, 64, 3, 24), torch.bfloat16),
+                                           (48, "tuned", torch.float32)])
+def test_apb_qknorm_first_key_masked(device, M, shape, dtype):
+    """The qk-norm variant with key 0 masked (and a random key mask) matches the oracle on the tuned,
+    any-shape and fp32 paths."""
+    C, Cz, H, D = (128, 128, 4, 32) if shape == "tuned" else shape
+    inp = apb_qkn_inputs(M, C=C, Cz=Cz, H=H, D=D, seed=M + 5, mask="random", dtype=dtype)
+    inp["key_mask"][0] = False
+    _check(_qkn_call(inp, device), _qkn_ref(inp), dtype, f"apb qk-norm key0 masked M={M} {shape} {dtype}")
 
 
 @pytest.mark.parametrize("M", [1024, 2048])

@@ -202,3 +202,55 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], cwd=ROOT,
                        capture_output=True, text=True, timeout=300)
     assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+@pytest.mark.parametrize("N,ldn", [(100, 8192), (100, 64), (100, 192), (4096, 4160), (16385, 16448), (0, 0)])
+def test_tri_abi_rejects_bad_ldn_and_n(N, ldn):
+    """tops_tri_prep / tops_tri_attention accept only ldn = max(64, round_up(N, 64)) and N <= 16384
+    (the attention kernel's per-row key-block tables in LDS hold that many blocks); anything else
+    returns TOPS_EINVAL before any launch (the pointers below are never dereferenced)."""
+    lib = _native.load()
+    fake = ctypes.c_void_p(1 << 20)
+    rc = lib.tops_tri_attention(fake, fake, fake, None, 0, 0, fake, 0, 0, N, ldn, 4, 32, 2, None)
+    assert rc == 1, (N, ldn, rc)
+    assert b"tops_tri_attention" in lib.tops_last_error()
+    rc = lib.tops_tri_prep(fake, 0, 0, None, None, 0, fake, fake, None, fake, fake, fake, N, ldn, 128, 4, 32, 1e-5,
+                           1.0, 2, None)
+    assert rc == 1, (N, ldn, rc)
+
+
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+def test_apb_abi_rejects_misaligned_z():
+    """tops_apb_forward refuses Z token strides that are not multiples of 8 and misaligned bases (the
+    kernel reads Z, X and the workspace with 16-byte loads)."""
+    lib = _native.load()
+    a = ctypes.c_void_p(1 << 20)
+    for sz0, sz1, z in ((128 * 100 + 4, 128, 1 << 20), (128 * 100, 132, 1 << 20), (128 * 100, 128, (1 << 20) + 2)):
+        rc = lib.tops_apb_forward(a, a, ctypes.c_void_p(z), sz0, sz1, a, a, a, None, a, a, 100, 128, 128, 4, 32,
+                                  1.0, 1e-5, 2, None)
+        assert rc == 1 and b"16-byte" in lib.tops_last_error(), (sz0, sz1, z)
+
+
+def test_tri_dispatch_decision():
+    """The tuned kernels serve (C_in, H, D, C_out) = (128, 4, 32, 128) up to N = 16384; other shapes and
+    larger N go to the any-shape kernels."""
+    from triangleops_amd.triangle_attn.kernel import TUNED_MAX_N, fast_shape
+
+    assert TUNED_MAX_N == 16384
+    assert fast_shape(128, 4, 32, 128, 1024) and fast_shape(128, 4, 32, 128, 16384)
+    assert not fast_shape(128, 4, 32, 128, 16385)
+    assert not fast_shape(64, 4, 16, 64, 128) and not fast_shape(128, 4, 32, 64, 128)
+
+
+def test_vec16_copies_misaligned_views():
+    """A contiguous view whose base is off a 16-byte boundary is copied (`.contiguous()` alone would
+    return it unchanged); aligned views with strides that are multiples of 8 are passed through."""
+    base = torch.zeros(1024, dtype=torch.bfloat16)
+    v = base[1:129].view(1, 128)
+    assert v.is_contiguous() and v.data_ptr() % 16 != 0 and not _native.vec16_ok(v)
+    c = _native.vec16(v)
+    assert c.data_ptr() % 16 == 0 and torch.equal(c, v) and c.data_ptr() != v.data_ptr()
+    x = torch.zeros(8, 8, 128, dtype=torch.bfloat16)
+    t = x.transpose(0, 1)
+    assert _native.vec16_ok(t) and _native.vec16(t).data_ptr() == t.data_ptr()

@@ -142,6 +142,18 @@ def check_device(*tensors) -> None:
             raise ValueError(f"all tensors must be on one device (got {dev} and {t.device})")
 
 
+def vec16_ok(t: torch.Tensor) -> bool:
+    """True when the kernels' 16-byte vector accesses of `t` are valid: unit last stride, every
+    other stride a multiple of 8 elements and a 16-byte aligned base."""
+    return t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+
+
+def vec16(t: torch.Tensor) -> torch.Tensor:
+    """`t` itself when vec16_ok(t), else a fresh contiguous copy (which is 16-byte aligned;
+    `.contiguous()` alone would return a contiguous but misaligned view unchanged)."""
+    return t if vec16_ok(t) else t.clone(memory_format=torch.contiguous_format)
+
+
 def mask_i8(mask: torch.Tensor | None) -> torch.Tensor | None:
     """Mask as int8 storage without a copy for bool/int8/uint8 contiguous masks."""
     if mask is None:

@@ -33,9 +33,8 @@ def apb_forward(X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0,
         return _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm, H, D)
     code = io_dtype_code(X.dtype)
     _native.check_device(X, W_QKV, Z, W_combined, Og, mask)
-    X = X if X.is_contiguous() else X.contiguous()
-    if Z.stride(2) != 1 or Z.stride(0) % 8 or Z.stride(1) % 8:
-        Z = Z.contiguous()
+    X = _native.vec16(X)
+    Z = _native.vec16(Z)
     if wqkv_hm is None:
         wqkv_hm = wqkv_from_interleaved(W_QKV, H, D)
     if wqkv_hm.dtype != X.dtype:
@@ -154,8 +153,7 @@ def apb_forward_qkv(q, k, v, Z, W_combined, sum_W_combined, B_const, Og, scale=1
     _native.check_device(q, k, v, Z, W_combined, Og, mask)
     st = _native.stream_of(q)
     if HD == 128 and Cz == 128 and H == 4 and D == 32 and q.dtype != torch.float32:
-        if Z.stride(2) != 1 or Z.stride(0) % 8 or Z.stride(1) % 8:
-            Z = Z.contiguous()
+        q, k, v, Z = (_native.vec16(t) for t in (q, k, v, Z))
         nbytes = _native.apb_workspace_bytes(M, H, D)
         work = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8) if nbytes else None
         _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), Z.data_ptr(), Z.stride(0),

@@ -551,6 +551,10 @@ extern "C" int tops_apb_forward(const void* X, const void* wqkv, const void* Z, 
                (long long)C, (long long)Cz, (long long)H, (long long)D);
   TOPS_REQUIRE(M >= 0, "tops_apb_forward: bad M");
   TOPS_REQUIRE(work || M == 0, "tops_apb_forward: workspace of tops_apb_workspace_bytes(M, H, D) bytes required");
+  TOPS_REQUIRE(sz0 % 8 == 0 && sz1 % 8 == 0 && (uintptr_t)Z % 16 == 0 && (uintptr_t)X % 16 == 0 &&
+                   (uintptr_t)work % 16 == 0,
+               "tops_apb_forward: Z needs token strides that are multiples of 8, and Z, X and the workspace "
+               "16-byte aligned base pointers");
   if (M == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
   char* w = (char*)work;
@@ -577,6 +581,10 @@ extern "C" int tops_apb_forward_qkv(const void* Q, const void* K, const void* V,
                (long long)HD, (long long)Cz, (long long)H, (long long)D);
   TOPS_REQUIRE(M >= 0, "tops_apb_forward_qkv: bad M");
   TOPS_REQUIRE(work || M == 0, "tops_apb_forward_qkv: workspace of tops_apb_workspace_bytes(M, H, D) bytes required");
+  TOPS_REQUIRE(sz0 % 8 == 0 && sz1 % 8 == 0 && (uintptr_t)Z % 16 == 0 && (uintptr_t)Q % 16 == 0 &&
+                   (uintptr_t)K % 16 == 0 && (uintptr_t)V % 16 == 0 && (uintptr_t)work % 16 == 0,
+               "tops_apb_forward_qkv: Z needs token strides that are multiples of 8, and Z, Q, K, V and the "
+               "workspace 16-byte aligned base pointers");
   if (M == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)

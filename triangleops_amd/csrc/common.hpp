@@ -102,6 +102,15 @@ __device__ inline void stg(void* p, V v) {
   *reinterpret_cast<V*>(p) = v;
 }
 
+// Waits until at most N vector-memory operations of this wave are outstanding (s_waitcnt with
+// the expcnt / lgkmcnt fields at their maxima, i.e. not waited on).  gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+template <int N>
+__device__ inline void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)); saturates cleanly to 0 / 1.

@@ -138,7 +138,10 @@ __global__ __launch_bounds__(256) void tri_generic_attn_kernel(const T* __restri
     s += brow[k];
     if (mask && mask[i * sm0 + k * sm1] == 0) s = MASK_INF ? -INFINITY : s + -1e9f;
     const float mn = fmaxf(m, s);
-    const float corr = __expf(m - mn), p = __expf(s - mn);
+    // while every key so far is masked (MASK_INF), m = mn = -inf: shift by 0 instead, so the
+    // masked key gets p = 0 and the state stays (m, l, o) = (-inf, 0, 0) instead of NaN
+    const float sh = mn == -INFINITY ? 0.f : mn;
+    const float corr = __expf(m - sh), p = __expf(s - sh);
     m = mn;
     l = l * corr + p;
     const T* vp = vi_ + (i * N + k) * HD + h * D;

@@ -26,12 +26,19 @@
 //
 // Reference: triangle_attn/module.py:57-125 (forward), triangle_attn/kernel.py:36-98 (bias),
 // :110-253 (attention), :230-238 and :369 (additive -1e9 pair mask, -inf outside the row).
+#include <type_traits>
+
 #include "capi.hpp"
 #include "common.hpp"
 
 namespace tops {
 
 constexpr int kKVBlock = 4096;  // elements per (row, head, 64-key) KV block: 64x32 K + 32x64 V^T
+constexpr int kMaxN = 16384;    // largest N of the tuned kernels (per-row key-block tables in LDS)
+constexpr int kMaxKB = kMaxN / 64;
+
+// The pre-pass buffers' key stride: N rounded up to a multiple of 64 (at least 64).
+static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 * 64; }
 
 // ---------------------------------------------------------------------------------------------
 // Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 8 waves in two roles:
@@ -282,8 +289,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
   using V4 = vec<T, 4>;
 
   __shared__ __attribute__((aligned(16))) T kvs[3][kKVLds];
-  __shared__ unsigned long long kvalid[64];  // per 64-key block (N <= 4096)
-  __shared__ short vblk[64];                 // indices of blocks with a valid key
+  __shared__ unsigned long long kvalid[kMaxKB];  // per 64-key block (N <= kMaxN)
+  __shared__ short vblk[kMaxKB];                 // indices of blocks with a valid key
   __shared__ int nvblk, row_any;
 
   // ---- block -> (row i, head h, query chunk); XCD-aware: an XCD works through a contiguous
@@ -534,6 +541,341 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     }
   }
 }
+// ---------------------------------------------------------------------------------------------
+// Attention core, two rows per wave.  A block = 4 waves = rows (i0, i1 = i0 + 1) x 128 queries
+// of one head; wave w owns query tile qt = 4 qc + w of both rows.  Per 32-key tile step the
+// wave runs, for row r = 0 then 1 (a "stage" each):
+//     S_r^T = C_r + I . B^T + K_r . Q_r^T       4 MFMAs (C_r = -m_r, the lazily raised row max)
+//     P_r   = exp2(S_r^T), l_r += sum P_r        16 v_exp, 8 packed converts, 16 fp32 adds
+//     O_r^T += V_r^T . P_r^T                     2 MFMAs
+// The bias operand B (16 bytes per lane and half) is loaded once per step for both rows, so
+// each bias tile costs 1 KB of L2 reads per 32 x 32 tile instead of 2 KB; K and V of both rows
+// are copied straight into LDS (global_load_lds, 1 KB per wave instruction) with each lane
+// fetching the 16-byte chunk that belongs at its LDS slot under the operand reads' XOR swizzle
+// (K rows 64 B: chunk ^ ((key >> 2) & 3); V^T rows 128 B: chunk ^ ((d >> 1) & 7)), so the
+// operand reads are free of bank conflicts without padding.  A ring of 4 LDS slots per 64-key
+// block, one barrier per block, copies issued three blocks ahead.
+// Stages are software-pipelined: stage (row r, tile t) issues the PV MFMAs of the previous
+// stage and the score MFMAs of the next one (the other row) between its own exponentials, so
+// the matrix cores and the VALU of a wave work together; the row sums are fp32 adds of the
+// unrounded weights (as the reference's l_i += sum(p)), which, unlike packed dot products,
+// co-issue with MFMAs.  Masking, the lazy max and rows without valid keys (uniform average of
+// V over all N keys) follow the one-row kernel above.
+// ---------------------------------------------------------------------------------------------
+constexpr int kRing = 4;  // LDS slots of 64-key KV blocks (per block: 2 rows x 8 KB each)
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
+                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
+                                                          int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
+                                                          int64_t so1, int N, int ldn, int H, int nqc, int nrp) {
+  constexpr int D = 32, NW = 4, KVB = kKVBlock * 2;  // bytes of one (row, 64-key) KV block
+  using V8 = vec<T, 8>;
+  using V4 = vec<T, 4>;
+
+  // four separate arrays, indexed at compile time: the compiler then sees that the LDS reads of
+  // one slot do not alias the asynchronous copy into another, and does not wait for the copy
+  __shared__ __attribute__((aligned(16))) char slot0[2][KVB];
+  __shared__ __attribute__((aligned(16))) char slot1[2][KVB];
+  __shared__ __attribute__((aligned(16))) char slot2[2][KVB];
+  __shared__ __attribute__((aligned(16))) char slot3[2][KVB];
+  __shared__ unsigned long long kvalid[2][kMaxKB];
+  __shared__ short vblk[kMaxKB];
+  __shared__ int nvblk, row_any[2];
+  auto slot = [&](auto sc) -> char(*)[KVB] {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return slot0;
+    else if constexpr (S == 1) return slot1;
+    else if constexpr (S == 2) return slot2;
+    else return slot3;
+  };
+
+  // ---- block -> (head, row pair, query chunk), XCD-aware: consecutive ids on one XCD share
+  // ---- the head (its bias stays in that XCD's L2) and each row pair's chunks run together.
+  const int total = H * nrp * nqc;
+  int id = blockIdx.x;
+  if (total % 8 == 0) id = (id % 8) * (total / 8) + id / 8;
+  const int qc = id % nqc, rp = (id / nqc) % nrp, h = id / (nqc * nrp);
+  const int i0 = 2 * rp, i1v = 2 * rp + 1, i1 = i1v < N ? i1v : N - 1;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int nkb = ldn / 64, nqt = (N + 31) / 32, nkt = ldn / 32;
+  const int qt = qc * NW + wave;
+
+  // ---- key validity of both rows per 64-key block; the visit list is their union ----
+  if (tid < 2) row_any[tid] = 0;
+  __syncthreads();
+  for (int idx = wave; idx < 2 * nkb; idx += NW) {
+    const int r = idx & 1, kb = idx >> 1;
+    const int64_t k = 64LL * kb + lane;
+    bool ok = k < N;
+    if (ok && mask) ok = mask[(int64_t)(r ? i1 : i0) * sm0 + k * sm1] != 0;
+    const unsigned long long bits = __ballot(ok);
+    if (lane == 0) {
+      kvalid[r][kb] = bits;
+      if (bits) row_any[r] = 1;
+    }
+  }
+  __syncthreads();
+  const bool uni[2] = {row_any[0] == 0, row_any[1] == 0};  // no valid key: weights 1/N
+  if (tid == 0) {
+    int n = 0;
+    for (int kb = 0; kb < nkb; ++kb) {
+      const unsigned long long all = (N - 64 * kb >= 64) ? ~0ull : ((1ull << (N - 64 * kb)) - 1ull);
+      if (uni[0]) kvalid[0][kb] = all;
+      if (uni[1]) kvalid[1][kb] = all;
+      if (kvalid[0][kb] | kvalid[1][kb]) vblk[n++] = (short)kb;
+    }
+    nvblk = n;
+  }
+  __syncthreads();
+  const int nv = nvblk;  // >= 1 whenever N >= 1
+
+  // ---- per-row operands: Q^T (scaled, d-permuted), identity (zero for a uniform row) ----
+  const int irow[2] = {i0, i1};
+  int q = 32 * qt + col;
+  q = q < N ? q : N - 1;
+  V8 qop[2][2], ident[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const T* qr = Qp + (((int64_t)irow[r] * H + h) * ldn + q) * D + 8 * hl;
+    qop[r][0] = uni[r] ? V8{} : ldg<V8>(qr);
+    qop[r][1] = uni[r] ? V8{} : ldg<V8>(qr + 16);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ident[r][j][e] = (T)((!uni[r] && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
+  }
+  const int qtc = qt < nqt ? qt : nqt - 1;
+  const T* bq = bias + ((int64_t)h * nqt + qtc) * nkt * 1024 + (32 * hl + col) * 8;
+
+  // ---- KV block copy: wave w moves (row w >> 1, part w & 1 = K or V^T), 4 KB in four 1 KB
+  // ---- instructions; lane l of instruction s fills LDS chunk p = 64 s + l of the part with the
+  // ---- global chunk that the swizzle places there.  Inline asm: the compiler does not count
+  // ---- these loads, so it adds no waits of its own for them (the waits before the barriers are
+  // ---- explicit), and no copy is ever issued between a bias load and that load's first use, so
+  // ---- the compiler's own waits for the bias loads stay exact.
+  const int crow = wave >> 1, cpart = wave & 1;
+  const char* kvsrc = reinterpret_cast<const char*>(KV + ((int64_t)irow[crow] * H + h) * nkb * kKVBlock + cpart * 2048);
+  uint32_t gofs[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int p = 64 * s + lane;
+    gofs[s] = 16u * (uint32_t)(cpart == 0 ? ((p & ~3) | ((p & 3) ^ ((p >> 4) & 3))) : ((p & ~7) | ((p & 7) ^ ((p >> 4) & 7))));
+  }
+  auto dma = [&](int vj, auto sc) {
+    const int kb = vblk[vj < nv ? vj : nv - 1];
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        (uint32_t)reinterpret_cast<uintptr_t>(&slot(sc)[crow][cpart * 4096]));
+    const uint64_t a = (uint64_t)reinterpret_cast<uintptr_t>(kvsrc + (int64_t)kb * kKVBlock * (int64_t)sizeof(T));
+    // (readfirstlane returns int: each half goes through uint32_t so the low half is not
+    // sign-extended into the high one)
+    const char* src = reinterpret_cast<const char*>(
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t va = gofs[s], ma = dst + 1024u * s;
+      // s_nop 4: the base address comes from v_readfirstlane (a VALU write of the SGPRs), and a
+      // VMEM instruction may read an SGPR written by VALU only 5 wait states later; the compiler
+      // inserts those for its own instructions but not for inline asm
+      asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(src), "{m0}"(ma) : "memory");
+    }
+  };
+  // operand reads: K of row r, 32-key tile kt (A operand of S^T, k-steps j = 0, 1); V^T of
+  // row r, tile kt (A operand of O^T)
+  auto read_k = [&](auto sc, int r, int kt, V8* k) {
+    const int key = 32 * kt + col;
+    const char* base = &slot(sc)[r][key * 64];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) k[j] = *reinterpret_cast<const V8*>(base + (((2 * j + hl) ^ ((key >> 2) & 3)) << 4));
+  };
+  auto read_v = [&](auto sc, int r, int kt, V8* v) {
+    const char* base = &slot(sc)[r][4096 + col * 128];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      v[j] = *reinterpret_cast<const V8*>(base + (((4 * kt + 2 * j + hl) ^ ((col >> 1) & 7)) << 4));
+  };
+  auto load_bias = [&](int vj, int kt, V8* b) {
+    const int kb = vblk[vj < nv ? vj : nv - 1];
+    const T* p = bq + (int64_t)(2 * kb + kt) * 1024;
+    b[0] = ldg<V8>(p);
+    b[1] = ldg<V8>(p + 512);
+  };
+
+  f32x16 o[2], cinit[2], S[2];
+  float l[2] = {0.f, 0.f};
+  bool first[2] = {true, true};
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    o[r] = f32x16{};
+    cinit[r] = f32x16{};
+  }
+  V8 P[2][2], vop[2][2];
+  V8 b0[2], b1[2];  // bias operands of the current (or next) visit's 32-key tiles 0 and 1
+
+  auto scores = [&](int r, const V8* k, const V8* b) {
+    f32x16 s = Mma<T>::m32(ident[r][0], b[0], cinit[r]);
+    s = Mma<T>::m32(ident[r][1], b[1], s);
+    s = Mma<T>::m32(k[0], qop[r][0], s);
+    return Mma<T>::m32(k[1], qop[r][1], s);
+  };
+
+  // One stage: exponentials of row r's tile (key bits tb) in S[r]; the PV MFMAs of the other
+  // row's previous tile (P[1 - r], vop[1 - r]) and the score MFMAs of the next tile (row rn,
+  // K operands kn, bias bn, into S[rn]) are interleaved with them.
+  auto stage = [&](int r, unsigned int tb, bool pv, int rn, const V8* kn, const V8* bn) {
+    if (pv) {
+      o[1 - r] = Mma<T>::m32(vop[1 - r][0], P[1 - r][0], o[1 - r]);
+      o[1 - r] = Mma<T>::m32(vop[1 - r][1], P[1 - r][1], o[1 - r]);
+    }
+    f32x16 s = S[r];
+    if (tb != 0xffffffffu) {  // partial tile (wave-uniform): masked keys get probability 0
+      const unsigned int lb = tb >> (4 * hl);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[v] = ((lb >> (8 * (v / 4) + (v % 4))) & 1u) ? s[v] : -INFINITY;
+    }
+    S[rn] = scores(rn, kn, bn);
+    float e[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) e[v] = fast_exp2(s[v]);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      P[r][0][v] = (T)e[v];
+      P[r][1][v] = (T)e[8 + v];
+    }
+    pin(P[r][0]);
+    pin(P[r][1]);
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int v = 0; v < w; ++v) e[v] += e[v + w];
+    float ps = e[0];
+    const bool over = !(ps <= Mma<T>::kMaxP);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+    }
+    // ---- rare: the first tile with a valid key sets the exact max; later tiles raise it only
+    // ---- when a probability could overflow the I/O type ----
+    if ((__ballot(over) != 0) | (first[r] & (tb != 0))) {
+      float mr = s[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mr = fmaxf(mr, s[v]);
+      mr = halves_max(mr);
+      const float mt = first[r] ? mr : fmaxf(mr, 0.f);
+      float e2[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) e2[v] = fast_exp2(s[v] - mt);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        P[r][0][v] = (T)e2[v];
+        P[r][1][v] = (T)e2[8 + v];
+      }
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int v = 0; v < w; ++v) e2[v] += e2[v + w];
+      ps = e2[0];
+      if (!first[r]) {  // O and l are still zero before the first valid tile
+        const float alpha = fast_exp2(-mt);
+        o[r] *= alpha;
+        l[r] *= alpha;
+      }
+      cinit[r] -= mt;
+      first[r] = false;
+    }
+    l[r] += ps;
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  // ---- prologue: KV blocks 0..2 in flight, bias of visit 0, wait for blocks 0 and 1, scores
+  // ---- of the first stage (visit 0, tile 0, row 0) ----
+  dma(0, I0{});
+  dma(1, I1{});
+  dma(2, I2{});
+  load_bias(0, 0, b0);
+  load_bias(0, 1, b1);
+  vmcnt_wait<8>();
+  __builtin_amdgcn_s_barrier();
+  {
+    V8 k[2];
+    read_k(I0{}, 0, 0, k);
+    S[0] = scores(0, k, b0);
+  }
+
+  // One 64-key block (visit vj in LDS slot SL = vj % 4): four stages (kt, r).  Each bias
+  // register set is reloaded right after its last use: tile 0 of visit vj + 1 after the first
+  // stage, tile 1 after the last stage's copy of block vj + 3.  So no copy sits between a bias
+  // load and its first use, and behind the copy of block vj + 1 (issued two blocks earlier) there
+  // are exactly 12 memory operations when the last stage waits for it; the barrier that follows
+  // publishes block vj + 1 and frees the slot of block vj - 1 for the copy of block vj + 3.
+  auto block = [&](int vj, auto slc) {
+    constexpr int SL = decltype(slc)::value;
+    using SN = std::integral_constant<int, (SL + 1) % kRing>;
+    using SC = std::integral_constant<int, (SL + 3) % kRing>;
+    const int kb = vblk[vj];
+    const unsigned long long kv0 = kvalid[0][kb], kv1 = kvalid[1][kb];
+    V8 k[2];
+    // stage (kt 0, row 0): next = (0, row 1)
+    read_k(slc, 1, 0, k);
+    read_v(slc, 0, 0, vop[0]);
+    stage(0, (unsigned int)kv0, vj > 0, 1, k, b0);
+    load_bias(vj + 1, 0, b0);
+    // stage (kt 0, row 1): next = (1, row 0)
+    read_k(slc, 0, 1, k);
+    read_v(slc, 1, 0, vop[1]);
+    stage(1, (unsigned int)kv1, true, 0, k, b1);
+    // stage (kt 1, row 0): next = (1, row 1)
+    read_k(slc, 1, 1, k);
+    read_v(slc, 0, 1, vop[0]);
+    stage(0, (unsigned int)(kv0 >> 32), true, 1, k, b1);
+    // stage (kt 1, row 1): next = (visit vj + 1, kt 0, row 0)
+    vmcnt_wait<12>();  // this wave's copy of block vj + 1 has landed
+    asm volatile("s_barrier" ::: "memory");
+    read_k(SN{}, 0, 0, k);
+    read_v(slc, 1, 1, vop[1]);
+    stage(1, (unsigned int)(kv1 >> 32), true, 0, k, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    dma(vj + 3, SC{});
+    load_bias(vj + 1, 1, b1);
+  };
+  for (int vj = 0; vj < nv; vj += 4) {
+    block(vj, I0{});
+    if (vj + 1 < nv) block(vj + 1, I1{});
+    if (vj + 2 < nv) block(vj + 2, I2{});
+    if (vj + 3 < nv) block(vj + 3, I3{});
+  }
+  // ---- epilogue: PV of the last stage (row 1) ----
+  o[1] = Mma<T>::m32(vop[1][0], P[1][0], o[1]);
+  o[1] = Mma<T>::m32(vop[1][1], P[1][1], o[1]);
+
+  // ---- normalise and store O[i, q, h*D + d] ----
+  const int qo = 32 * qt + col;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const float inv = 1.0f / halves_sum(l[r]);
+    if (qo < N && (r == 0 || i1v < N)) {
+      T* dst = out + (int64_t)irow[r] * so0 + (int64_t)qo * so1 + (int64_t)h * D + 4 * hl;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        V4 w4 = {(T)(o[r][4 * g] * inv), (T)(o[r][4 * g + 1] * inv), (T)(o[r][4 * g + 2] * inv),
+                 (T)(o[r][4 * g + 3] * inv)};
+        stg<V4>(dst + 8 * g, w4);
+      }
+    }
+  }
+}
+
 template <typename T>
 static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                       const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
@@ -552,6 +894,17 @@ template <typename T>
 static int tri_attention_t(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
                            int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
                            hipStream_t st) {
+#ifdef TOPS_TRI_TWO_ROW  // off: not yet run on the GPU since its wait-state fix
+  {
+    const int nqc = (int)((N + 127) / 128), nrp = (int)((N + 1) / 2);
+    const int64_t grid = (int64_t)H * nrp * nqc;
+    if (grid == 0) return TOPS_OK;
+    hipLaunchKernelGGL((tri_attn2_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Qp, (const T*)KV,
+                       (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, (int)N, (int)ldn, (int)H,
+                       nqc, nrp);
+    return launched("tops_tri_attention");
+  }
+#endif
   const int qt = N <= 128 ? 1 : 2;
   const int64_t per_block = 4 * 32 * qt;
   const int nqc = (int)((N + per_block - 1) / per_block);
@@ -582,7 +935,9 @@ extern "C" int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void
   TOPS_REQUIRE(C == 128 && H == 4 && D == 32,
                "tops_tri_prep: supports C == 128, H == 4, D == 32 (got %lld, %lld, %lld)", (long long)C,
                (long long)H, (long long)D);
-  TOPS_REQUIRE(N >= 0 && N <= 4096 && ldn >= N && ldn % 64 == 0, "tops_tri_prep: bad N / ldn");
+  TOPS_REQUIRE(N >= 0 && N <= kMaxN, "tops_tri_prep: supports N <= %d (got %lld)", kMaxN, (long long)N);
+  TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_prep: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
+               (long long)tri_ldn(N), (long long)ldn);
   TOPS_REQUIRE(sx0 % 8 == 0 && sx1 % 8 == 0 && (uintptr_t)x % 16 == 0,
                "tops_tri_prep: x needs token strides that are multiples of 8 and a 16-byte aligned base");
   hipStream_t st = (hipStream_t)stream;
@@ -601,7 +956,9 @@ extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bi
   TOPS_REQUIRE(Qp && KV && bias && out, "tops_tri_attention: null pointer argument");
   TOPS_REQUIRE(D == 32 && H >= 1 && H <= 64, "tops_tri_attention: supports D == 32 (got D=%lld H=%lld)", (long long)D,
                (long long)H);
-  TOPS_REQUIRE(N >= 0 && N <= 4096 && ldn >= N && ldn % 64 == 0, "tops_tri_attention: bad N / ldn");
+  TOPS_REQUIRE(N >= 0 && N <= kMaxN, "tops_tri_attention: supports N <= %d (got %lld)", kMaxN, (long long)N);
+  TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_attention: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
+               (long long)tri_ldn(N), (long long)ldn);
   TOPS_REQUIRE(so0 % 4 == 0 && so1 % 4 == 0, "tops_tri_attention: out strides must be multiples of 4");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)

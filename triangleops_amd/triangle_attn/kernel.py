@@ -48,8 +48,7 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
     H, _, D, _ = wqkv.shape
     code = io_dtype_code(X.dtype)
     _native.check_device(X, wqkv, WZ_c, W_ln)
-    if X.stride(2) != 1 or X.stride(0) % 8 or X.stride(1) % 8:
-        X = X.contiguous()
+    X = _native.vec16(X)
     ldn = row_stride(N)
     Qp = torch.empty(N, H, ldn, D, device=X.device, dtype=X.dtype)
     KV = torch.empty(N, H, ldn // 64, 4096, device=X.device, dtype=X.dtype)
@@ -85,9 +84,14 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
 LOG2E = 1.4426950408889634
 
 
-def fast_shape(C, H, D, C_out=None):
-    """True when the tuned kernels apply: C_in = 128, H = 4, D = 32 (and C_out = 128)."""
-    return C == 128 and H == 4 and D == 32 and (C_out is None or C_out == 128)
+TUNED_MAX_N = 16384  # largest N of tops_tri_prep / tops_tri_attention (per-row key-block tables in LDS)
+
+
+def fast_shape(C, H, D, C_out=None, N=None):
+    """True when the tuned kernels apply: C_in = 128, H = 4, D = 32 (and C_out = 128) and N within
+    the tuned kernels' limit; every other call runs the any-shape kernels."""
+    return (C == 128 and H == 4 and D == 32 and (C_out is None or C_out == 128)
+            and (N is None or N <= TUNED_MAX_N))
 
 
 def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=True):
@@ -225,7 +229,7 @@ def triangle_attn_forward(
     assert WKV_c.shape == (C, 2 * H * D)
     assert out.shape == (N, N, H * D)
     wqkv = wqkv_from_layouts(_as(X_ln, WQ_c), _as(X_ln, WKV_c), H, D, _as(X_ln, WK_c), _as(X_ln, WV_c))
-    if not fast_shape(C, H, D) or X_ln.dtype == torch.float32:
+    if not fast_shape(C, H, D, N=N) or X_ln.dtype == torch.float32:
         xln, q, k, v, bias = generic_prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, apply_ln=False)
         if Bias_buf is not None:
             Bias_buf.copy_(bias)
@@ -244,7 +248,7 @@ def _residual_views(o, residual, out, Cout, aligned):
     assert residual.shape == (N1, N2, Cout), "residual must be (N1, N2, C_out)"
     _native.check_device(o, residual, out)
     if residual.dtype != o.dtype or not aligned(residual):
-        residual = residual.to(o.dtype).contiguous()
+        residual = residual.to(o.dtype).clone(memory_format=torch.contiguous_format)
     if out is None:
         out = torch.empty(N1, N2, Cout, device=o.device, dtype=o.dtype)
     assert out.shape == (N1, N2, Cout) and out.dtype == o.dtype, "out must be (N1, N2, C_out) of the I/O dtype"
@@ -266,11 +270,8 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None, residual=None, out=
     assert out is None or residual is not None, "out= is supported together with residual="
     if not (C == 128 and Cin == 128 and W_o.shape[0] == 128) or o.dtype == torch.float32:
         return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln, residual=residual, out=out)
-    if o.stride(2) != 1 or o.stride(0) % 8 or o.stride(1) % 8 or o.data_ptr() % 16:
-        o = o.contiguous()
-    gin = gin.reshape(N1, N2, C) if gin.dim() != 3 else gin
-    if gin.stride(2) != 1 or gin.stride(0) % 8 or gin.stride(1) % 8 or gin.data_ptr() % 16:
-        gin = gin.contiguous()
+    o = _native.vec16(o)
+    gin = _native.vec16(gin.reshape(N1, N2, C) if gin.dim() != 3 else gin)
     w_ln = b_ln = None
     eps = 1e-5
     if ln is not None:
@@ -283,10 +284,7 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None, residual=None, out=
         _native.call("tops_gate_out", *args, out.data_ptr(), N1, N2, C, io_dtype_code(o.dtype), _native.stream_of(o))
         return out
 
-    def aligned(t):
-        return t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0
-
-    residual, out = _residual_views(o, residual, out, C, aligned)
+    residual, out = _residual_views(o, residual, out, C, _native.vec16_ok)
     _native.call("tops_gate_out_residual", *args, residual.data_ptr(), residual.stride(0), residual.stride(1),
                  out.data_ptr(), out.stride(0), out.stride(1), N1, N2, C, io_dtype_code(o.dtype), _native.stream_of(o))
     return out

@@ -59,8 +59,8 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
     if wqkv.dtype != X.dtype:
         wqkv = wqkv.to(X.dtype)
     H, _, D, C = wqkv.shape
-    if not fast_shape(C, H, D, W_proj_o.shape[0]) or X.dtype == torch.float32:
-        # any-shape kernels: other shapes (e.g. D = 16, C_in = 64) and fp32 I/O
+    if not fast_shape(C, H, D, W_proj_o.shape[0], N) or X.dtype == torch.float32:
+        # any-shape kernels: other shapes (e.g. D = 16, C_in = 64), N above the tuned limit, fp32 I/O
         xln, q, k, v, bias = generic_prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], eps=eps)
         O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
         generic_attention(q, k, v, bias, O, scale=scale, mask=mask)
