@@ -172,6 +172,23 @@ int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0
                      int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
 
 /*
+ * tops_apb_forward without allocation: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same computation and arguments as tops_apb_forward minus `work`; the workspace is
+ * a library-owned static device array of 16 MiB per GPU (held until the process ends), so calls
+ * with tops_apb_workspace_bytes(M, H, D) > 16 MiB return TOPS_EINVAL (M up to 16384 on a 256-CU
+ * MI355X).  The entry point allocates nothing and calls no allocating routine; the array's device
+ * address is looked up once per device on the first call made with that device current.  Every
+ * call on one GPU shares that GPU's array: calls that overlap in time on one GPU (other streams,
+ * other threads) race; calls ordered on one stream do not.  Nothing in the array needs to start
+ * at zero (each call writes every byte it reads).
+ */
+int tops_apb_forward_noalloc(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
+                             const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og, int64_t M,
+                             int64_t C, int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype,
+                             void* stream);
+
+/*
  * Q / K / V pre-pass and the attention with given Q / K / V.  tops_apb_forward is the two run
  * back to back (Q scaled by `scale` in the pre-pass, Q / K / V at the head of `work`).  They also
  * serve the qk-norm variant of attention_pair_bias (the K-Fold formulation the reference states

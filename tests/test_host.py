@@ -254,3 +254,15 @@ def test_vec16_copies_misaligned_views():
     x = torch.zeros(8, 8, 128, dtype=torch.bfloat16)
     t = x.transpose(0, 1)
     assert _native.vec16_ok(t) and _native.vec16(t).data_ptr() == t.data_ptr()
+
+
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+def test_apb_noalloc_rejects_oversized_call_cpu():
+    """tops_apb_forward_noalloc refuses a call whose workspace exceeds its 16 MiB static array before
+    touching the GPU (M = 65536 needs 48 MiB of Q/K/V alone)."""
+    lib = _native.load()
+    assert lib.tops_apb_workspace_bytes(65536, 4, 32) > 16 << 20
+    fake = ctypes.c_void_p(1 << 20)
+    rc = lib.tops_apb_forward_noalloc(fake, fake, fake, 128 * 65536, 128, fake, fake, fake, None, fake, 65536, 128, 128,
+                                      4, 32, 1.0, 1e-5, 2, None)
+    assert rc == 1 and b"static workspace" in lib.tops_last_error()

@@ -36,6 +36,9 @@ _SIGNATURES = {
     "tops_apb_forward": [
         _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],
+    "tops_apb_forward_noalloc": [
+        _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
+    ],
     "tops_apb_forward_qkv": [
         _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],

@@ -22,6 +22,7 @@
 //
 // Reference: attn_pair_bias/kernel.py:24-202 (`_apb_kernel`), :205-257 (`apb_forward`);
 // the key mask follows benchmarks/references.py:273-274 (masked keys -> -inf).
+#include <mutex>
 #include <type_traits>
 
 #include "capi.hpp"
@@ -541,20 +542,79 @@ extern "C" int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D) {
   return apb_qkv_bytes(M) + part;
 }
 
+// The workspace of tops_apb_forward_noalloc: a library-owned array in device memory (one copy per
+// GPU the library runs on, held until the process ends).  Host code never uses the array's name
+// as an address: its device address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kApbScratchBytes = 16LL << 20;
+static __device__ __align__(256) char scratch[kApbScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+}  // namespace
+
+static int apb_forward_impl(const char* who, const void* X, const void* wqkv, const void* Z, int64_t sz0,
+                            int64_t sz1, const float* Wc, const float* sWc, const float* Bc, const void* mask,
+                            void* Og, void* work, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float scale,
+                            float eps, int dtype, void* stream);
+
+extern "C" int tops_apb_forward_noalloc(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
+                                        const float* Wc, const float* sWc, const float* Bc, const void* mask,
+                                        void* Og, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float scale,
+                                        float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc && Og, "tops_apb_forward_noalloc: null pointer argument");
+  TOPS_REQUIRE(C == 128 && Cz == 128 && H == 4 && D == 32,
+               "tops_apb_forward_noalloc: supports C == Cz == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld D=%lld)",
+               (long long)C, (long long)Cz, (long long)H, (long long)D);
+  TOPS_REQUIRE(M >= 0, "tops_apb_forward_noalloc: bad M");
+  const int64_t need = tops_apb_workspace_bytes(M, H, D);
+  TOPS_REQUIRE(need <= kApbScratchBytes,
+               "tops_apb_forward_noalloc: M = %lld needs %lld workspace bytes, more than the library's %lld-byte "
+               "static workspace; use tops_apb_forward with a caller-allocated workspace",
+               (long long)M, (long long)need, (long long)kApbScratchBytes);
+  if (M == 0) return TOPS_OK;
+  int dev = 0;
+  TOPS_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64,
+               "tops_apb_forward_noalloc: no current HIP device");
+  void* ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(TOPS_ELAUNCH, "tops_apb_forward_noalloc: hipGetSymbolAddress of the workspace failed: %s",
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev] = p;
+    }
+    ws = g_scratch_ptr[dev];
+  }
+  return apb_forward_impl("tops_apb_forward_noalloc", X, wqkv, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, ws, M, C, Cz, H,
+                          D, scale, eps, dtype, stream);
+}
+
 extern "C" int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
                                 const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og,
                                 void* work, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float scale,
                                 float eps, int dtype, void* stream) {
-  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc && Og, "tops_apb_forward: null pointer argument");
+  return apb_forward_impl("tops_apb_forward", X, wqkv, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, C, Cz, H, D,
+                          scale, eps, dtype, stream);
+}
+
+static int apb_forward_impl(const char* who, const void* X, const void* wqkv, const void* Z, int64_t sz0,
+                            int64_t sz1, const float* Wc, const float* sWc, const float* Bc, const void* mask,
+                            void* Og, void* work, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float scale,
+                            float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc && Og, "%s: null pointer argument", who);
   TOPS_REQUIRE(C == 128 && Cz == 128 && H == 4 && D == 32,
-               "tops_apb_forward: supports C == Cz == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld D=%lld)",
-               (long long)C, (long long)Cz, (long long)H, (long long)D);
-  TOPS_REQUIRE(M >= 0, "tops_apb_forward: bad M");
-  TOPS_REQUIRE(work || M == 0, "tops_apb_forward: workspace of tops_apb_workspace_bytes(M, H, D) bytes required");
+               "%s: supports C == Cz == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld D=%lld)", who, (long long)C,
+               (long long)Cz, (long long)H, (long long)D);
+  TOPS_REQUIRE(M >= 0, "%s: bad M", who);
+  TOPS_REQUIRE(work || M == 0, "%s: workspace of tops_apb_workspace_bytes(M, H, D) bytes required", who);
   TOPS_REQUIRE(sz0 % 8 == 0 && sz1 % 8 == 0 && (uintptr_t)Z % 16 == 0 && (uintptr_t)X % 16 == 0 &&
                    (uintptr_t)work % 16 == 0,
-               "tops_apb_forward: Z needs token strides that are multiples of 8, and Z, X and the workspace "
-               "16-byte aligned base pointers");
+               "%s: Z needs token strides that are multiples of 8, and Z, X and the workspace 16-byte aligned base "
+               "pointers", who);
   if (M == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
   char* w = (char*)work;
@@ -568,7 +628,7 @@ extern "C" int tops_apb_forward(const void* X, const void* wqkv, const void* Z, 
     rc = apb_qkv_t<_Float16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
     return rc != TOPS_OK ? rc : apb_attention_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st);
   }
-  return fail(TOPS_EUNSUPPORTED, "tops_apb_forward: unsupported dtype code %d", dtype);
+  return fail(TOPS_EUNSUPPORTED, "%s: unsupported dtype code %d", who, dtype);
 }
 
 extern "C" int tops_apb_forward_qkv(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0,
