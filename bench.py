@@ -180,6 +180,43 @@ def torch_tri(d, eps=1e-5):
     return F.linear(o * g, d["W_proj_o"])
 
 
+def tri_inputs_shape(N, Cin, Hh, Dd, seed=0):
+    """triangle attention inputs at another shape (the Apo shape: C_in = 64, H = 4, D = 16)."""
+    g = _gen(seed)
+    s = Cin**-0.5
+    d = dict(
+        X=torch.randn(N, N, Cin, generator=g),
+        W_ln=1 + 0.1 * torch.randn(Cin, generator=g),
+        B_ln=0.1 * torch.randn(Cin, generator=g),
+        WQ=torch.randn(Cin, Hh * Dd, generator=g) * s,
+        WK=torch.randn(Cin, Hh * Dd, generator=g) * s,
+        WV=torch.randn(Cin, Hh * Dd, generator=g) * s,
+        W_proj_z=torch.randn(Cin, Hh, generator=g) * s,
+        B_proj_z=torch.zeros(Hh),
+        W_proj_g=torch.randn(Hh * Dd, Cin, generator=g) * s,
+        W_proj_o=torch.randn(Cin, Hh * Dd, generator=g) * (Hh * Dd) ** -0.5,
+    )
+    d = {k: v.to(torch.bfloat16) for k, v in d.items()}
+    d["mask"] = pad_mask2(N)
+    return d
+
+
+def torch_tri_shape(d, Hh, Dd, eps=1e-5):
+    """torch_tri at any (C_in, H, D)."""
+    X = d["X"]
+    N, _, Cin = X.shape
+    xln = F.layer_norm(X, (Cin,), d["W_ln"], d["B_ln"], eps=eps)
+    q = (xln @ d["WQ"]).view(N, N, Hh, Dd).permute(0, 2, 1, 3)
+    k = (xln @ d["WK"]).view(N, N, Hh, Dd).permute(0, 2, 3, 1).contiguous()
+    v = (xln @ d["WV"]).view(N, N, Hh, Dd).permute(0, 2, 1, 3).contiguous()
+    bp = (xln @ d["W_proj_z"] + d["B_proj_z"]).permute(2, 0, 1).unsqueeze(0)
+    scores = torch.matmul((q * Dd**-0.5).contiguous(), k) + bp
+    scores = scores + torch.where(d["mask"][:, None, None, :], 0.0, -1e9).to(scores.dtype)
+    o = torch.matmul(torch.softmax(scores, -1), v).permute(0, 2, 1, 3).reshape(N, N, Hh * Dd)
+    g = torch.sigmoid(F.linear(xln, d["W_proj_g"]))
+    return F.linear(o * g, d["W_proj_o"])
+
+
 def torch_apb(d, eps=1e-5):
     X, Z = d["X"], d["Z"]
     M = X.shape[0]
@@ -574,6 +611,33 @@ def sweep(path, sizes, dev):
             f.flush()
             rows.append(r)
             del d, pre
+        # the Apo shape (C_in = 64, H = 4, D = 16): any-shape pre-pass, repack, the MFMA attention
+        # kernel with D padded to 32, any-shape gate; the scalar any-shape attention timed beside it
+        for N in [n for n in sizes if n in (256, 1024)]:
+            torch.cuda.empty_cache()
+            from triangleops_amd.triangle_attn.kernel import generic_attention, generic_prep_forward, padded_attention
+            d = to_dev(tri_inputs_shape(N, 64, 4, 16), dev)
+            pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                                d["B_proj_z"], 4, 16)
+            it, wu = (20, 5) if N <= 512 else (10, 3)
+            fwd = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=16**-0.5,  # noqa: E731
+                                                     W_proj_g=d["W_proj_g"], B_proj_g=None,
+                                                     W_proj_o=d["W_proj_o"], B_proj_o=None)
+            ms = time_ms(fwd, it, wu)
+            tms = time_ms(lambda: torch_tri_shape(d, 4, 16), 3, 1)
+            xln, q, k, v, bias = generic_prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"],
+                                                      pre["BZ"])
+            o = torch.empty(N, N, 64, device=dev, dtype=torch.bfloat16)
+            ms_att = time_ms(lambda: padded_attention(q, k, v, bias, o, scale=16**-0.5, mask=d["mask"]), it, wu)
+            ms_scalar = time_ms(lambda: generic_attention(q, k, v, bias, o, scale=16**-0.5, mask=d["mask"]), 2, 1)
+            r = {"op": "triangle_attention_apo", "shape": "C_in=64 H=4 D=16", "size": N, "ms": round(ms, 4),
+                 "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4),
+                 "attention_ms_mfma_padded": round(ms_att, 4), "attention_ms_scalar": round(ms_scalar, 4),
+                 "kernels": {}}
+            f.write(json.dumps(r) + "\n")
+            f.flush()
+            rows.append(r)
+            del d, pre, xln, q, k, v, bias, o
         for M in sizes:
             torch.cuda.empty_cache()
             d = to_dev(apb_inputs(M), dev)

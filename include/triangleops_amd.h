@@ -110,6 +110,21 @@ int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const v
                        void* stream);
 
 /*
+ * Repack for triangle attention at shapes the pre-pass does not cover (any H <= 64, D <= 32; e.g.
+ * the D = 16, C_in = 64 "Apo" shape of tests/test_triangle_attn.py:137-192, which the reference runs
+ * on its tensor-core kernel: triangle_attn/kernel.py:211-213, :282): the any-shape pre-pass's
+ *   q, k, v io (N, N, H, D) contiguous and bias fp32 (H, N, N) (tops_tri_generic_prep)
+ * rewritten into tops_tri_attention's layouts with D zero-padded to 32:
+ *   Qp     io   (N, H, ldn, 32): scale * log2(e) * q, d permuted as in tops_tri_prep, zero for d >= D
+ *   KV     io   (N, H, ldn/64, 4096): K and V^T as in tops_tri_prep, zero for d >= D or keys >= N
+ *   btiles io   (H, ceil(N/32), ldn/32, 1024): log2(e) * bias in tops_tri_prep's tile order
+ * tops_tri_attention then writes O with 32 columns per head, of which the first D are the result.
+ * N <= 16384, ldn = max(64, round_up(N, 64)); bf16 / fp16.
+ */
+int tops_tri_repack(const void* q, const void* k, const void* v, const float* bias, void* Qp, void* KV, void* btiles,
+                    int64_t N, int64_t ldn, int64_t H, int64_t D, float scale, int dtype, void* stream);
+
+/*
  * Gate + output projection over M1*M2 tokens.  Replaces `fused_gate_forward` /
  * `fused_gate_kernel` (triangle_attn/kernel.py:387-470) and the apb epilogue
  * (attn_pair_bias/module.py:69-70):

@@ -381,6 +381,35 @@ def test_tri_apo_d16(device, masked):
     _check(out, _tri_ref(inp), torch.bfloat16, f"tri Apo masked={masked}")
 
 
+@pytest.mark.parametrize("N,mask", [(256, "pad"), (520, "random")])
+def test_tri_apo_mfma_path_sampled_rows(device, N, mask):
+    """The Apo shape (C_in = 64, H = 4, D = 16) at larger N runs the MFMA attention kernel after
+    tops_tri_repack (D zero-padded to 32): starting and ending node on sampled rows, and the padded
+    path equals the any-shape scalar attention within the bf16 bar on the same pre-pass outputs."""
+    from triangleops_amd.triangle_attn.kernel import (generic_attention, generic_prep_forward, padded_attention,
+                                                      padded_ok)
+
+    inp = tri_inputs(N, C=64, H=4, D=16, seed=N + 17, mask=mask, bias_z=True)
+    assert padded_ok(N, 4, 16, torch.bfloat16)
+    out = _tri_call(inp, device)
+    rows = torch.tensor([0, N // 3, N // 2, N - 1])
+    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri Apo N={N} start")
+    Xd = inp["X"].to(device)
+    out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
+    exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T, rows=rows)
+    _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri Apo N={N} end")
+    d = to_dev(inp, device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], 4, 16)
+    xln, q, k, v, bias = generic_prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"],
+                                              pre["BZ"])
+    a = padded_attention(q, k, v, bias, torch.empty(N, N, 64, device=device, dtype=torch.bfloat16),
+                         scale=inp["scale"], mask=d["mask"])
+    b = generic_attention(q, k, v, bias, torch.empty(N, N, 64, device=device, dtype=torch.bfloat16),
+                          scale=inp["scale"], mask=d["mask"])
+    _check(a[rows].cpu(), b[rows].float().cpu(), torch.bfloat16, f"tri Apo N={N} padded vs scalar attention")
+
+
 @pytest.mark.parametrize("N,C,H,D", [(40, 96, 3, 24), (70, 64, 2, 64), (130, 32, 8, 8), (257, 64, 4, 16)])
 @pytest.mark.parametrize("mask", ["pad", "random"])
 def test_tri_any_shape(device, N, C, H, D, mask):

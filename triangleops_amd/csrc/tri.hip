@@ -876,6 +876,103 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Repack for the shapes the pre-pass does not cover: the any-shape pre-pass's plain Q / K / V
+// (N, N, H, D) and fp32 pair bias (H, N, N) rewritten into the attention kernel's layouts with
+// D zero-padded to 32 (any D <= 32, any H), so that triangle attention at those shapes (e.g. the
+// D = 16, C_in = 64 "Apo" shape) runs on the MFMA attention kernel; the padded dimensions are
+// zero in Q, K and V, so they add nothing to the scores and give zero output columns.
+// One thread per 16-byte output chunk; reads past N or D give zeros (finite padding, as the
+// attention kernel requires).
+//   what 0: Qp    chunk (row r = (i H + h) ldn + p, c < 4): d-permuted elements 8c .. 8c + 7
+//   what 1: KV    chunk (block (i H + h) nkb + kb, m < 512): m < 256 -> K row m / 4, chunk m % 4;
+//                 else V^T row d = (m - 256) / 8, chunk (m - 256) % 8 (keys permuted per 32)
+//   what 2: bias  chunk (tile (h nqt + qt) nkt + kt, ch < 128): elements 8 ch .. 8 ch + 7
+// ---------------------------------------------------------------------------------------------
+__device__ inline int perm32(int x) {  // position x of a permuted group of 32 -> natural index
+  const int j = x >> 4, hl = (x >> 3) & 1, e = x & 7;
+  return 16 * j + 8 * (e >> 2) + 4 * hl + (e & 3);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tri_repack_kernel(int what, const T* __restrict__ q, const T* __restrict__ k,
+                                                        const T* __restrict__ v, const float* __restrict__ bias,
+                                                        T* __restrict__ dst, int64_t nchunks, int N, int ldn, int H,
+                                                        int D, float qscale) {
+  using V8 = vec<T, 8>;
+  const int nkb = ldn / 64, nqt = (N + 31) / 32, nkt = ldn / 32;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < nchunks; idx += (int64_t)gridDim.x * 256) {
+    V8 out;
+    if (what == 0) {
+      const int c = (int)(idx & 3);
+      const int64_t r = idx >> 2;
+      const int p = (int)(r % ldn);
+      const int64_t ih = r / ldn;
+      const int h = (int)(ih % H);
+      const int64_t i = ih / H;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = perm32(8 * c + e);
+        out[e] = (p < N && d < D) ? (T)((float)q[((i * N + p) * H + h) * D + d] * qscale) : (T)0.f;
+      }
+    } else if (what == 1) {
+      const int m = (int)(idx & 511);
+      const int64_t blk = idx >> 9;
+      const int kb = (int)(blk % nkb);
+      const int64_t ih = blk / nkb;
+      const int h = (int)(ih % H);
+      const int64_t i = ih / H;
+      if (m < 256) {
+        const int key = 64 * kb + (m >> 2), c = m & 3;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = perm32(8 * c + e);
+          out[e] = (key < N && d < D) ? k[((i * N + key) * H + h) * D + d] : (T)0.f;
+        }
+      } else {
+        const int d = (m - 256) >> 3, c = (m - 256) & 7;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int kappa = 8 * c + e;
+          const int key = 64 * kb + 32 * (kappa >> 5) + perm32(kappa & 31);
+          out[e] = (key < N && d < D) ? v[((i * N + key) * H + h) * D + d] : (T)0.f;
+        }
+      }
+    } else {
+      const int ch = (int)(idx & 127);
+      const int64_t tile = idx >> 7;
+      const int kt = (int)(tile % nkt);
+      const int64_t hq = tile / nkt;
+      const int qt = (int)(hq % nqt);
+      const int h = (int)(hq / nqt);
+      const int j = ch >> 6, hl = (ch >> 5) & 1, c = ch & 31;
+      const int qq = 32 * qt + c, k0 = 32 * kt + 16 * j + 8 * hl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        out[e] = (qq < N && k0 + e < N) ? (T)(kLog2e * bias[((int64_t)h * N + qq) * N + k0 + e]) : (T)0.f;
+    }
+    stg<V8>(dst + 8 * idx, out);
+  }
+}
+
+template <typename T>
+static int tri_repack_t(const void* q, const void* k, const void* v, const float* bias, void* Qp, void* KV,
+                        void* btiles, int64_t N, int64_t ldn, int64_t H, int64_t D, float qscale, hipStream_t st) {
+  const int64_t nkb = ldn / 64, nqt = (N + 31) / 32, nkt = ldn / 32;
+  const int64_t n[3] = {N * H * ldn * 4, N * H * nkb * 512, H * nqt * nkt * 128};
+  void* dst[3] = {Qp, KV, btiles};
+  for (int w = 0; w < 3; ++w) {
+    if (n[w] == 0) continue;
+    const int64_t want = (n[w] + 255) / 256, cap = 64LL * num_cus();
+    const unsigned grid = (unsigned)(want < cap ? want : cap);
+    hipLaunchKernelGGL((tri_repack_kernel<T>), dim3(grid), dim3(256), 0, st, w, (const T*)q, (const T*)k,
+                       (const T*)v, bias, (T*)dst[w], n[w], (int)N, (int)ldn, (int)H, (int)D, qscale);
+    const int rc = launched("tops_tri_repack");
+    if (rc != TOPS_OK) return rc;
+  }
+  return TOPS_OK;
+}
+
 template <typename T>
 static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                       const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
@@ -966,4 +1063,20 @@ extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bi
   if (dtype == TOPS_DTYPE_F16)
     return tri_attention_t<_Float16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_attention: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_tri_repack(const void* q, const void* k, const void* v, const float* bias, void* Qp, void* KV,
+                               void* btiles, int64_t N, int64_t ldn, int64_t H, int64_t D, float scale, int dtype,
+                               void* stream) {
+  TOPS_REQUIRE(q && k && v && bias && Qp && KV && btiles, "tops_tri_repack: null pointer argument");
+  TOPS_REQUIRE(N >= 0 && N <= kMaxN, "tops_tri_repack: supports N <= %d (got %lld)", kMaxN, (long long)N);
+  TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_repack: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
+               (long long)tri_ldn(N), (long long)ldn);
+  TOPS_REQUIRE(H >= 1 && H <= 64 && D >= 1 && D <= 32, "tops_tri_repack: supports H <= 64, D <= 32 (got %lld, %lld)",
+               (long long)H, (long long)D);
+  hipStream_t st = (hipStream_t)stream;
+  const float qscale = scale * kLog2e;
+  if (dtype == TOPS_DTYPE_BF16) return tri_repack_t<__bf16>(q, k, v, bias, Qp, KV, btiles, N, ldn, H, D, qscale, st);
+  if (dtype == TOPS_DTYPE_F16) return tri_repack_t<_Float16>(q, k, v, bias, Qp, KV, btiles, N, ldn, H, D, qscale, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_tri_repack: unsupported dtype code %d", dtype);
 }

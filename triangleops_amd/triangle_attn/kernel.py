@@ -134,6 +134,37 @@ def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=Tr
     return xln, q, k, v, bias
 
 
+def padded_ok(N, H, D, dtype):
+    """True when attention at a shape the pre-pass does not cover can run on the MFMA attention
+    kernel after tops_tri_repack: D <= 32 (zero-padded to 32), H <= 64, 16-bit I/O, N within the
+    tuned kernels' limit."""
+    return D <= 32 and H <= 64 and dtype in (torch.bfloat16, torch.float16) and N <= TUNED_MAX_N
+
+
+def padded_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
+    """generic_attention on the MFMA attention kernel: q, k, v (N, N, H, D) and the fp32 bias
+    (H, N, N) of the any-shape pre-pass are repacked into the attention kernel's layouts with D
+    zero-padded to 32 (tops_tri_repack), then tops_tri_attention runs; out (N, N, H*D)."""
+    N, _, H, D = q.shape
+    _native.check_device(q, k, v, bias, out, mask)
+    assert padded_ok(N, H, D, q.dtype) and out.shape == (N, N, H * D) and out.stride(2) == 1
+    ldn = row_stride(N)
+    dev, dt = q.device, q.dtype
+    Qp = torch.empty(N, H, ldn, 32, device=dev, dtype=dt)
+    KV = torch.empty(N, H, ldn // 64, 4096, device=dev, dtype=dt)
+    bt = torch.empty(H, (N + 31) // 32, ldn // 32, 1024, device=dev, dtype=dt)
+    q, k, v = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
+    _native.call("tops_tri_repack", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.float().contiguous().data_ptr(),
+                 Qp.data_ptr(), KV.data_ptr(), bt.data_ptr(), N, ldn, H, D, float(scale), io_dtype_code(dt),
+                 _native.stream_of(q))
+    if D == 32:
+        return attention_core(Qp, KV, bt, out, N=N, ldn=ldn, mask=mask)
+    opad = torch.empty(N, N, H * 32, device=dev, dtype=dt)
+    attention_core(Qp, KV, bt, opad, N=N, ldn=ldn, mask=mask)
+    out.copy_(opad.view(N, N, H, 32)[..., :D].reshape(N, N, H * D))
+    return out
+
+
 def generic_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
     """Any-shape attention core: out[i, q, h*D:(h+1)*D] = softmax_k(scale q.k + bias - 1e9 [masked]) v."""
     N, _, H, D = q.shape
@@ -233,6 +264,8 @@ def triangle_attn_forward(
         xln, q, k, v, bias = generic_prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, apply_ln=False)
         if Bias_buf is not None:
             Bias_buf.copy_(bias)
+        if padded_ok(N, H, D, X_ln.dtype):
+            return padded_attention(q, k, v, bias, out, scale=scale, mask=mask)
         return generic_attention(q, k, v, bias, out, scale=scale, mask=mask)
     Qp, KV, bias, ldn = prep_forward(X_ln, None, None, wqkv, WZ_c, BZ, scale=scale, apply_ln=False)
     if Bias_buf is not None:

@@ -17,7 +17,8 @@ read the transposed view in place, so no transpose copy is made.  Any N is handl
 import torch
 
 from .._common.layouts import interleave_kv, qkv_head_major
-from .kernel import attention_core, fast_shape, gate_out_forward, generic_attention, generic_prep_forward, prep_forward
+from .kernel import (attention_core, fast_shape, gate_out_forward, generic_attention, generic_prep_forward,
+                     padded_attention, padded_ok, prep_forward)
 
 
 def precompute(W_ln, B_ln, WQ, WK, WV, W_proj_z, B_proj_z, H, D):
@@ -63,7 +64,10 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
         # any-shape kernels: other shapes (e.g. D = 16, C_in = 64), N above the tuned limit, fp32 I/O
         xln, q, k, v, bias = generic_prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], eps=eps)
         O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
-        generic_attention(q, k, v, bias, O, scale=scale, mask=mask)
+        if padded_ok(N, H, D, X.dtype):  # D <= 32 in 16-bit I/O: the MFMA attention kernel, D padded
+            padded_attention(q, k, v, bias, O, scale=scale, mask=mask)
+        else:
+            generic_attention(q, k, v, bias, O, scale=scale, mask=mask)
         return gate_out_forward(O, xln, W_proj_g, None, W_proj_o, None, residual=residual, out=out)
     Qp, KV, bias, ldn = prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], scale=scale, eps=eps)
     O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
