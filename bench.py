@@ -362,16 +362,17 @@ def tmu_work(L):
     }
 
 
-def tri_phases(d, pre):
+def tri_phases(d, pre, hd=(H, D)):
     st = {}
     N = d["X"].shape[0]
+    h, dh = hd
 
     def p_prep():
         st["qp"], st["kv"], st["bias"], st["ldn"] = prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"],
-                                                                 pre["WZ_c"], pre["BZ"], scale=D**-0.5)
+                                                                 pre["WZ_c"], pre["BZ"], scale=dh**-0.5)
 
     def p_att():
-        st["o"] = torch.empty(N, N, H * D, device=d["X"].device, dtype=d["X"].dtype)
+        st["o"] = torch.empty(N, N, h * dh, device=d["X"].device, dtype=d["X"].dtype)
         attention_core(st["qp"], st["kv"], st["bias"], st["o"], N=N, ldn=st["ldn"], mask=d["mask"])
 
     def p_gate():
@@ -381,11 +382,13 @@ def tri_phases(d, pre):
     return [p_prep, p_att, p_gate]
 
 
-def tri_work(N):
+def tri_work(N, c=C, h=H, dh=D):
+    """Algorithmic work per launch at (C_in, H, D); at D = 16 the kernels carry heads zero-padded to
+    32 lanes (twice the Q / K / V bytes and attention flops counted here)."""
     return {
-        "tri_prep": ("hbm", 2 * N * N * C + 6 * N * N * H * D + 2 * H * N * N),
-        "tri_attention": ("mfma", 4 * N**3 * H * D),
-        "tri_gate_out": ("hbm", 6 * N * N * C),
+        "tri_prep": ("hbm", 2 * N * N * c + 6 * N * N * h * dh + 2 * h * N * N),
+        "tri_attention": ("mfma", 4 * N**3 * h * dh),
+        "tri_gate_out": ("hbm", 6 * N * N * c),
     }
 
 
@@ -637,11 +640,11 @@ def sweep(path, sizes, dev):
             f.flush()
             rows.append(r)
             del d, pre
-        # the Apo shape (C_in = 64, H = 4, D = 16): any-shape pre-pass, repack, the MFMA attention
-        # kernel with D padded to 32, any-shape gate; the scalar any-shape attention timed beside it
+        # the Apo shape (C_in = 64, H = 4, D = 16) on the tuned kernels (C = 64 pre-pass and gate, heads
+        # zero-padded to 32 lanes in the attention kernel); the any-shape scalar attention timed beside
         for N in [n for n in sizes if n in (256, 1024)]:
             torch.cuda.empty_cache()
-            from triangleops_amd.triangle_attn.kernel import generic_attention, generic_prep_forward, padded_attention
+            from triangleops_amd.triangle_attn.kernel import generic_attention, generic_prep_forward
             d = to_dev(tri_inputs_shape(N, 64, 4, 16), dev)
             pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
                                                 d["B_proj_z"], 4, 16)
@@ -651,15 +654,16 @@ def sweep(path, sizes, dev):
                                                      W_proj_o=d["W_proj_o"], B_proj_o=None)
             ms = time_ms(fwd, it, wu)
             tms = time_ms(lambda: torch_tri_shape(d, 4, 16), 3, 1)
+            work = tri_work(N, 64, 4, 16)
+            ph = run_phases([tri_phases(d, pre, (4, 16))], list(work), it, wu)
+            kern = {n: kernel_entry(n, ph[n], *work[n]) for n in ph}
             xln, q, k, v, bias = generic_prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"],
                                                       pre["BZ"])
             o = torch.empty(N, N, 64, device=dev, dtype=torch.bfloat16)
-            ms_att = time_ms(lambda: padded_attention(q, k, v, bias, o, scale=16**-0.5, mask=d["mask"]), it, wu)
             ms_scalar = time_ms(lambda: generic_attention(q, k, v, bias, o, scale=16**-0.5, mask=d["mask"]), 2, 1)
             r = {"op": "triangle_attention_apo", "shape": "C_in=64 H=4 D=16", "size": N, "ms": round(ms, 4),
                  "calls_per_s": round(1e3 / ms, 1), "torch_path_ms": round(tms, 4),
-                 "attention_ms_mfma_padded": round(ms_att, 4), "attention_ms_scalar": round(ms_scalar, 4),
-                 "kernels": {}}
+                 "attention_ms_scalar": round(ms_scalar, 4), "kernels": kern}
             f.write(json.dumps(r) + "\n")
             f.flush()
             rows.append(r)

@@ -83,14 +83,16 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
  *   wqkv   io   (H, 3, D, C): per head the rows of WQ^T, WK^T, WV^T
  *   WZ     io   (H, C);  BZ fp32 (H,) or NULL
  *   ldn         max(64, N rounded up to a multiple of 64); any other value is rejected (TOPS_EINVAL)
- *   Qp     io   (N, H, ldn, D): scale * log2(e) * Q, d permuted within each 32 as
- *               [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]
- *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x D, d permuted) then
- *               V^T (D x 64 keys, keys permuted the same way within each 32)
+ *   Qp     io   (N, H, ldn, 32): scale * log2(e) * Q, d permuted within each 32 as
+ *               [0-3, 8-11, 4-7, 12-15, 16-19, 24-27, 20-23, 28-31]; zero for d >= D
+ *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x 32, d permuted) then
+ *               V^T (32 x 64 keys, keys permuted the same way within each 32); zero for d >= D
  *   bias   io   (H, ceil(N/32), ldn/32, 1024): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]) per
  *               32 x 32 (query, key) tile; (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e) at
  *               element (64 j + 32 hl + c) * 8 + e of tile (qt, kt); zeros for k >= N
- * C == 128, H == 4, D == 32, N <= 16384 (tops_tri_generic_prep serves larger N).
+ * C in {128, 64}, H == 4, D in {32, 16} (the default shape and the C_in = 64, D = 16 "Apo" shape
+ * of tests/test_triangle_attn.py:137-192, which the reference runs on its tensor-core kernel:
+ * triangle_attn/kernel.py:211-213), N <= 16384 (tops_tri_generic_prep serves other shapes).
  */
 int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                   const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
@@ -100,10 +102,12 @@ int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, con
  * triangle_attention core (starting node) over the pre-pass outputs.  Replaces the attention
  * of `triangle_attn_kernel` (triangle_attn/kernel.py:197-253, launched at :335-373).
  *   mask   int8 (N, N) with strides (sm0, sm1), nonzero = valid key, or NULL
- *   out    io   O[i, q, h*D + d] at out[i*so0 + q*so1 + h*D + d]
+ *   out    io   O[i, q, h*D + d] at out[i*so0 + q*so1 + h*D + d], d < D (so0, so1 multiples of 4)
  * out[i,q,h] = softmax_k(scale * Q.K + bias[h,q,k] - 1e9 * (mask[i,k] == 0)) V; a row with no
- * valid key is the uniform average of V over all N keys (what the -1e9 add gives).  D == 32,
- * N <= 16384, ldn as in tops_tri_prep (any other value is rejected).
+ * valid key is the uniform average of V over all N keys (what the -1e9 add gives).  Qp and KV
+ * always hold 32-wide heads (tops_tri_prep / tops_tri_repack layouts); D in {8, 16, 24, 32} is
+ * the head width written (Q, K, V zero for d >= D), H <= 64, N <= 16384, ldn as in
+ * tops_tri_prep (any other value is rejected).
  */
 int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0, int64_t sm1,
                        void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H, int64_t D, int dtype,
@@ -118,7 +122,8 @@ int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const v
  *   Qp     io   (N, H, ldn, 32): scale * log2(e) * q, d permuted as in tops_tri_prep, zero for d >= D
  *   KV     io   (N, H, ldn/64, 4096): K and V^T as in tops_tri_prep, zero for d >= D or keys >= N
  *   btiles io   (H, ceil(N/32), ldn/32, 1024): log2(e) * bias in tops_tri_prep's tile order
- * tops_tri_attention then writes O with 32 columns per head, of which the first D are the result.
+ * tops_tri_attention then writes O with D columns per head (D in {8, 16, 24, 32}), or with 32 of
+ * which the first D are the result.
  * N <= 16384, ldn = max(64, round_up(N, 64)); bf16 / fp16.
  */
 int tops_tri_repack(const void* q, const void* k, const void* v, const float* bias, void* Qp, void* KV, void* btiles,
@@ -133,7 +138,7 @@ int tops_tri_repack(const void* q, const void* k, const void* v, const float* bi
  *               16-byte aligned base)
  *   gin    io   token (m1, m2) at gin[m1*sg0 + m2*sg1 + c], same constraints;  w_ln, b_ln io (C,)
  *   Wg, Wo io   (C, C) in (out, in) layout;  bg, bo io (C,) or NULL
- *   out    io   (M1*M2, C) contiguous.  C == 128.
+ *   out    io   (M1*M2, C) contiguous.  C (= C_in = H*D = C_out) in {128, 64}.
  */
 int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
                   const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg, const void* bg,

@@ -369,7 +369,8 @@ def test_tri_large_n_kernel(device, N, mask):
 @pytest.mark.parametrize("masked", [False, True])
 def test_tri_apo_d16(device, masked):
     """The Apo shape of the reference's tests/test_triangle_attn.py:137-192 (N=33, H=4, D=16, C_in=64)
-    runs the any-shape kernels; precompute keeps separate WK_c / WV_c for D = 16."""
+    runs the tuned kernels (C = 64 pre-pass and gate, heads zero-padded to 32 in the attention
+    kernel); precompute keeps separate WK_c / WV_c for D = 16."""
     inp = tri_inputs(33, C=64, H=4, D=16, seed=31, mask="random" if masked else "none", bias_z=True)
     d = to_dev(inp, device)
     pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
@@ -383,9 +384,10 @@ def test_tri_apo_d16(device, masked):
 
 @pytest.mark.parametrize("N,mask", [(256, "pad"), (520, "random")])
 def test_tri_apo_mfma_path_sampled_rows(device, N, mask):
-    """The Apo shape (C_in = 64, H = 4, D = 16) at larger N runs the MFMA attention kernel after
-    tops_tri_repack (D zero-padded to 32): starting and ending node on sampled rows, and the padded
-    path equals the any-shape scalar attention within the bf16 bar on the same pre-pass outputs."""
+    """The Apo shape (C_in = 64, H = 4, D = 16) at larger N on the tuned kernels: starting and ending
+    node on sampled rows; and, on the any-shape pre-pass's outputs, the MFMA attention kernel after
+    tops_tri_repack (D zero-padded to 32, heads of 16 written directly) equals the any-shape scalar
+    attention within the bf16 bar."""
     from triangleops_amd.triangle_attn.kernel import (generic_attention, generic_prep_forward, padded_attention,
                                                       padded_ok)
 
@@ -410,10 +412,51 @@ def test_tri_apo_mfma_path_sampled_rows(device, N, mask):
     _check(a[rows].cpu(), b[rows].float().cpu(), torch.bfloat16, f"tri Apo N={N} padded vs scalar attention")
 
 
+@pytest.mark.parametrize("N,C,D,mask", [(100, 64, 16, "pad"), (200, 64, 16, "random"), (130, 128, 16, "random"),
+                                        (96, 64, 32, "pad")])
+def test_tri_tuned_other_shapes(device, N, C, D, mask):
+    """The tuned pre-pass and attention at C_in in {64, 128} x D in {16, 32} beyond the default
+    (128, 32), whole grids vs the oracle, starting and ending node: the Apo shape (64, 16) also on
+    the tuned gate (C_in = H*D = C_out = 64); (128, 16) and (64, 32) on the any-shape gate."""
+    inp = tri_inputs(N, C=C, H=4, D=D, seed=N + C + D, mask=mask, bias_z=True)
+    _check(_tri_call(inp, device), _tri_ref(inp), torch.bfloat16, f"tri tuned N={N} C={C} D={D} start")
+    Xd = inp["X"].to(device)
+    out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
+    exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T)
+    _check(out_e, exp_e, torch.bfloat16, f"tri tuned N={N} C={C} D={D} end")
+
+
+@pytest.mark.parametrize("C", [64, 128])
+def test_gate_tuned_matches_generic(device, C):
+    """The tuned gate (C = 64 and 128) against the any-shape gate on the same inputs: with and without
+    the LayerNorm of its input, with the fused residual add into a transposed destination view."""
+    from triangleops_amd.triangle_attn.kernel import _gate_out_generic, gate_out_forward
+
+    g = torch.Generator().manual_seed(C)
+    N1, N2 = 37, 70
+    o = torch.randn(N1, N2, C, generator=g).to(torch.bfloat16).to(device)
+    x = torch.randn(N1, N2, C, generator=g).to(torch.bfloat16).to(device)
+    Wg = (torch.randn(C, C, generator=g) * C**-0.5).to(torch.bfloat16).to(device)
+    Wo = (torch.randn(C, C, generator=g) * C**-0.5).to(torch.bfloat16).to(device)
+    ln = ((1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(device),
+          (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(device), 1e-5)
+    for lnv in (None, ln):
+        a = gate_out_forward(o, x, Wg, None, Wo, None, ln=lnv)
+        b = _gate_out_generic(o, x, Wg, None, Wo, None, ln=lnv)
+        _check(a, b.float().cpu(), torch.bfloat16, f"gate C={C} ln={lnv is not None}")
+    res = torch.randn(N2, N1, C, generator=g).to(torch.bfloat16).to(device)
+    dst_a, dst_b = torch.zeros_like(res), torch.zeros_like(res)
+    gate_out_forward(o, x, Wg, None, Wo, None, ln=ln, residual=res.transpose(0, 1), out=dst_a.transpose(0, 1))
+    _gate_out_generic(o, x, Wg, None, Wo, None, ln=ln, residual=res.transpose(0, 1), out=dst_b.transpose(0, 1))
+    _check(dst_a, dst_b.float().cpu(), torch.bfloat16, f"gate C={C} residual")
+
+
 @pytest.mark.parametrize("N,C,H,D", [(40, 96, 3, 24), (70, 64, 2, 64), (130, 32, 8, 8), (257, 64, 4, 16)])
 @pytest.mark.parametrize("mask", ["pad", "random"])
 def test_tri_any_shape(device, N, C, H, D, mask):
-    """Shapes outside the tuned (C_in, H, D) = (128, 4, 32) run the any-shape kernels."""
+    """Shapes outside the tuned pre-pass run the any-shape pre-pass, then the MFMA attention kernel
+    (D <= 32; D = 24 and 8 written directly, heads zero-padded to 32) or the scalar one (D = 64);
+    (257, 64, 4, 16) is the Apo shape on the tuned kernels."""
     inp = tri_inputs(N, C=C, H=H, D=D, seed=N + C, mask=mask, bias_z=True)
     out = _tri_call(inp, device)
     _check(out, _tri_ref(inp), torch.bfloat16, f"tri any-shape N={N} C={C} H={H} D={D} mask={mask}")

@@ -221,6 +221,24 @@ def test_tri_abi_rejects_bad_ldn_and_n(N, ldn):
 
 
 @pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+def test_tri_abi_shape_limits():
+    """Shapes outside the tuned kernels return TOPS_EINVAL before any launch: the pre-pass takes
+    C in {128, 64}, H = 4, D in {32, 16}; the attention D in {8, 16, 24, 32}; the gate C in {128, 64}
+    (the pointers below are never dereferenced)."""
+    lib = _native.load()
+    f = ctypes.c_void_p(1 << 20)
+    for C, H, D in ((96, 4, 32), (128, 8, 32), (128, 4, 24), (64, 4, 8), (256, 4, 32)):
+        rc = lib.tops_tri_prep(f, 0, 0, None, None, 0, f, f, None, f, f, f, 64, 64, C, H, D, 1e-5, 1.0, 2, None)
+        assert rc == 1 and b"tops_tri_prep: supports" in lib.tops_last_error(), (C, H, D)
+    for D in (12, 40, 64):
+        rc = lib.tops_tri_attention(f, f, f, None, 0, 0, f, 0, 0, 64, 64, 4, D, 2, None)
+        assert rc == 1 and b"supports D in" in lib.tops_last_error(), D
+    for C in (96, 32, 256):
+        rc = lib.tops_gate_out(f, 0, 0, f, 0, 0, None, None, 1e-5, 0, f, None, f, None, f, 8, 8, C, 2, None)
+        assert rc == 1 and b"C must be 128 or 64" in lib.tops_last_error(), C
+
+
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
 def test_apb_abi_rejects_misaligned_z():
     """tops_apb_forward refuses Z token strides that are not multiples of 8 and misaligned bases (the
     kernel reads Z, X and the workspace with 16-byte loads)."""
@@ -233,14 +251,18 @@ def test_apb_abi_rejects_misaligned_z():
 
 
 def test_tri_dispatch_decision():
-    """The tuned kernels serve (C_in, H, D, C_out) = (128, 4, 32, 128) up to N = 16384; other shapes and
-    larger N go to the any-shape kernels."""
-    from triangleops_amd.triangle_attn.kernel import TUNED_MAX_N, fast_shape
+    """The tuned pre-pass and attention serve C_in in {128, 64}, H = 4, D in {32, 16} up to N = 16384
+    (the Apo shape C_in = 64, D = 16 included); other shapes and larger N go to the any-shape
+    pre-pass.  The tuned gate serves C_in = H*D = C_out in {128, 64}."""
+    from triangleops_amd.triangle_attn.kernel import TUNED_MAX_N, fast_shape, gate_fast_shape
 
     assert TUNED_MAX_N == 16384
-    assert fast_shape(128, 4, 32, 128, 1024) and fast_shape(128, 4, 32, 128, 16384)
-    assert not fast_shape(128, 4, 32, 128, 16385)
-    assert not fast_shape(64, 4, 16, 64, 128) and not fast_shape(128, 4, 32, 64, 128)
+    assert fast_shape(128, 4, 32, 1024) and fast_shape(128, 4, 32, 16384) and fast_shape(64, 4, 16, 128)
+    assert fast_shape(128, 4, 16, 128) and fast_shape(64, 4, 32, 128)
+    assert not fast_shape(128, 4, 32, 16385) and not fast_shape(96, 4, 32, 128)
+    assert not fast_shape(128, 8, 16, 128) and not fast_shape(128, 4, 8, 128)
+    assert gate_fast_shape(128, 128, 128) and gate_fast_shape(64, 64, 64)
+    assert not gate_fast_shape(128, 64, 128) and not gate_fast_shape(128, 128, 64)
 
 
 def test_vec16_copies_misaligned_views():

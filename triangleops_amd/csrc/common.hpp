@@ -111,6 +111,16 @@ __device__ inline void vmcnt_wait() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// LDS chunk swizzle of a token row of the pre-pass and gate tiles: 16 rows read together (one
+// per lane of a 16-lane group) hit 16 distinct 16-byte bank groups.  A 256-byte row (C = 128)
+// spans all 64 banks: chunk ^ (t & 15).  A 128-byte row (C = 64) spans half of them, the row
+// parity picks the half: chunk ^ ((t >> 1) & 7).
+template <int C>
+__device__ inline int row_key(int t) {
+  static_assert(C == 128 || C == 64, "row width");
+  return C == 128 ? (t & 15) : ((t >> 1) & 7);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)); saturates cleanly to 0 / 1.

@@ -1,5 +1,6 @@
 // Gate + output projection, shared by triangle_attention and attention_pair_bias:
-//   out[t] = ((o[t] * sigmoid(g_in[t] . Wg^T + bg)) -> io) . Wo^T + bo,   C = 128,
+//   out[t] = ((o[t] * sigmoid(g_in[t] . Wg^T + bg)) -> io) . Wo^T + bo,   C = C_in = H*D = C_out,
+// C = 128 or 64,
 // where g_in = LN(x) (triangle attention: the gate reads LN(x), recomputed here from x so the
 // normalized tensor is never written to HBM) or the raw input (attention_pair_bias).
 //
@@ -7,14 +8,15 @@
 // strides) and attn_pair_bias/module.py:69-70 (gate on raw X with biases, then Wo).
 // Both weights are read in their (out, in) nn.Linear layout: no per-call transposes.
 //
-// 64-token tiles, 8 waves.  Waves 0-3 fetch the o and gate-input tiles two tiles ahead (two
-// register stages; 16 lanes per 256-byte token row) and stage them in LDS, normalising the
-// gate input on the way; waves 4-7 write the results, so no wave has loads and stores in flight
-// together and each stage is waited for only when consumed.  All waves compute: wave w owns
-// features [32 (w & 3), +32) of both GEMMs for tokens [32 (w >> 2), +32), weight rows in
-// registers (permuted so each lane ends up with 16 consecutive features of one token).  The
-// gated activations overwrite the o tile in LDS and are the second GEMM's operand; the output
-// goes through a token-major LDS tile so each store instruction writes whole 256-byte rows.
+// Tiles of 8192 / C tokens (64 at C = 128, 128 at C = 64: 16 KB of each input), 8 waves.  Waves
+// 0-3 fetch the o and gate-input tiles two tiles ahead (two register stages; C / 8 lanes per
+// token row) and stage them in LDS, normalising the gate input on the way; waves 4-7 write the
+// results, so no wave has loads and stores in flight together and each stage is waited for only
+// when consumed.  All waves compute: wave w owns features [32 (w % (C / 32)), +32) of both GEMMs
+// for tokens [32 (w / (C / 32)), +32), weight rows in registers (permuted so each lane ends up
+// with 16 consecutive features of one token).  The gated activations overwrite the o tile in LDS
+// and are the second GEMM's operand; the output goes through a token-major LDS tile so each
+// store instruction writes whole token rows.
 #include "capi.hpp"
 #include "common.hpp"
 
@@ -22,7 +24,7 @@ namespace tops {
 
 // RES: out[m1, m2] = res[m1, m2] + result, both at their own token strides (the residual add of
 // a Pairformer block fused into the store; the sum is rounded once, as a separate add would be).
-template <typename T, bool LN, bool RES>
+template <typename T, bool LN, bool RES, int C>
 __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
                                                       const T* __restrict__ gin, int64_t sg0, int64_t sg1,
                                                       const T* __restrict__ w_ln, const T* __restrict__ b_ln,
@@ -31,22 +33,26 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
                                                       const T* __restrict__ bo, const T* __restrict__ res,
                                                       int64_t sr0, int64_t sr1, T* __restrict__ out, int64_t sd0,
                                                       int64_t sd1, FastDiv M2, uint32_t M, uint32_t ntiles) {
-  constexpr int C = 128, ROW = C * 2, KS = C / 16;
-  constexpr int NL = 256;  // loader threads (waves 0-3); writers are waves 4-7
-  constexpr int PD = 2;    // register stages in flight
+  static_assert(C == 128 || C == 64, "feature width");
+  constexpr int ROW = C * 2, KS = C / 16;
+  constexpr int TOK = 8192 / C;  // tokens per tile
+  constexpr int LPT = C / 8;     // loader lanes (16-byte chunks) per token row
+  constexpr int FS = C / 32;     // feature groups of 32: wave w = feature group w % FS, tokens w / FS
+  constexpr int NL = 256;        // loader threads (waves 0-3); writers are waves 4-7
+  constexpr int PD = 2;          // register stages in flight
   using V8 = vec<T, 8>;
   using V2 = vec<T, 2>;
 
   // one staging buffer suffices: the next tile is staged only after the third barrier, when
   // every wave has finished reading this one
-  __shared__ __attribute__((aligned(16))) char gs[64 * ROW];   // gate input (normalised)
-  __shared__ __attribute__((aligned(16))) char ots[64 * ROW];  // o, then the gated values
-  __shared__ __attribute__((aligned(16))) T os[64 * C];          // output tile, token-major
+  __shared__ __attribute__((aligned(16))) char gs[TOK * ROW];   // gate input (normalised)
+  __shared__ __attribute__((aligned(16))) char ots[TOK * ROW];  // o, then the gated values
+  __shared__ __attribute__((aligned(16))) T os[TOK * C];          // output tile, token-major
   __shared__ __attribute__((aligned(16))) float cst[2][C];       // -log2(e) bg, bo
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
-  const int fset = wave & 3, sub = wave >> 2;
+  const int fset = wave % FS, sub = wave / FS;
 
   for (int i = tid; i < C; i += 512) {
     cst[0][i] = bg ? -kLog2e * (float)bg[i] : 0.f;
@@ -66,7 +72,7 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
   }
   __syncthreads();  // cst
 
-  auto swz = [](int t, int chunk) { return (chunk ^ (t & 15)) << 4; };
+  auto swz = [](int t, int chunk) { return (chunk ^ row_key<C>(t)) << 4; };
   const int f0 = 32 * fset + 16 * hl;
   // GEMM 1, sigmoid gate, o * gate -> in place over the o tile (all waves)
   auto compute1 = [&]() {
@@ -105,7 +111,7 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[1][f0 + 8 * h + e]);
       const int c = f0 / 8 + h;
-      *reinterpret_cast<V8*>(&os[tok * C + ((c ^ (tok & 15)) << 3)]) = r;
+      *reinterpret_cast<V8*>(&os[tok * C + ((c ^ row_key<C>(tok)) << 3)]) = r;
     }
   };
 
@@ -113,7 +119,7 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
   uint32_t t = blockIdx.x;
   if (wave < 4) {
     // ================= loaders =================
-    const int ch = tid & 15;  // this thread's 16-byte chunk of every token row it loads
+    const int ch = tid % LPT;  // this thread's 16-byte chunk of every token row it loads
     V8 lnw = {}, lnb = {};
     if constexpr (LN) {
       lnw = ldg<V8>(w_ln + 8 * ch);
@@ -127,7 +133,7 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
       tt = tt < ntiles ? tt : ntiles - 1;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        uint32_t m = tt * 64 + ((k * NL + tid) >> 4);
+        uint32_t m = tt * TOK + (k * NL + tid) / LPT;
         m = m < M ? m : M - 1;
         const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
         sg.o[k] = ldg<V8>(o + m1 * so0 + m2 * so1 + 8 * ch);
@@ -137,9 +143,9 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
     auto step = [&](uint32_t tt, Stage& sg) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int tk = (k * NL + tid) >> 4;
+        const int tk = (k * NL + tid) / LPT;
         V8 g = sg.g[k];
-        if constexpr (LN) {  // LayerNorm over the token's 16 lanes (sum and sum of squares in fp32)
+        if constexpr (LN) {  // LayerNorm over the token's LPT lanes (sum and sum of squares in fp32)
           float s1 = 0.f, s2 = 0.f;
           const V2 one = {(T)1.f, (T)1.f};
 #pragma unroll
@@ -148,8 +154,8 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
             s1 = Mma<T>::dot2(pr, one, s1);
             s2 = Mma<T>::dot2(pr, pr, s2);
           }
-          const float mean = group_sum<16>(s1) * (1.0f / C);
-          const float var = fmaxf(group_sum<16>(s2) * (1.0f / C) - mean * mean, 0.f);
+          const float mean = group_sum<LPT>(s1) * (1.0f / C);
+          const float var = fmaxf(group_sum<LPT>(s2) * (1.0f / C) - mean * mean, 0.f);
           const float rstd = rsqrtf(var + ln_eps);
 #pragma unroll
           for (int e = 0; e < 8; ++e) g[e] = (T)(((float)g[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e]);
@@ -189,12 +195,12 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
       compute2();
       __syncthreads();  // output tile complete
 #pragma unroll
-      for (int k = 0; k < 64 * C / 8 / NL; ++k) {
-        const int ci = k * NL + wt;  // token ci / 16, chunk ci % 16
-        const int tk = ci >> 4, c = ci & 15;
-        const uint32_t m = t * 64 + tk;
+      for (int k = 0; k < TOK * C / 8 / NL; ++k) {
+        const int ci = k * NL + wt;  // token ci / LPT, chunk ci % LPT
+        const int tk = ci / LPT, c = ci % LPT;
+        const uint32_t m = t * TOK + tk;
         if (m >= M) continue;
-        V8 v = *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ (tk & 15)) << 3)]);
+        V8 v = *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ row_key<C>(tk)) << 3)]);
         if constexpr (RES) {
           const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
           const V8 r = ldg<V8>(res + m1 * sr0 + m2 * sr1 + 8 * c);
@@ -209,22 +215,28 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
   }
 }
 
-template <typename T>
+template <typename T, int C>
 static int gate_out_t(const void* o, int64_t so0, int64_t so1, const void* gin, int64_t sg0, int64_t sg1,
                       const void* w_ln, const void* b_ln, float ln_eps, int apply_ln, const void* Wg, const void* bg,
                       const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
                       int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, hipStream_t st) {
+  constexpr int64_t TOK = 8192 / C;
   const int64_t M = M1 * M2;
-  const int64_t ntiles = (M + 63) / 64;
+  const int64_t ntiles = (M + TOK - 1) / TOK;
   if (ntiles == 0) return TOPS_OK;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
-  auto kern = apply_ln ? (res ? gate_out_kernel<T, true, true> : gate_out_kernel<T, true, false>)
-                       : (res ? gate_out_kernel<T, false, true> : gate_out_kernel<T, false, false>);
+  auto kern = apply_ln ? (res ? gate_out_kernel<T, true, true, C> : gate_out_kernel<T, true, false, C>)
+                       : (res ? gate_out_kernel<T, false, true, C> : gate_out_kernel<T, false, false, C>);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), 0, st, (const T*)o, so0, so1, (const T*)gin, sg0, sg1,
                      (const T*)w_ln, (const T*)b_ln, ln_eps, (const T*)Wg, (const T*)bg, (const T*)Wo,
                      (const T*)bo, (const T*)res, sr0, sr1, (T*)out, sd0, sd1, FastDiv((uint32_t)M2), (uint32_t)M,
                      (uint32_t)ntiles);
   return launched(res ? "tops_gate_out_residual" : "tops_gate_out");
+}
+
+template <typename T, typename... A>
+static int gate_out_c(int64_t C, A... a) {
+  return C == 128 ? gate_out_t<T, 128>(a...) : gate_out_t<T, 64>(a...);
 }
 
 }  // namespace tops
@@ -237,7 +249,7 @@ extern "C" int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void
                              int64_t C, int dtype, void* stream) {
   TOPS_REQUIRE(o && gin && Wg && Wo && out, "tops_gate_out: null pointer argument");
   TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out: w_ln is required when apply_ln != 0");
-  TOPS_REQUIRE(C == 128, "tops_gate_out: C must be 128 (got %lld)", (long long)C);
+  TOPS_REQUIRE(C == 128 || C == 64, "tops_gate_out: C must be 128 or 64 (got %lld)", (long long)C);
   TOPS_REQUIRE(M1 >= 0 && M2 >= 0 && M1 * M2 < (1LL << 31), "tops_gate_out: bad sizes");
   TOPS_REQUIRE(so0 % 8 == 0 && so1 % 8 == 0 && sg0 % 8 == 0 && sg1 % 8 == 0,
                "tops_gate_out: token strides must be multiples of 8 elements");
@@ -245,10 +257,10 @@ extern "C" int tops_gate_out(const void* o, int64_t so0, int64_t so1, const void
                "tops_gate_out: o, gin and out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0, 0,
+    return gate_out_c<__bf16>(C, o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0, 0,
                               out, 0, 0, M1, M2, st);
   if (dtype == TOPS_DTYPE_F16)
-    return gate_out_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0,
+    return gate_out_c<_Float16>(C, o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, nullptr, 0,
                                 0, out, 0, 0, M1, M2, st);
   return fail(TOPS_EUNSUPPORTED, "tops_gate_out: unsupported dtype code %d", dtype);
 }
@@ -260,7 +272,7 @@ extern "C" int tops_gate_out_residual(const void* o, int64_t so0, int64_t so1, c
                                       int64_t M2, int64_t C, int dtype, void* stream) {
   TOPS_REQUIRE(o && gin && Wg && Wo && res && out, "tops_gate_out_residual: null pointer argument");
   TOPS_REQUIRE(!apply_ln || w_ln, "tops_gate_out_residual: w_ln is required when apply_ln != 0");
-  TOPS_REQUIRE(C == 128, "tops_gate_out_residual: C must be 128 (got %lld)", (long long)C);
+  TOPS_REQUIRE(C == 128 || C == 64, "tops_gate_out_residual: C must be 128 or 64 (got %lld)", (long long)C);
   TOPS_REQUIRE(M1 >= 0 && M2 >= 0 && M1 * M2 < (1LL << 31), "tops_gate_out_residual: bad sizes");
   TOPS_REQUIRE(so0 % 8 == 0 && so1 % 8 == 0 && sg0 % 8 == 0 && sg1 % 8 == 0 && sr0 % 8 == 0 && sr1 % 8 == 0 &&
                    sd0 % 8 == 0 && sd1 % 8 == 0,
@@ -270,10 +282,10 @@ extern "C" int tops_gate_out_residual(const void* o, int64_t so0, int64_t so1, c
                "tops_gate_out_residual: o, gin, res and out must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return gate_out_t<__bf16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0, sr1,
+    return gate_out_c<__bf16>(C, o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0, sr1,
                               out, sd0, sd1, M1, M2, st);
   if (dtype == TOPS_DTYPE_F16)
-    return gate_out_t<_Float16>(o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0,
+    return gate_out_c<_Float16>(C, o, so0, so1, gin, sg0, sg1, w_ln, b_ln, ln_eps, apply_ln, Wg, bg, Wo, bo, res, sr0,
                                 sr1, out, sd0, sd1, M1, M2, st);
   return fail(TOPS_EUNSUPPORTED, "tops_gate_out_residual: unsupported dtype code %d", dtype);
 }

@@ -42,7 +42,7 @@ static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 *
 
 // ---------------------------------------------------------------------------------------------
 // Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 8 waves in two roles:
-//   waves 0-3 (loaders) fetch x four tiles ahead (16 lanes per 256-byte token row; positions
+//   waves 0-3 (loaders) fetch x four tiles ahead (C / 8 lanes per 2C-byte token row; positions
 //   >= N reload position N - 1, so every fetch issues the same loads), take the LayerNorm and
 //   the 4 heads' pair bias in fp32, and stage the normalised tile in LDS (double-buffered);
 //   waves 4-7 (head w - 4) run that head's Q / K / V GEMM over the 64 positions with its WQ /
@@ -52,18 +52,24 @@ static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 *
 // when it is consumed, and the loaders' LayerNorm of tile n + 1 overlaps the writers' GEMM of
 // tile n: one barrier per tile.  Positions >= N are computed from zeros (finite values, masked
 // by the attention kernel).
+// C (the pair channel count) is 128 or 64.  The outputs always have the 32-wide head layout the
+// attention kernel reads; with a head width D < 32 the weight rows d >= D are zeros, so Q, K and
+// V are exact zeros there and add nothing to the scores or to O.
 // ---------------------------------------------------------------------------------------------
-template <typename T, bool LN>
+template <typename T, bool LN, int C>
 __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
                                                       const T* __restrict__ w_ln, const T* __restrict__ b_ln,
                                                       const T* __restrict__ wqkv, const T* __restrict__ WZ,
                                                       const float* __restrict__ BZ, T* __restrict__ Qp,
                                                       T* __restrict__ KV, T* __restrict__ bias, uint32_t N,
                                                       uint32_t ldn, float eps, float qscale, float bias_scale,
-                                                      uint32_t ntiles, FastDiv nkbd) {
-  constexpr int C = 128, D = 32, H = 4, ROW = C * 2, KS = C / 16;
-  constexpr int PD = 4;             // loader register stages in flight
-  constexpr int PART = 64 * D * 2;  // bytes of one head's Q, K or V^T block of a tile
+                                                      uint32_t ntiles, FastDiv nkbd, int dh) {
+  constexpr int D = 32, H = 4, ROW = C * 2, KS = C / 16;
+  constexpr int LPT = C / 8;       // loader lanes per token row (16 bytes each)
+  constexpr int TPP = 256 / LPT;   // tokens per loader pass
+  constexpr int NP = 64 / TPP;     // loader passes per tile
+  constexpr int PD = 4;            // loader register stages in flight
+  constexpr int PART = 64 * D * 2; // bytes of one head's Q, K or V^T block of a tile
   using V8 = vec<T, 8>;
 
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];    // normalised x tiles
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 
   if (wave < 4) {
     // ================= loaders =================
-    const int ch = tid & 15, tq = tid >> 4;  // 16-byte chunk ch of tokens 16 k + tq, k < 4
+    const int ch = tid % LPT, tq = tid / LPT;  // 16-byte chunk ch of tokens TPP k + tq, k < NP
     V8 lnw = {}, lnb = {}, wz[H];
     if constexpr (LN) {
       lnw = ldg<V8>(w_ln + 8 * ch);
@@ -87,15 +93,15 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
     for (int hh = 0; hh < H; ++hh) wz[hh] = ldg<V8>(WZ + hh * C + 8 * ch);
     const float bz = BZ ? BZ[ch & 3] : 0.f;
     struct Stage {
-      V8 x[4];
+      V8 x[NP];
     };
     auto fetch = [&](uint32_t tt, Stage& sg) {
       tt = tt < ntiles ? tt : ntiles - 1;
       const uint32_t i = nkbd.div(tt), kb = tt - i * nkb;
       const T* row = x + (int64_t)i * sx0 + 8 * ch;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        uint32_t p = kb * 64 + 16 * k + tq;
+      for (int k = 0; k < NP; ++k) {
+        uint32_t p = kb * 64 + TPP * k + tq;
         p = p < N ? p : N - 1;
         sg.x[k] = ldg<V8>(row + (int64_t)p * sx1);
       }
@@ -103,21 +109,21 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
     auto step = [&](uint32_t tt, int bb, Stage& sg) {
       const uint32_t kb = tt - nkbd.div(tt) * nkb;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int tk = 16 * k + tq;
+      for (int k = 0; k < NP; ++k) {
+        const int tk = TPP * k + tq;
         const bool valid = kb * 64 + tk < N;
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = valid ? (float)sg.x[k][e] : 0.f;
-        if constexpr (LN) {  // two-pass statistics over the token's 16 lanes
+        if constexpr (LN) {  // two-pass statistics over the token's LPT lanes
           float s = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) s += v[e];
-          const float mean = group_sum<16>(s) * (1.0f / C);
+          const float mean = group_sum<LPT>(s) * (1.0f / C);
           float q = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
-          const float rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+          const float rstd = rsqrtf(group_sum<LPT>(q) * (1.0f / C) + eps);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = (v[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e];
         }
@@ -129,14 +135,14 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
           float d = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) d = fmaf(v[e], (float)wz[hh][e], d);
-          d = group_sum<16>(d);
+          d = group_sum<LPT>(d);
           bsel = (ch & 3) == hh ? d : bsel;
         }
         bs[bb][(ch & 3) * 64 + tk] = valid ? (T)((bsel + bz) * bias_scale) : (T)0.f;
         V8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (T)v[e];
-        *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ (tk & 15)) << 4)]) = o;
+        *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ row_key<C>(tk)) << 4)]) = o;
       }
       __syncthreads();  // tile tt staged; the writers are done with the tile before tt - 1
       fetch(tt + PD * G, sg);  // refill this stage
@@ -168,14 +174,17 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
   } else {
     // ================= writers: wave 4 + h owns head h =================
     const int h = wave - 4, hl = lane >> 5, col = lane & 31;
+    // weight rows (H, 3, dh, C): row col < dh of head h's Q, K and V blocks; rows col >= dh
+    // (a head narrower than 32) are zeros and are not read
     V8 wq[KS], wk[KS], wv[KS];
     {
-      const T* wh = wqkv + (int64_t)h * 3 * D * C + (int64_t)col * C + 8 * hl;
+      const bool live = col < dh;
+      const T* wh = wqkv + ((int64_t)h * 3 * dh + (live ? col : 0)) * C + 8 * hl;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        wq[s] = ldg<V8>(wh + 16 * s);
-        wk[s] = ldg<V8>(wh + D * C + 16 * s);
-        wv[s] = ldg<V8>(wh + 2 * D * C + 16 * s);
+        wq[s] = live ? ldg<V8>(wh + 16 * s) : V8{};
+        wk[s] = live ? ldg<V8>(wh + (int64_t)dh * C + 16 * s) : V8{};
+        wv[s] = live ? ldg<V8>(wh + 2 * (int64_t)dh * C + 16 * s) : V8{};
       }
     }
     char* oh = os[h];
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
         f32x16 aq = {}, ak = {}, av = {};
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-          const V8 xb = *reinterpret_cast<const V8*>(&xs[bb][tp * ROW + (((2 * s + hl) ^ (tp & 15)) << 4)]);
+          const V8 xb = *reinterpret_cast<const V8*>(&xs[bb][tp * ROW + (((2 * s + hl) ^ row_key<C>(tp)) << 4)]);
           aq = Mma<T>::m32(wq[s], xb, aq);
           ak = Mma<T>::m32(wk[s], xb, ak);
           av = Mma<T>::m32(xb, wv[s], av);
@@ -283,7 +292,8 @@ template <typename T, int QT>
 __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
                                                          int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
-                                                         int64_t so1, int64_t N, int64_t ldn, int H, int nqc) {
+                                                         int64_t so1, int64_t N, int64_t ldn, int H, int nqc,
+                                                         int dv) {
   constexpr int D = 32, NW = 4;
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
@@ -525,15 +535,17 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     if (j + 1 < nv) block(j + 1, kvB, kvA);
   }
 
-  // ---- normalise and store O[i, q, h*D + d] ----
+  // ---- normalise and store O[i, q, h*dv + d], d < dv: the head's first dv of its 32 lanes
+  // ---- (dv < 32 when the head is narrower and its Q / K / V are zero-padded to 32) ----
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int64_t q = qbase + 32 * t + col;
     const float inv = 1.0f / halves_sum(l[t]);
     if (q < N) {
-      T* dst = out + i * so0 + q * so1 + (int64_t)h * D + 4 * hl;
+      T* dst = out + i * so0 + q * so1 + (int64_t)h * dv + 4 * hl;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
+        if (8 * g >= dv) break;  // wave-uniform: slots 4 g .. 4 g + 3 hold d = 8 g + 4 hl + 0..3
         V4 w4 = {(T)(o[t][4 * g] * inv), (T)(o[t][4 * g + 1] * inv), (T)(o[t][4 * g + 2] * inv),
                  (T)(o[t][4 * g + 3] * inv)};
         stg<V4>(dst + 8 * g, w4);
@@ -976,23 +988,24 @@ static int tri_repack_t(const void* q, const void* k, const void* v, const float
 template <typename T>
 static int tri_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln, int apply_ln,
                       const void* wqkv, const void* WZ, const float* BZ, void* Qp, void* KV, void* bias, int64_t N,
-                      int64_t ldn, float eps, float qscale, hipStream_t st) {
+                      int64_t ldn, int64_t C, int64_t D, float eps, float qscale, hipStream_t st) {
   const int64_t ntiles = N * (ldn / 64);
   if (ntiles == 0) return TOPS_OK;
   const int64_t grid = ntiles < (int64_t)num_cus() ? ntiles : (int64_t)num_cus();
-  auto kern = apply_ln ? tri_prep_kernel<T, true> : tri_prep_kernel<T, false>;
+  auto kern = C == 128 ? (apply_ln ? tri_prep_kernel<T, true, 128> : tri_prep_kernel<T, false, 128>)
+                       : (apply_ln ? tri_prep_kernel<T, true, 64> : tri_prep_kernel<T, false, 64>);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), 0, st, (const T*)x, sx0, sx1, (const T*)w_ln,
                      (const T*)b_ln, (const T*)wqkv, (const T*)WZ, BZ, (T*)Qp, (T*)KV, (T*)bias, (uint32_t)N,
-                     (uint32_t)ldn, eps, qscale, kLog2e, (uint32_t)ntiles, FastDiv((uint32_t)(ldn / 64)));
+                     (uint32_t)ldn, eps, qscale, kLog2e, (uint32_t)ntiles, FastDiv((uint32_t)(ldn / 64)), (int)D);
   return launched("tops_tri_prep");
 }
 
 template <typename T>
 static int tri_attention_t(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
                            int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
-                           hipStream_t st) {
+                           int64_t dv, hipStream_t st) {
 #ifdef TOPS_TRI_TWO_ROW  // off: not yet run on the GPU since its wait-state fix
-  {
+  if (dv == 32) {
     const int nqc = (int)((N + 127) / 128), nrp = (int)((N + 1) / 2);
     const int64_t grid = (int64_t)H * nrp * nqc;
     if (grid == 0) return TOPS_OK;
@@ -1010,7 +1023,7 @@ static int tri_attention_t(const void* Qp, const void* KV, const void* bias, con
 #define TOPS_TRI(QTV)                                                                                     \
   hipLaunchKernelGGL((tri_attn_kernel<T, QTV>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Qp,      \
                      (const T*)KV, (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, ldn, \
-                     (int)H, nqc)
+                     (int)H, nqc, (int)dv)
   if (qt == 1)
     TOPS_TRI(1);
   else
@@ -1029,8 +1042,8 @@ extern "C" int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void
                              float scale, int dtype, void* stream) {
   TOPS_REQUIRE(x && wqkv && WZ && Qp && KV && bias, "tops_tri_prep: null pointer argument");
   TOPS_REQUIRE(!apply_ln || w_ln, "tops_tri_prep: w_ln is required when apply_ln != 0");
-  TOPS_REQUIRE(C == 128 && H == 4 && D == 32,
-               "tops_tri_prep: supports C == 128, H == 4, D == 32 (got %lld, %lld, %lld)", (long long)C,
+  TOPS_REQUIRE((C == 128 || C == 64) && H == 4 && (D == 32 || D == 16),
+               "tops_tri_prep: supports C in {128, 64}, H == 4, D in {32, 16} (got %lld, %lld, %lld)", (long long)C,
                (long long)H, (long long)D);
   TOPS_REQUIRE(N >= 0 && N <= kMaxN, "tops_tri_prep: supports N <= %d (got %lld)", kMaxN, (long long)N);
   TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_prep: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
@@ -1040,10 +1053,11 @@ extern "C" int tops_tri_prep(const void* x, int64_t sx0, int64_t sx1, const void
   hipStream_t st = (hipStream_t)stream;
   const float qscale = scale * kLog2e;
   if (dtype == TOPS_DTYPE_BF16)
-    return tri_prep_t<__bf16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, eps, qscale, st);
+    return tri_prep_t<__bf16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, C, D, eps, qscale,
+                              st);
   if (dtype == TOPS_DTYPE_F16)
-    return tri_prep_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, eps, qscale,
-                                st);
+    return tri_prep_t<_Float16>(x, sx0, sx1, w_ln, b_ln, apply_ln, wqkv, WZ, BZ, Qp, KV, bias, N, ldn, C, D, eps,
+                                qscale, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_prep: unsupported dtype code %d", dtype);
 }
 
@@ -1051,7 +1065,8 @@ extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bi
                                   int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
                                   int64_t D, int dtype, void* stream) {
   TOPS_REQUIRE(Qp && KV && bias && out, "tops_tri_attention: null pointer argument");
-  TOPS_REQUIRE(D == 32 && H >= 1 && H <= 64, "tops_tri_attention: supports D == 32 (got D=%lld H=%lld)", (long long)D,
+  TOPS_REQUIRE((D == 32 || D == 24 || D == 16 || D == 8) && H >= 1 && H <= 64,
+               "tops_tri_attention: supports D in {8, 16, 24, 32} and H <= 64 (got D=%lld H=%lld)", (long long)D,
                (long long)H);
   TOPS_REQUIRE(N >= 0 && N <= kMaxN, "tops_tri_attention: supports N <= %d (got %lld)", kMaxN, (long long)N);
   TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_attention: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
@@ -1059,9 +1074,9 @@ extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bi
   TOPS_REQUIRE(so0 % 4 == 0 && so1 % 4 == 0, "tops_tri_attention: out strides must be multiples of 4");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return tri_attention_t<__bf16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, st);
+    return tri_attention_t<__bf16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, D, st);
   if (dtype == TOPS_DTYPE_F16)
-    return tri_attention_t<_Float16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, st);
+    return tri_attention_t<_Float16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, D, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_attention: unsupported dtype code %d", dtype);
 }
 

@@ -50,7 +50,8 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
     _native.check_device(X, wqkv, WZ_c, W_ln)
     X = _native.vec16(X)
     ldn = row_stride(N)
-    Qp = torch.empty(N, H, ldn, D, device=X.device, dtype=X.dtype)
+    # the attention kernel's 32-wide head layout; a head with D = 16 is zero-padded to 32
+    Qp = torch.empty(N, H, ldn, 32, device=X.device, dtype=X.dtype)
     KV = torch.empty(N, H, ldn // 64, 4096, device=X.device, dtype=X.dtype)
     bias = torch.empty(H, (N + 31) // 32, ldn // 32, 1024, device=X.device, dtype=X.dtype)
     BZf = None if BZ is None else BZ.float().contiguous()
@@ -87,11 +88,17 @@ LOG2E = 1.4426950408889634
 TUNED_MAX_N = 16384  # largest N of tops_tri_prep / tops_tri_attention (per-row key-block tables in LDS)
 
 
-def fast_shape(C, H, D, C_out=None, N=None):
-    """True when the tuned kernels apply: C_in = 128, H = 4, D = 32 (and C_out = 128) and N within
-    the tuned kernels' limit; every other call runs the any-shape kernels."""
-    return (C == 128 and H == 4 and D == 32 and (C_out is None or C_out == 128)
-            and (N is None or N <= TUNED_MAX_N))
+def fast_shape(C, H, D, N=None):
+    """True when the tuned pre-pass and attention kernels apply: C_in in (128, 64), H = 4, D in (32,
+    16) (the Apo shape C_in = 64, D = 16 included: heads zero-padded to 32 lanes) and N within the
+    tuned kernels' limit.  Other shapes run the any-shape pre-pass (then the MFMA attention kernel
+    when `padded_ok`).  The gate picks its own kernel (`gate_fast_shape`)."""
+    return C in (128, 64) and H == 4 and D in (32, 16) and (N is None or N <= TUNED_MAX_N)
+
+
+def gate_fast_shape(C_in, HD, C_out):
+    """True when the tuned gate kernel applies: C_in = H*D = C_out in (128, 64)."""
+    return C_in == HD == C_out and HD in (128, 64)
 
 
 def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=True):
@@ -157,7 +164,7 @@ def padded_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
     _native.call("tops_tri_repack", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.float().contiguous().data_ptr(),
                  Qp.data_ptr(), KV.data_ptr(), bt.data_ptr(), N, ldn, H, D, float(scale), io_dtype_code(dt),
                  _native.stream_of(q))
-    if D == 32:
+    if D % 8 == 0:  # the kernel writes heads of D in {8, 16, 24, 32} directly
         return attention_core(Qp, KV, bt, out, N=N, ldn=ldn, mask=mask)
     opad = torch.empty(N, N, H * 32, device=dev, dtype=dt)
     attention_core(Qp, KV, bt, opad, N=N, ldn=ldn, mask=mask)
@@ -205,8 +212,11 @@ def untile_bias(bias, N):
 
 
 def attention_core(Qp, KV, bias, out, *, N, ldn, mask=None):
-    """O[i, q, h*D:(h+1)*D] = softmax_k(scale Q.K + bias - 1e9 [mask[i,k] == 0]) V, written into `out`."""
-    _, H, _, D = Qp.shape
+    """O[i, q, h*D:(h+1)*D] = softmax_k(scale Q.K + bias - 1e9 [mask[i,k] == 0]) V, written into `out`
+    (N, N, H*D); Qp / KV hold 32-wide heads, of which the first D = out.shape[2] / H are written."""
+    _, H, _, D32 = Qp.shape
+    assert D32 == 32, "Qp must have the kernel's 32-wide head layout"
+    D = out.shape[2] // H
     _native.check_device(Qp, KV, bias, out, mask)
     assert out.shape == (N, N, H * D) and out.stride(2) == 1, "out must be (N, N, H*D) with unit last stride"
     m8 = None
@@ -301,7 +311,7 @@ def gate_out_forward(o, gin, W_g, b_g, W_o, b_o, *, ln=None, residual=None, out=
     _native.check_device(o, gin, W_g, W_o)
     Cin = gin.shape[-1]
     assert out is None or residual is not None, "out= is supported together with residual="
-    if not (C == 128 and Cin == 128 and W_o.shape[0] == 128) or o.dtype == torch.float32:
+    if not gate_fast_shape(Cin, C, W_o.shape[0]) or o.dtype == torch.float32:
         return _gate_out_generic(o, gin, W_g, b_g, W_o, b_o, ln=ln, residual=residual, out=out)
     o = _native.vec16(o)
     gin = _native.vec16(gin.reshape(N1, N2, C) if gin.dim() != 3 else gin)

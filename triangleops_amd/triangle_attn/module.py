@@ -60,8 +60,8 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
     if wqkv.dtype != X.dtype:
         wqkv = wqkv.to(X.dtype)
     H, _, D, C = wqkv.shape
-    if not fast_shape(C, H, D, W_proj_o.shape[0], N) or X.dtype == torch.float32:
-        # any-shape kernels: other shapes (e.g. D = 16, C_in = 64), N above the tuned limit, fp32 I/O
+    if not fast_shape(C, H, D, N) or X.dtype == torch.float32:
+        # any-shape pre-pass: other shapes, N above the tuned limit, fp32 I/O
         xln, q, k, v, bias = generic_prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], eps=eps)
         O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
         if padded_ok(N, H, D, X.dtype):  # D <= 32 in 16-bit I/O: the MFMA attention kernel, D padded
@@ -72,7 +72,8 @@ def forward(X, pre, *, mask=None, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_pro
     Qp, KV, bias, ldn = prep_forward(X, pre["W_ln"], pre["B_ln"], wqkv, pre["WZ_c"], pre["BZ"], scale=scale, eps=eps)
     O = torch.empty(N, N, H * D, device=X.device, dtype=X.dtype)
     attention_core(Qp, KV, bias, O, N=N, ldn=ldn, mask=mask)
-    # the gate reads LN(X); it is recomputed from X inside the gate kernel
+    # the gate reads LN(X); it is recomputed from X inside the gate kernel (the tuned one when
+    # C_in = H*D = C_out, e.g. 128 / 128 / 128 or the Apo shape's 64 / 64 / 64)
     return gate_out_forward(O, X, W_proj_g, None, W_proj_o, None, ln=(pre["W_ln"], pre["B_ln"], eps),
                             residual=residual, out=out)
 
