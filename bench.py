@@ -785,9 +785,17 @@ def traffic_run(L):
 
 def op_run(op, n):
     """Workload of the counter runs (no timing): 5 calls of one op at size n after 2 warmup calls
-    (`tri`: starting-node triangle attention; `apb`: attention_pair_bias; `tmu`: outgoing tmu)."""
+    (`tri`: starting-node triangle attention; `tri_apo`: the same at the Apo shape C_in = 64, H = 4,
+    D = 16; `apb`: attention_pair_bias; `tmu`: outgoing tmu)."""
     dev = torch.device("cuda:0")
-    if op == "tri":
+    if op == "tri_apo":
+        d = to_dev(tri_inputs_shape(n, 64, 4, 16), dev)
+        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                            d["B_proj_z"], 4, 16)
+        fn = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=16**-0.5,  # noqa: E731
+                                                W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
+                                                B_proj_o=None)
+    elif op == "tri":
         d = to_dev(tri_inputs(n), dev)
         pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
                                             d["B_proj_z"], H, D)
@@ -825,7 +833,7 @@ def main():
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-path reference timing")
     ap.add_argument("--no-ops", action="store_true", help="skip the triangle_attention / attention_pair_bias entries")
     ap.add_argument("--ops-size", type=int, default=1024, help="N = M of the triangle_attention / apb entries")
-    ap.add_argument("--op-run", choices=("tri", "apb", "tmu"), default=None,
+    ap.add_argument("--op-run", choices=("tri", "tri_apo", "apb", "tmu"), default=None,
                     help="only run 7 calls of one op at --size (workload of rocprofv3 counter runs)")
     ap.add_argument("--traffic-run", action="store_true",
                     help="only run the workload of the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
