@@ -196,8 +196,10 @@ int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): the same computation and arguments as tops_apb_forward minus `work`; the workspace is
  * a library-owned static device array of 16 MiB per GPU (held until the process ends), so calls
- * with tops_apb_workspace_bytes(M, H, D) > 16 MiB return TOPS_EINVAL (M up to 16384 on a 256-CU
- * MI355X).  The entry point allocates nothing and calls no allocating routine; the array's device
+ * with tops_apb_workspace_bytes(M, H, D) > 16 MiB return TOPS_EINVAL (on a 256-CU MI355X every M up
+ * to 6990 fits, and M in 8161..9039 or 16353..21845, where the keys are split into fewer parts;
+ * other M up to 16352 need the split partials of tops_apb_forward's workspace).  The entry point
+ * allocates nothing and calls no allocating routine; the array's device
  * address is looked up once per device on the first call made with that device current.  Every
  * call on one GPU shares that GPU's array: calls that overlap in time on one GPU (other streams,
  * other threads) race; calls ordered on one stream do not.  Nothing in the array needs to start

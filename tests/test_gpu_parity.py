@@ -568,6 +568,34 @@ def test_apb_precompute_forward_matches_oneshot(device):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("M,mask", [(40, "pad"), (200, "random"), (1024, "pad"), (2048, "random")])
+def test_apb_forward_matches_forward_qkv_bitwise(device, M, mask):
+    """tops_apb_forward (its own Q / K / V pre-pass) and tops_apb_forward_qkv on the Q / K / V of that
+    pre-pass (tops_apb_qkn_prep at the tuned shape) give the same bits, split-key merge included
+    (M = 40 .. 2048: 1 to 16 key splits), and consecutive calls repeat them."""
+    from triangleops_amd.attn_pair_bias.kernel import apb_forward, apb_forward_qkv, apb_qkn_prep
+
+    inp = apb_inputs(M, seed=M + 3, mask=mask, biases=True)
+    d = to_dev(inp, device)
+    H, D = 4, 32
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], H, D)
+    scale = D**-0.5
+    og_fused = torch.empty(M, H * D, device=device, dtype=torch.bfloat16)
+    apb_forward(d["X"], pre["W_QKV"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], og_fused,
+                scale=scale, mask=d["mask"], wqkv_hm=pre["wqkv_hm"])
+    q, k, v = apb_qkn_prep(d["X"], pre["wqkv_hm"], None, None, qscale=scale)
+    og_comb = torch.empty_like(og_fused)
+    apb_forward_qkv(q, k, v, d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], og_comb, scale=1.0,
+                    mask=d["mask"])
+    assert torch.equal(og_fused, og_comb), f"M={M}: tops_apb_forward differs from tops_apb_forward_qkv"
+    for _ in range(2):
+        again = torch.empty_like(og_fused)
+        apb_forward(d["X"], pre["W_QKV"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], again,
+                    scale=scale, mask=d["mask"], wqkv_hm=pre["wqkv_hm"])
+        assert torch.equal(again, og_fused), f"M={M}: repeated call differs"
+
+
 def _apb_perturbed(inp, kmask, seed):
     """inputs with X rows and Z key columns replaced at the masked keys"""
     g = torch.Generator().manual_seed(seed)

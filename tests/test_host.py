@@ -250,6 +250,18 @@ def test_apb_abi_rejects_misaligned_z():
         assert rc == 1 and b"16-byte" in lib.tops_last_error(), (sz0, sz1, z)
 
 
+@pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
+def test_apb_noalloc_size_ranges_cpu():
+    """The M that fit tops_apb_forward_noalloc's 16 MiB workspace on a 256-CU part (the count the
+    library assumes without a GPU): every M up to 6990, and 8161..9039, 16353..21845, where the keys
+    are split into fewer parts; the bounds the header states."""
+    lib = _native.load()
+    lim = 16 << 20
+    for M, fits in ((6990, True), (6991, False), (8160, False), (8161, True), (9039, True), (9040, False),
+                    (16352, False), (16353, True), (21845, True), (21846, False)):
+        assert (lib.tops_apb_workspace_bytes(M, 4, 32) <= lim) == fits, M
+
+
 def test_tri_dispatch_decision():
     """The tuned pre-pass and attention serve C_in in {128, 64}, H = 4, D in {32, 16} up to N = 16384
     (the Apo shape C_in = 64, D = 16 included); other shapes and larger N go to the any-shape

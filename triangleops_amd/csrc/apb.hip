@@ -282,16 +282,21 @@ __global__ __launch_bounds__(256) void apb_combine_kernel(const float* __restric
   const int64_t q = idx / (H * D);
   const int hd = (int)(idx % (H * D));
   const int h = hd / D;
-  const float* ml = ws + (int64_t)nsplit * M * (H * D);
+  const float* ml = ws + (int64_t)nsplit * M * (H * D) + (q * H + h) * 2;  // split s: + s * M * H * 2
+  const float* op = ws + q * (H * D) + hd;                                  // split s: + s * M * H * D
+  const int64_t sml = M * H * 2, so = M * (H * D);
+  // the loops are unrolled so that several splits' loads are in flight together (a thread's loads
+  // are otherwise one dependent round trip per split); same arithmetic and order as a plain loop
   float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml[(((int64_t)s * M + q) * H + h) * 2]);
+#pragma unroll 8
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml[s * sml]);
   const float mu = mx == -INFINITY ? 0.f : mx;
   float lt = 0.f, ot = 0.f;
+#pragma unroll 8
   for (int s = 0; s < nsplit; ++s) {
-    const float ms = ml[(((int64_t)s * M + q) * H + h) * 2];
-    const float w = fast_exp2((ms - mu) * kLog2e);
-    lt += w * ml[(((int64_t)s * M + q) * H + h) * 2 + 1];
-    ot += w * ws[((int64_t)s * M + q) * (H * D) + hd];
+    const float w = fast_exp2((ml[s * sml] - mu) * kLog2e);
+    lt += w * ml[s * sml + 1];
+    ot += w * op[s * so];
   }
   Og[q * (H * D) + hd] = (T)(ot / lt);
 }
