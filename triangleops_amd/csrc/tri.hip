@@ -318,37 +318,12 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
   const int hl = lane >> 5, col = lane & 31;
   const int nkb = (int)(ldn / 64);
 
-  // ---- key validity per 64-key block; compact list of blocks to visit ----
-  if (tid == 0) row_any = 0;
-  __syncthreads();
-  for (int kb = wave; kb < nkb; kb += NW) {
-    const int64_t k = (int64_t)kb * 64 + lane;
-    bool ok = k < N;
-    if (ok && mask) ok = mask[i * sm0 + k * sm1] != 0;
-    const unsigned long long bits = __ballot(ok);
-    if (lane == 0) {
-      kvalid[kb] = bits;
-      if (bits) row_any = 1;
-    }
-  }
-  __syncthreads();
-  const bool uniform = row_any == 0;  // no valid key: every score is -1e9, weights 1/N
-  if (tid == 0) {
-    int n = 0;
-    for (int kb = 0; kb < nkb; ++kb) {
-      if (uniform) kvalid[kb] = (N - 64LL * kb >= 64) ? ~0ull : ((1ull << (N - 64LL * kb)) - 1ull);
-      if (kvalid[kb]) vblk[n++] = (short)kb;
-    }
-    nvblk = n;
-  }
-  __syncthreads();
-  const int nv = nvblk;  // >= 1 whenever N >= 1
-
   const T* kvrow = KV + ((int64_t)i * H + h) * nkb * kKVBlock;
   const int64_t nqt = (N + 31) / 32;
 
-  // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) and bias pointers.
-  // ---- A row without valid keys zeroes Q and the identity, so its scores are all C0. ----
+  // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) and bias pointers, loaded
+  // ---- before the key-validity pass so the loads overlap it (a row without valid keys zeroes
+  // ---- Q and the identity below, so its scores are all C0) ----
   const int64_t qbase = (int64_t)qc * (NW * 32 * QT) + (int64_t)wave * 32 * QT;
   V8 qop[QT][2];
   const T* bq[QT];
@@ -357,16 +332,10 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     int64_t q = qbase + 32 * t + col;
     q = q < N ? q : N - 1;
     const T* qr = Qp + (((int64_t)i * H + h) * ldn + q) * D + 8 * hl;
-    qop[t][0] = uniform ? V8{} : ldg<V8>(qr);
-    qop[t][1] = uniform ? V8{} : ldg<V8>(qr + 16);
+    qop[t][0] = ldg<V8>(qr);
+    qop[t][1] = ldg<V8>(qr + 16);
     bq[t] = bias + ((int64_t)h * nqt + q / 32) * (2 * nkb) * 1024 + (32 * hl + q % 32) * 8;
   }
-  // identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j
-  V8 ident[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((!uniform && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
 
   // KV block copy: thread t moves 16-byte chunks t (K: row t / 4) and 256 + t (V^T: row t / 8);
   // each load instruction of a wave reads 1 KB contiguous.
@@ -386,6 +355,62 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
 #pragma unroll
       for (int j = 0; j < 2; ++j) bb[t][j] = ldg<V8>(bq[t] + (int64_t)(2 * kb + kt) * 1024 + 512 * j);
   };
+  // The first visited block is block 0 unless all its keys are masked: its KV and bias operands
+  // are loaded now, speculatively, and reloaded below in the rare other case.
+  V8 bA[QT][2], bB[QT][2];
+  V8 kvA[2], kvB[2];
+  kv_load(0, kvA);
+  load_bias(0, 0, bA);
+  load_bias(0, 1, bB);
+
+  // ---- key validity per 64-key block ----
+  for (int kb = wave; kb < nkb; kb += NW) {
+    const int64_t k = (int64_t)kb * 64 + lane;
+    bool ok = k < N;
+    if (ok && mask) ok = mask[i * sm0 + k * sm1] != 0;
+    const unsigned long long bits = __ballot(ok);
+    if (lane == 0) kvalid[kb] = bits;
+  }
+  __syncthreads();
+  // ---- wave 0: the list of blocks to visit, compacted 64 blocks per step (ballot + prefix
+  // ---- count); a row without valid keys visits every block with keys < N ----
+  if (wave == 0) {
+    unsigned long long seen = 0;
+    for (int g = 0; g < nkb; g += 64) seen |= __ballot(g + lane < nkb && kvalid[g + lane] != 0);
+    const bool unif = seen == 0;
+    int n = 0;
+    for (int g = 0; g < nkb; g += 64) {
+      const int kb = g + lane;
+      bool vis = false;
+      if (kb < nkb) {
+        if (unif) kvalid[kb] = (N - 64LL * kb >= 64) ? ~0ull : ((1ull << (N - 64LL * kb)) - 1ull);
+        vis = kvalid[kb] != 0;
+      }
+      const unsigned long long bal = __ballot(vis);
+      const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+      if (vis) vblk[n + pos] = (short)kb;
+      n += __popcll(bal);
+    }
+    if (lane == 0) {
+      nvblk = n;
+      row_any = unif ? 0 : 1;
+    }
+  }
+  __syncthreads();
+  const bool uniform = row_any == 0;  // no valid key: every score is -1e9, weights 1/N
+  const int nv = nvblk;               // >= 1 whenever N >= 1
+  if (uniform) {
+#pragma unroll
+    for (int t = 0; t < QT; ++t) qop[t][0] = qop[t][1] = V8{};
+  }
+
+  // identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j
+  V8 ident[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((!uniform && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
+
   f32x16 o[QT], cinit[QT];
   float l[QT];
 #pragma unroll
@@ -502,12 +527,12 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
   // previous barrier) and are loaded into registers two blocks ahead.  One barrier per block.
   // Past the last block the pipeline recomputes a tile of the last block (results unused).
   f32x16 sA[QT], sB[QT];
-  V8 bA[QT][2], bB[QT][2];
-  V8 kvA[2], kvB[2];
   auto blk = [&](int j) { return (int)vblk[j < nv ? j : nv - 1]; };
-  kv_load(blk(0), kvA);
-  load_bias(blk(0), 0, bA);
-  load_bias(blk(0), 1, bB);
+  if (blk(0) != 0) {  // block-uniform: block 0 has no valid key
+    kv_load(blk(0), kvA);
+    load_bias(blk(0), 0, bA);
+    load_bias(blk(0), 1, bB);
+  }
   if (nv > 1) kv_load(blk(1), kvB);
   kv_store(0, kvA);
   __syncthreads();
