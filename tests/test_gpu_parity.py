@@ -65,11 +65,12 @@ def test_tmu_fp16(device, dtype, direction):
     _check(out, expect, dtype, f"tmu fp16 {direction}")
 
 
-@pytest.mark.parametrize("C", [32, 64, 96, 192])
+@pytest.mark.parametrize("C", [32, 64, 96, 192, 320])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_tmu_any_channels(device, C, direction):
-    """C != 128 runs the any-shape input / output phases; the einsum kernels take any channel count."""
-    x, m, w = tmu_inputs(70, C=C, seed=C, mask="random")
+    """C != 128 runs the any-shape input / output phases (tiled up to C = 256, per-token above);
+    the einsum kernels take any channel count."""
+    x, m, w = tmu_inputs(70 if C <= 256 else 24, C=C, seed=C, mask="random")
     out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
                                               **to_dev(w, device))
     expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
@@ -86,6 +87,16 @@ def test_tmu_fp32_io(device, C, L, direction):
     assert out.dtype == torch.float32
     expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
     _check(out, expect, torch.float32, f"tmu fp32 C={C} L={L} {direction}")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_fp32_batch(device, direction):
+    """fp32 I/O with B = 2 and a ragged L: the tiled any-shape phases index batch rows and tail tiles."""
+    x, m, w = tmu_inputs(33, B=2, C=96, seed=5, mask="random", dtype=torch.float32)
+    out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device))
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.float32, f"tmu fp32 B=2 {direction}")
 
 
 def test_tmu_batch(device):
@@ -208,6 +219,24 @@ def test_tmu_einsum_large_kernels(device, L, nslab, dtype):
     bound = half_ulp * expect[:, :, :L].abs() + 1e-5 * expect.abs().max()
     assert bool((err <= bound).all()), f"L={L} nslab={nslab}: max excess {float((err - bound).max()):.3e}"
     assert bool(torch.isfinite(y[..., L:].float()).all()), "padding columns must be finite"
+
+
+@pytest.mark.parametrize("L,nslab", [(40, 3), (128, 2), (130, 4), (300, 5), (1024, 2)])
+def test_tmu_einsum_fp32(device, L, nslab):
+    """The fp32 product (fp32 MFMA, fp32 sums) against a float64 product of the same operands:
+    rows past L in the last 128-row tile (L = 40, 130, 300), an exact tile (L = 128) and L = 1024.
+    Bound: 1e-5 of sum_k |a||b| (fp32 rounding of up to 1024 terms, random signs)."""
+    ld = (L + 63) // 64 * 64
+    g = torch.Generator().manual_seed(L + 3 * nslab)
+    ab = torch.zeros(2 * nslab, 1, L, ld, dtype=torch.float32)
+    ab[..., :L] = torch.randn(2 * nslab, 1, L, L, generator=g)
+    y = tops.triangle_mul.triangle_einsum(ab.to(device), L, ld, nslab, 1)
+    assert y.dtype == torch.float32
+    a, b = ab[:nslab, 0, :, :L].double(), ab[nslab:, 0, :, :L].double()
+    expect = torch.bmm(a, b.transpose(1, 2))
+    scale = torch.bmm(a.abs(), b.abs().transpose(1, 2))
+    err = (y[:, 0, :, :L].cpu().double() - expect).abs()
+    assert bool((err <= 1e-5 * scale + 1e-30).all()), f"L={L}: max err/scale {float((err / scale).max()):.3e}"
 
 
 @pytest.mark.parametrize("L,nslab,pad,dtype", [(1024, 8, 128, torch.bfloat16), (600, 16, 64, torch.bfloat16),

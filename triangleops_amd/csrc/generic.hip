@@ -17,7 +17,6 @@
 //   tmu_generic_in_kernel     triangle_multiplicative_update input phase at any C / C_out:
 //                             ab[f] = (xn . Wp[f] + Bp[f]) * sigmoid(xn . Wg[f] + Bg[f]) * mask,
 //                             xn = (x - mean) * rstd (the LN affine is folded into Wp / Wg)
-//   tmu_generic_einsum_kernel fp32 batched y = A . B^T (64 x 64 tiles, 4 x 4 per thread)
 //   tmu_generic_out_kernel    output phase: (yn . Wp + Bp) * sigmoid(xn . Wg + Bg), yn = LN_out(y)
 //
 // Reference: triangle_attn/module.py:57-125 and benchmarks/references.py:174-205 (the op),
@@ -389,57 +388,6 @@ __global__ __launch_bounds__(256) void tmu_generic_in_kernel(const T* __restrict
   }
 }
 
-// fp32 batched product: per slab s, Y[i][j] = sum_k A[i][k] B[j][k] over k < round_up(L, 64)
-// (the columns [L, ld) are zero; those past round_up(L, 64) are row padding and not read).
-__global__ __launch_bounds__(256) void tmu_generic_einsum_kernel(const float* __restrict__ A,
-                                                                const float* __restrict__ Bm, float* __restrict__ Y,
-                                                                int64_t L, int64_t ld, int64_t ldy, int tiles) {
-  constexpr int TM = 64, TK = 16;
-  __shared__ float As[TK][TM + 1], Bs[TK][TM + 1];
-  const int64_t slab = blockIdx.x / (tiles * tiles);
-  const int rem = (int)(blockIdx.x % (tiles * tiles));
-  const int tm = rem / tiles, tn = rem % tiles;
-  const float* Ab = A + slab * L * ld;
-  const float* Bb = Bm + slab * L * ld;
-  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  float acc[4][4] = {};
-  const int64_t kend = (L + 63) / 64 * 64;  // <= ld
-  for (int64_t k0 = 0; k0 < kend; k0 += TK) {
-    for (int e = tid; e < TM * TK; e += 256) {
-      const int r = e / TK, k = e % TK;
-      const int64_t ia = (int64_t)tm * TM + r, ib = (int64_t)tn * TM + r;
-      As[k][r] = ia < L ? Ab[ia * ld + k0 + k] : 0.f;
-      Bs[k][r] = ib < L ? Bb[ib * ld + k0 + k] : 0.f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < TK; ++k) {
-      float a[4], b[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        a[u] = As[k][ty * 4 + u];
-        b[u] = Bs[k][tx * 4 + u];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(a[u], b[v], acc[u][v]);
-    }
-    __syncthreads();
-  }
-  float* Yb = Y + slab * L * ldy;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t i = (int64_t)tm * TM + ty * 4 + u;
-    if (i >= L) continue;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t j = (int64_t)tn * TM + tx * 4 + v;
-      if (j < L) Yb[i * ldy + j] = acc[u][v];
-    }
-  }
-}
-
 template <typename T>
 __global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restrict__ y, const T* __restrict__ x,
                                                              const T* __restrict__ Wp, const T* __restrict__ Wg,
@@ -490,12 +438,213 @@ __global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restric
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Tiled forms of the two phases for C <= 256 (the kernels above remain for wider C): a block
+// takes a tile of tokens, normalises them into LDS k-major ([channel][token], fp32, rounded to
+// the I/O type as the products' operand, exactly as above), stages the weights of a chunk of
+// output features k-major through LDS in 32-deep k-tiles, and each thread accumulates 4 tokens
+// x 4 features of P and of G in registers (fp32 FMAs), then applies bias, gate and mask.
+//   input phase:  64 tokens of one row r of the (B, L, ld) store grid (tokens (r, c) or,
+//                 transposed, (c, r), c = c0 .. c0 + 63; c >= L stores zeros), 64-feature chunks,
+//                 each thread's 4 tokens stored as one vector per feature (contiguous in ab)
+//   output phase: 32 tokens (b, i, j0 .. j0 + 31), y read channel-major 32 tokens per channel,
+//                 128-feature chunks, each thread's 4 features stored as one vector per token
+// ---------------------------------------------------------------------------------------------
+constexpr int kTinTok = 64, kTinRow = kTinTok + 4;    // input phase: tokens per tile, LDS row
+constexpr int kToutTok = 32, kToutRow = kToutTok + 4;  // output phase
+constexpr int kTF = 128, kTFRow = kTF + 4;              // output phase: features per chunk, LDS row
+constexpr int kTK = 32;                                 // k-tile of the staged weights
+
+// LayerNorm of the `ntok` token columns of a k-major LDS tile (4 threads per token, two-pass),
+// rounding the normalised values to T; rows k in [C, CK) are set to zero.
+template <typename T>
+__device__ inline void tiled_layer_norm(float* xs, int row, int ntok, int C, int CK, float eps) {
+  const int t = threadIdx.x >> 2, part = threadIdx.x & 3;
+  if (t >= ntok) return;  // whole quads drop out together, so the quad sums stay exact
+  float s = 0.f;
+  for (int k = part; k < C; k += 4) s += xs[k * row + t];
+  const float mean = group_sum<4>(s) / (float)C;
+  float q = 0.f;
+  for (int k = part; k < C; k += 4) {
+    const float d = xs[k * row + t] - mean;
+    q = fmaf(d, d, q);
+  }
+  const float rstd = rsqrtf(group_sum<4>(q) / (float)C + eps);
+  for (int k = part; k < CK; k += 4) xs[k * row + t] = k < C ? (float)(T)((xs[k * row + t] - mean) * rstd) : 0.f;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_gen_in_tiled_kernel(const T* __restrict__ x, const int8_t* __restrict__ mask,
+                                                              const T* __restrict__ Wp, const T* __restrict__ Wg,
+                                                              const float* __restrict__ Bp, const float* __restrict__ Bg,
+                                                              T* __restrict__ ab, int64_t L, int C, int Cout, int64_t ld,
+                                                              int64_t fstride, int transpose, float eps) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CK = (C + kTK - 1) / kTK * kTK;
+  float* xs = sm;                     // [CK][kTinRow]  normalised tile
+  float* wps = xs + CK * kTinRow;     // [kTK][kTinRow] P weights of the chunk, k-major
+  float* wgs = wps + kTK * kTinRow;   // [kTK][kTinRow] G weights
+  float* msk = wgs + kTK * kTinRow;   // [kTinTok] 1 for a valid, unmasked token
+  const int tid = threadIdx.x;
+  const int64_t tpr = ld / kTinTok, rr = blockIdx.x / tpr, r = rr % L, b = rr / L;
+  const int64_t c0 = (blockIdx.x % tpr) * kTinTok;
+  auto token = [&](int t) -> int64_t {  // x / mask index of tile token t (t >= L - c0: position L - 1)
+    int64_t c = c0 + t;
+    c = c < L ? c : L - 1;
+    return transpose ? (b * L + c) * L + r : (b * L + r) * L + c;
+  };
+  for (int e = tid; e < kTinTok * C; e += 256) {  // row-major reads, k-major LDS
+    const int t = e / C, k = e % C;
+    xs[k * kTinRow + t] = (float)x[token(t) * C + k];
+  }
+  if (tid < kTinTok) msk[tid] = c0 + tid < L ? (mask ? (mask[token(tid)] != 0 ? 1.f : 0.f) : 1.f) : 0.f;
+  __syncthreads();
+  tiled_layer_norm<T>(xs, kTinRow, kTinTok, C, CK, eps);
+
+  const int ty = tid >> 4, tx = tid & 15;  // tokens 4 ty .. + 3, chunk features 4 tx .. + 3
+  T* abt = ab + (b * L + r) * ld + c0 + 4 * ty;
+  for (int f0 = 0; f0 < Cout; f0 += 64) {
+    float ap[4][4] = {}, ag[4][4] = {};
+    for (int k0 = 0; k0 < CK; k0 += kTK) {
+      __syncthreads();  // the previous k-tile's weights are consumed (first time: the tile is normalised)
+      for (int e = tid; e < 64 * kTK; e += 256) {
+        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
+        const bool ok = ff < Cout && kk < C;
+        wps[k * kTinRow + f] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
+        wgs[k * kTinRow + f] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int k = 0; k < kTK; ++k) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kTinRow + 4 * ty]);
+        const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTinRow + 4 * tx]);
+        const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTinRow + 4 * tx]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
+            ag[u][v] = fmaf(a[u], wg[v], ag[u][v]);
+          }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int f = f0 + 4 * tx + v;
+      if (f >= Cout) break;
+      const float bp = Bp[f], bg = Bg[f];
+      vec<T, 4> o;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o[u] = (T)((ap[u][v] + bp) * sigmoid(ag[u][v] + bg) * msk[4 * ty + u]);
+      *reinterpret_cast<vec<T, 4>*>(abt + (int64_t)f * fstride) = o;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tmu_gen_out_tiled_kernel(const T* __restrict__ y, const T* __restrict__ x,
+                                                               const T* __restrict__ Wp, const T* __restrict__ Wg,
+                                                               const float* __restrict__ Bp,
+                                                               const float* __restrict__ Bg, const T* __restrict__ res,
+                                                               T* __restrict__ out, int64_t L, int C, int Cout,
+                                                               int64_t ldy, int64_t cstride, float eps) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CK = (C + kTK - 1) / kTK * kTK;
+  float* ys = sm;                      // [CK][kToutRow]  LN_out(y), k-major
+  float* xs = ys + CK * kToutRow;      // [CK][kToutRow]  LN_in(x)
+  float* wps = xs + CK * kToutRow;     // [kTK][kTFRow]
+  float* wgs = wps + kTK * kTFRow;     // [kTK][kTFRow]
+  const int tid = threadIdx.x;
+  const int64_t tpr = (L + kToutTok - 1) / kToutTok, bi = blockIdx.x / tpr;  // bi = b * L + i
+  const int64_t j0 = (blockIdx.x % tpr) * kToutTok;
+  const int ntok = (int)(L - j0 < kToutTok ? L - j0 : kToutTok);
+  for (int e = tid; e < kToutTok * C; e += 256) {  // y channel-major: 32 consecutive tokens per channel
+    const int k = e / kToutTok, t = e % kToutTok;
+    ys[k * kToutRow + t] = t < ntok ? (float)y[(int64_t)k * cstride + bi * ldy + j0 + t] : 0.f;
+  }
+  for (int e = tid; e < kToutTok * C; e += 256) {  // x token-major
+    const int t = e / C, k = e % C;
+    xs[k * kToutRow + t] = t < ntok ? (float)x[(bi * L + j0 + t) * C + k] : 0.f;
+  }
+  __syncthreads();
+  tiled_layer_norm<T>(ys, kToutRow, kToutTok, C, CK, eps);
+  tiled_layer_norm<T>(xs, kToutRow, kToutTok, C, CK, eps);
+
+  const int ty = tid >> 5, tx = tid & 31;  // tokens 4 ty .. + 3, chunk features 4 tx .. + 3
+  for (int f0 = 0; f0 < Cout; f0 += kTF) {
+    float ap[4][4] = {}, ag[4][4] = {};
+    for (int k0 = 0; k0 < CK; k0 += kTK) {
+      __syncthreads();
+      for (int e = tid; e < kTF * kTK; e += 256) {
+        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
+        const bool ok = ff < Cout && kk < C;
+        wps[k * kTFRow + f] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
+        wgs[k * kTFRow + f] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int k = 0; k < kTK; ++k) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(&ys[(k0 + k) * kToutRow + 4 * ty]);
+        const f32x4 g = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kToutRow + 4 * ty]);
+        const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTFRow + 4 * tx]);
+        const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTFRow + 4 * tx]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
+            ag[u][v] = fmaf(g[u], wg[v], ag[u][v]);
+          }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * ty + u;
+      if (t >= ntok) break;
+      const int64_t o = (bi * L + j0 + t) * Cout;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int f = f0 + 4 * tx + v;
+        if (f >= Cout) break;
+        const T rv = (T)((ap[u][v] + Bp[f]) * sigmoid(ag[u][v] + Bg[f]));
+        out[o + f] = res ? (T)((float)res[o + f] + (float)rv) : rv;
+      }
+    }
+  }
+}
+
 int tmu_generic_input_phase(const void* x, const void* mask, const void* Wp, const void* Wg, const float* Bp,
                             const float* Bg, void* ab, int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ld,
                             int transpose, float eps, int dtype, hipStream_t st) {
   TOPS_REQUIRE(C >= 1 && C <= 1024 && C_out >= 1 && C_out <= 4096,
                "tops_tmu_input_phase: supports C <= 1024, C_out <= 4096 (got %lld, %lld)", (long long)C,
                (long long)C_out);
+  if (C <= 256) {  // tiled kernel
+    const int64_t tiles = B * L * (ld / kTinTok);
+    if (tiles == 0) return TOPS_OK;
+    TOPS_REQUIRE(tiles < (1LL << 31), "tops_tmu_input_phase: too many tokens");
+    const int CK = (int)((C + kTK - 1) / kTK * kTK);
+    const size_t lds = ((size_t)(CK + 2 * kTK) * kTinRow + kTinTok) * sizeof(float);
+    const int64_t fstride = B * L * ld;
+#define TOPS_GEN_IN_T(TT)                                                                                        \
+  do {                                                                                                           \
+    hipFuncSetAttribute((const void*)tmu_gen_in_tiled_kernel<TT>, hipFuncAttributeMaxDynamicSharedMemorySize,    \
+                        (int)lds);                                                                               \
+    hipLaunchKernelGGL((tmu_gen_in_tiled_kernel<TT>), dim3((unsigned)tiles), dim3(256), lds, st, (const TT*)x,     \
+                       (const int8_t*)mask, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (TT*)ab, L, (int)C, (int)C_out, ld, \
+                       fstride, transpose, eps);                                                                  \
+  } while (0)
+    if (dtype == TOPS_DTYPE_BF16)
+      TOPS_GEN_IN_T(__bf16);
+    else if (dtype == TOPS_DTYPE_F16)
+      TOPS_GEN_IN_T(_Float16);
+    else if (dtype == TOPS_DTYPE_F32)
+      TOPS_GEN_IN_T(float);
+    else
+      return fail(TOPS_EUNSUPPORTED, "tops_tmu_input_phase: unsupported dtype code %d", dtype);
+#undef TOPS_GEN_IN_T
+    return launched("tops_tmu_input_phase");
+  }
   const int64_t blocks = (B * L * L + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   const size_t lds = (size_t)kGenTok * C * sizeof(float);
@@ -512,25 +661,38 @@ int tmu_generic_input_phase(const void* x, const void* mask, const void* Wp, con
   return launched("tops_tmu_input_phase");
 }
 
-int tmu_generic_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
-                       hipStream_t st) {
-  TOPS_REQUIRE(dtype == TOPS_DTYPE_F32, "tops_tmu_einsum: the any-shape product is fp32 only (dtype %d)", dtype);
-  const int tiles = (int)((L + 63) / 64);
-  const int64_t grid = nslab * tiles * tiles;
-  if (grid == 0) return TOPS_OK;
-  TOPS_REQUIRE(grid < (1LL << 31), "tops_tmu_einsum: too many tiles");
-  const float* A = (const float*)ab;
-  hipLaunchKernelGGL(tmu_generic_einsum_kernel, dim3((unsigned)grid), dim3(256), 0, st, A, A + nslab * L * ld,
-                     (float*)y, L, ld, ldy, tiles);
-  return launched("tops_tmu_einsum");
-}
-
 int tmu_generic_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* Bp,
                              const float* Bg, const void* res, void* out, int64_t B, int64_t L, int64_t C,
                              int64_t C_out, int64_t ldy, float eps, int dtype, hipStream_t st) {
   TOPS_REQUIRE(C >= 1 && C <= 512 && C_out >= 1 && C_out <= 4096,
                "tops_tmu_output_phase: supports C <= 512, C_out <= 4096 (got %lld, %lld)", (long long)C,
                (long long)C_out);
+  if (C <= 256) {  // tiled kernel
+    const int64_t tiles = B * L * ((L + kToutTok - 1) / kToutTok);
+    if (tiles == 0) return TOPS_OK;
+    TOPS_REQUIRE(tiles < (1LL << 31), "tops_tmu_output_phase: too many tokens");
+    const int CK = (int)((C + kTK - 1) / kTK * kTK);
+    const size_t lds = ((size_t)2 * CK * kToutRow + (size_t)2 * kTK * kTFRow) * sizeof(float);
+    const int64_t cstride = B * L * ldy;
+#define TOPS_GEN_OUT_T(TT)                                                                                       \
+  do {                                                                                                           \
+    hipFuncSetAttribute((const void*)tmu_gen_out_tiled_kernel<TT>, hipFuncAttributeMaxDynamicSharedMemorySize,   \
+                        (int)lds);                                                                               \
+    hipLaunchKernelGGL((tmu_gen_out_tiled_kernel<TT>), dim3((unsigned)tiles), dim3(256), lds, st, (const TT*)y,    \
+                       (const TT*)x, (const TT*)Wp, (const TT*)Wg, Bp, Bg, (const TT*)res, (TT*)out, L, (int)C,    \
+                       (int)C_out, ldy, cstride, eps);                                                            \
+  } while (0)
+    if (dtype == TOPS_DTYPE_BF16)
+      TOPS_GEN_OUT_T(__bf16);
+    else if (dtype == TOPS_DTYPE_F16)
+      TOPS_GEN_OUT_T(_Float16);
+    else if (dtype == TOPS_DTYPE_F32)
+      TOPS_GEN_OUT_T(float);
+    else
+      return fail(TOPS_EUNSUPPORTED, "tops_tmu_output_phase: unsupported dtype code %d", dtype);
+#undef TOPS_GEN_OUT_T
+    return launched("tops_tmu_output_phase");
+  }
   const int64_t blocks = (B * L * L + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   const size_t lds = (size_t)2 * kGenTok * C * sizeof(float);

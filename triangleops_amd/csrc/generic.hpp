@@ -10,8 +10,6 @@ namespace tops {
 int tmu_generic_input_phase(const void* x, const void* mask, const void* Wp, const void* Wg, const float* Bp,
                             const float* Bg, void* ab, int64_t B, int64_t L, int64_t C, int64_t C_out, int64_t ld,
                             int transpose, float eps, int dtype, hipStream_t st);
-int tmu_generic_einsum(const void* ab, void* y, int64_t nslab, int64_t L, int64_t ld, int64_t ldy, int dtype,
-                       hipStream_t st);
 int tmu_generic_output_phase(const void* y, const void* x, const void* Wp, const void* Wg, const float* Bp,
                              const float* Bg, const void* res, void* out, int64_t B, int64_t L, int64_t C,
                              int64_t C_out, int64_t ldy, float eps, int dtype, hipStream_t st);

@@ -770,6 +770,103 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
 }
 
 // ---------------------------------------------------------------------------------------------
+// Einsum in fp32 (fp32 I/O): the same Y = A . B^T per slab on the fp32 MFMA
+// (v_mfma_f32_32x32x2_f32: fp32 products, fp32 sums).  128 x 128 block tile, 4 waves of 64 x 64
+// (2 x 2 MFMA tiles), k-tiles of 32 register-staged into double-buffered LDS, one barrier per
+// k-tile.  Within a k-tile, MFMA k-step s (of 16) pairs k = s in lane half 0 with k = s + 16 in
+// lane half 1 (any k order applied to both operands gives the same product), so each lane's
+// operand values of a tile are 16 consecutive floats of one row: four 16-byte LDS reads per
+// fragment.  LDS rows are padded to 36 floats (the 32 rows of a fragment read spread over the
+// banks).  Rows >= L read as zeros; k < round_up(L, 64) is read (the columns [L, ld) are zeros).
+// ---------------------------------------------------------------------------------------------
+constexpr int kF32Row = 36;  // LDS floats per 32-float k-tile row
+
+__global__ __launch_bounds__(256, 2) void tmu_einsum_f32_kernel(const float* __restrict__ A,
+                                                               const float* __restrict__ Bm, float* __restrict__ Y,
+                                                               int64_t L, int64_t ld, int64_t ldy, int tiles) {
+  constexpr int TM = 128, TK = 32;
+  __shared__ __attribute__((aligned(16))) float as[2][TM * kF32Row];
+  __shared__ __attribute__((aligned(16))) float bs[2][TM * kF32Row];
+  const int64_t slab = blockIdx.x / ((int64_t)tiles * tiles);
+  const int rem = (int)(blockIdx.x % ((int64_t)tiles * tiles));
+  const int tm = rem / tiles, tn = rem % tiles;
+  const float* Ab = A + slab * L * ld;
+  const float* Bb = Bm + slab * L * ld;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1, hl = lane >> 5, col = lane & 31;
+  const int nkt = (int)((L + 63) / 64 * 64 / TK);
+
+  // global -> registers: thread t moves the 16-byte chunks c = t + 256 i (i < 4) of each operand
+  // tile, row c / 8, floats 4 (c % 8) .. + 3: eight lanes per 128-byte row
+  f32x4 ra[4], rb[4];
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, p = c & 7;
+      const int64_t ia = (int64_t)tm * TM + r, ib = (int64_t)tn * TM + r;
+      ra[i] = ia < L ? ldg<f32x4>(Ab + ia * ld + (int64_t)kt * TK + 4 * p) : f32x4{};
+      rb[i] = ib < L ? ldg<f32x4>(Bb + ib * ld + (int64_t)kt * TK + 4 * p) : f32x4{};
+    }
+  };
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i, r = c >> 3, p = c & 7;
+      *reinterpret_cast<f32x4*>(&as[buf][r * kF32Row + 4 * p]) = ra[i];
+      *reinterpret_cast<f32x4*>(&bs[buf][r * kF32Row + 4 * p]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt) gload(kt + 1);
+    f32x4 fa[2][4], fb[2][4];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        fa[mi][q] = *reinterpret_cast<const f32x4*>(&as[buf][(wm * 64 + 32 * mi + col) * kF32Row + 16 * hl + 4 * q]);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        fb[ni][q] = *reinterpret_cast<const f32x4*>(&bs[buf][(wn * 64 + 32 * ni + col) * kF32Row + 16 * hl + 4 * q]);
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] =
+              __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mi][s / 4][s % 4], fb[ni][s / 4][s % 4], acc[mi][ni], 0, 0, 0);
+    if (kt + 1 < nkt) lstore(buf ^ 1);  // buf ^ 1 was last read before the previous barrier
+    __syncthreads();
+  }
+
+  // D slot v of lane (col, hl): row 8 (v / 4) + 4 hl + v % 4, column col of its 32 x 32 tile
+  float* Yb = Y + slab * L * ldy;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int64_t j = (int64_t)tn * TM + wn * 64 + 32 * ni + col;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t i = (int64_t)tm * TM + wm * 64 + 32 * mi + 8 * (v / 4) + 4 * hl + v % 4;
+        if (i < L && j < L) Yb[i * ldy + j] = acc[mi][ni][v];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Output phase (C = C_out = 128).  64-token tiles, 12 waves in two roles:
 //   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
@@ -1108,7 +1205,15 @@ extern "C" int tops_tmu_einsum(const void* ab, void* y, int64_t nslab, int64_t L
                (long long)nslab, (long long)L, (long long)ld, (long long)ldy);
   if (L == 0 || nslab == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == TOPS_DTYPE_F32) return tmu_generic_einsum(ab, y, nslab, L, ld, ldy, dtype, st);
+  if (dtype == TOPS_DTYPE_F32) {
+    const int t = (int)((L + 127) / 128);
+    const int64_t grid = nslab * t * t;
+    TOPS_REQUIRE(grid < (1LL << 31), "tops_tmu_einsum: too many tiles");
+    const float* A = (const float*)ab;
+    hipLaunchKernelGGL(tmu_einsum_f32_kernel, dim3((unsigned)grid), dim3(256), 0, st, A, A + nslab * L * ld, (float*)y,
+                       L, ld, ldy, t);
+    return launched("tops_tmu_einsum");
+  }
   if (dtype == TOPS_DTYPE_BF16) return tmu_einsum_t<__bf16>(ab, y, nslab, L, ld, ldy, st);
   if (dtype == TOPS_DTYPE_F16) return tmu_einsum_t<_Float16>(ab, y, nslab, L, ld, ldy, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tmu_einsum: unsupported dtype code %d", dtype);
