@@ -8,9 +8,9 @@
 //
 //   tri_generic_prep_kernel   per token: LN(x) (fp32, two-pass), Q / K / V of all heads and
 //                             the row-shared pair bias bias[h][a][b] = LN(x[a, b]) . Wz[h] + bz[h]
-//   tri_generic_attn_kernel   one thread per (row i, head h, query q): online softmax over the
-//                             row's keys in fp32, scores q . k * scale + bias, masked keys get
-//                             the reference's fp32 "+ (-1e9)"
+//   tri_generic_attn_kernel   64 queries of one (row i, head h) per block, keys split over 4 waves
+//                             in 32-key chunks staged in LDS: online softmax in fp32, scores
+//                             q . k * scale + bias, masked keys get the reference's fp32 "+ (-1e9)"
 //   gate_generic_kernel       per token: y = (o * sigmoid(g . Wg^T + bg)) -> io, out = y . Wo^T + bo
 //                             with g = LN(gin) or gin
 //
@@ -101,58 +101,149 @@ __global__ __launch_bounds__(256) void tri_generic_prep_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention over R rows of N queries and N keys: thread = (row i, head h, query q), q fastest
-// so a wave shares (i, h) and its K / V loads are broadcasts.  DM >= D is the register length
-// of q and o.  Masked keys (mask[i*sm0 + k*sm1] == 0) get "+ (-1e9)" in fp32 (triangle
-// attention) or -inf (MASK_INF, attention_pair_bias: a row without valid keys gives NaN, as
-// torch's softmax does).
+// Attention over R rows of N queries and N keys, any H, D <= DM.  A block takes 64 queries of
+// one (row i, head h), lane = query; its 4 waves split the keys into 32-key chunks (chunk c to
+// wave c % 4).  Per chunk a wave stages the chunk's K and V in LDS (fp32; every lane then reads
+// the same element, a broadcast), computes the 32 scores of its queries (q . k * scale + bias;
+// masked keys (mask[i*sm0 + k*sm1] == 0) get "+ (-1e9)" in fp32 (triangle attention) or -inf
+// (MASK_INF, attention_pair_bias: a row without valid keys gives NaN, as torch's softmax does);
+// keys >= N are left out), rescales its running (o, l) once to the chunk's maximum and adds
+// exp(s - m) and exp(s - m) v.  The 4 waves' (m, l, o) are merged through LDS at the end.
 // ---------------------------------------------------------------------------------------------
+constexpr int kGenKC = 32, kGenAW = 4;  // keys per chunk, waves (key splits) per block
+
 template <typename T, int DM, bool MASK_INF>
-__global__ __launch_bounds__(256) void tri_generic_attn_kernel(const T* __restrict__ qi_, const T* __restrict__ ki_,
+__global__ __launch_bounds__(256, 2) void tri_generic_attn_kernel(const T* __restrict__ qi_, const T* __restrict__ ki_,
                                                               const T* __restrict__ vi_, const float* __restrict__ bias,
                                                               const int8_t* __restrict__ mask, int64_t sm0, int64_t sm1,
                                                               T* __restrict__ out, int64_t so0, int64_t so1, int64_t R,
                                                               int64_t N, int H, int D, float scale) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= R * H * N) return;
-  const int64_t q = idx % N, ih = idx / N;
+  __shared__ __attribute__((aligned(16))) float kvs[kGenAW][2][kGenKC][DM];  // per wave: K, V of its chunk
+  __shared__ float madd[kGenAW][kGenKC];                                     // per key: 0, -1e9, -inf
+  __shared__ float mls[kGenAW][64][2];                                       // per wave and query: m, l
+  const int64_t nqb = (N + 63) / 64, qb = blockIdx.x % nqb, ih = blockIdx.x / nqb;
   const int h = (int)(ih % H);
   const int64_t i = ih / H;
+  (void)R;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t q = qb * 64 + lane, qq = q < N ? q : N - 1;
   const int HD = H * D;
   float qv[DM], o[DM];
-  const T* qp = qi_ + (i * N + q) * HD + h * D;
+  const T* qp = qi_ + (i * N + qq) * HD + h * D;
 #pragma unroll
   for (int d = 0; d < DM; ++d) {
     qv[d] = d < D ? (float)qp[d] * scale : 0.f;
     o[d] = 0.f;
   }
-  const float* brow = bias + ((int64_t)h * N + q) * N;
+  const float* brow = bias + ((int64_t)h * N + qq) * N;
   float m = -INFINITY, l = 0.f;
-  for (int64_t k = 0; k < N; ++k) {
-    const T* kp = ki_ + (i * N + k) * HD + h * D;
-    float s = 0.f;
+  const int64_t nch = (N + kGenKC - 1) / kGenKC;
+  for (int64_t c = wave; c < nch; c += kGenAW) {
+    const int64_t k0 = c * kGenKC;
+    for (int e = lane; e < kGenKC * DM; e += 64) {
+      const int kk = e / DM, d = e % DM;
+      const int64_t key = k0 + kk;
+      const bool ok = key < N && d < D;
+      const int64_t off = (i * N + key) * HD + h * D + d;
+      kvs[wave][0][kk][d] = ok ? (float)ki_[off] : 0.f;
+      kvs[wave][1][kk][d] = ok ? (float)vi_[off] : 0.f;
+    }
+    if (lane < kGenKC) {
+      const int64_t key = k0 + lane;
+      madd[wave][lane] = key >= N ? -INFINITY
+                         : (mask && mask[i * sm0 + key * sm1] == 0) ? (MASK_INF ? -INFINITY : -1e9f)
+                                                                     : 0.f;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 8-key sub-chunks, each with its own maximum and one rescale of (o, l)
+#pragma unroll 1
+    for (int k8 = 0; k8 < kGenKC; k8 += 8) {
+      float sc[8] = {};
+      // q . k for the 8 keys, 4 channels per step; at most 32 K values live (the pins end a step's
+      // products, the empty asm with a memory clobber keeps the next step's LDS reads after them)
 #pragma unroll
-    for (int d = 0; d < DM; ++d)
-      if (d < D) s = fmaf(qv[d], (float)kp[d], s);
-    s += brow[k];
-    if (mask && mask[i * sm0 + k * sm1] == 0) s = MASK_INF ? -INFINITY : s + -1e9f;
-    const float mn = fmaxf(m, s);
-    // while every key so far is masked (MASK_INF), m = mn = -inf: shift by 0 instead, so the
-    // masked key gets p = 0 and the state stays (m, l, o) = (-inf, 0, 0) instead of NaN
-    const float sh = mn == -INFINITY ? 0.f : mn;
-    const float corr = __expf(m - sh), p = __expf(s - sh);
-    m = mn;
-    l = l * corr + p;
-    const T* vp = vi_ + (i * N + k) * HD + h * D;
+      for (int d0 = 0; d0 < DM; d0 += 4) {
 #pragma unroll
-    for (int d = 0; d < DM; ++d)
-      if (d < D) o[d] = fmaf(p, (float)vp[d], o[d] * corr);
+        for (int kk = 0; kk < 8; ++kk) {
+          const f32x4 kq = *reinterpret_cast<const f32x4*>(&kvs[wave][0][k8 + kk][d0]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[kk] = fmaf(qv[d0 + e], kq[e], sc[kk]);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) pin(sc[kk]);  // this step's products are done here
+        asm volatile("" ::: "memory");                 // and the next step's reads follow
+      }
+      float cm = -INFINITY;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const float a = sc[kk];
+        const float ma = madd[wave][k8 + kk];
+        const int64_t key = k0 + k8 + kk;
+        const float sk = a + (key < N ? brow[key] : 0.f);
+        sc[kk] = ma == 0.f ? sk : (ma == -INFINITY ? -INFINITY : sk + ma);
+        cm = fmaxf(cm, sc[kk]);
+      }
+      const float mn = fmaxf(m, cm);
+      // while every key so far is left out, m = mn = -inf: shift by 0 instead, so those keys get
+      // p = 0 and the state stays (m, l, o) = (-inf, 0, 0) instead of NaN
+      const float sh = mn == -INFINITY ? 0.f : mn;
+      const float corr = __expf(m - sh);
+      l *= corr;
+#pragma unroll
+      for (int d = 0; d < DM; ++d) o[d] *= corr;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const float p = __expf(sc[kk] - sh);
+        l += p;
+#pragma unroll
+        for (int d = 0; d < DM; d += 4) {
+          const f32x4 vq = *reinterpret_cast<const f32x4*>(&kvs[wave][1][k8 + kk][d]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[d + e] = fmaf(p, vq[e], o[d + e]);
+        }
+#pragma unroll
+        for (int d = 0; d < DM; ++d) pin(o[d]);
+        asm volatile("" ::: "memory");
+      }
+      m = mn;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the chunk's K / V are read before the next chunk overwrites them
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  const float inv = 1.f / l;
-  T* dst = out + i * so0 + q * so1 + h * D;
+  // ---- merge the 4 waves' partial states (o goes through the K / V staging area) ----
+  __syncthreads();
+  float* ob = &kvs[0][0][0][0];  // [kGenAW][64][DM]
 #pragma unroll
-  for (int d = 0; d < DM; ++d)
-    if (d < D) dst[d] = (T)(o[d] * inv);
+  for (int d = 0; d < DM; ++d) ob[(wave * 64 + lane) * DM + d] = o[d];
+  mls[wave][lane][0] = m;
+  mls[wave][lane][1] = l;
+  __syncthreads();
+  float mw[kGenAW], mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kGenAW; ++w) {
+    mw[w] = mls[w][lane][0];
+    mx = fmaxf(mx, mw[w]);
+  }
+  const float sh = mx == -INFINITY ? 0.f : mx;
+  float sw[kGenAW], lt = 0.f;
+#pragma unroll
+  for (int w = 0; w < kGenAW; ++w) {
+    sw[w] = __expf(mw[w] - sh);
+    lt += sw[w] * mls[w][lane][1];
+  }
+  const float inv = 1.f / lt;
+  if (q < N) {
+    T* dst = out + i * so0 + q * so1 + h * D;
+    for (int d = wave; d < D; d += kGenAW) {  // each wave writes every 4th element of the row
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGenAW; ++w) acc += sw[w] * ob[(w * 64 + lane) * DM + d];
+      dst[d] = (T)(acc * inv);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -228,8 +319,9 @@ template <typename T>
 static int tri_generic_attention_t(const void* q, const void* k, const void* v, const float* bias, const void* mask,
                                    int64_t sm0, int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int H,
                                    int D, float scale, hipStream_t st) {
-  const int64_t blocks = (N * H * N + 255) / 256;
+  const int64_t blocks = N * H * ((N + 63) / 64);
   if (blocks == 0) return TOPS_OK;
+  TOPS_REQUIRE(blocks < (1LL << 31), "tops_tri_generic_attention: too many query blocks");
 #define TOPS_GEN_ATTN(DMV)                                                                                           \
   hipLaunchKernelGGL((tri_generic_attn_kernel<T, DMV, false>), dim3((unsigned)blocks), dim3(256), 0, st,            \
                      (const T*)q, (const T*)k, (const T*)v, bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, \
@@ -326,7 +418,7 @@ static int apb_generic_prep_t(const void* X, const void* wqkv, const void* Z, in
 template <typename T>
 static int apb_generic_attention_t(const void* q, const void* k, const void* v, const float* bias, const void* mask,
                                    void* Og, int64_t M, int H, int D, float scale, hipStream_t st) {
-  const int64_t blocks = (M * H + 255) / 256;
+  const int64_t blocks = H * ((M + 63) / 64);
   if (blocks == 0) return TOPS_OK;
   const int64_t HD = (int64_t)H * D;
 #define TOPS_GEN_APB(DMV)                                                                                         \
