@@ -29,6 +29,7 @@
 namespace tops {
 
 constexpr int kGenTok = 16;  // tokens per block; 16 lanes per token for the LayerNorm sums
+constexpr int kTK = 32;      // k-tile of the weights the tiled kernels stage through LDS
 
 // LayerNorm of kGenTok token rows held in LDS (fp32, row length C, row stride ld): 16
 // consecutive lanes per token, two-pass statistics.  Writes normalised rows back in place.
@@ -302,11 +303,192 @@ __global__ __launch_bounds__(256) void gate_generic_kernel(const T* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Tiled pre-pass and gate for C_in <= 256 (and H * D <= 256 for the gate): 64 tokens per block,
+// 256 threads.  Activations go to LDS k-major ([channel][token], fp32); every product is a block
+// GEMM over that tile (tiled_gemm64: weights of 64 output features at a time staged k-major
+// through LDS in 32-deep k-tiles, 4 tokens x 4 features per thread in registers).  Rounding
+// points are those of the per-token kernels above.
+// ---------------------------------------------------------------------------------------------
+constexpr int kGT = 64, kGRow = kGT + 4;  // tokens per tile, LDS row of the k-major tiles
+
+// out[t][f] = sum_k a[k][t] * W[f][k] (a: k-major LDS tile of kGT tokens, K valid rows of CK;
+// W: F x K row-major in global memory), handed to epi(t, f, value) for t < ntok, f < F.  With
+// ROUND the activations are rounded to T as the products' operand.
+template <typename T, bool ROUND, typename Epi>
+__device__ __attribute__((always_inline)) inline void tiled_gemm64(const float* a, int K, int CK, const T* __restrict__ W, int F, float* ws,
+                                    int ntok, Epi epi) {
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  for (int f0 = 0; f0 < F; f0 += 64) {
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < CK; k0 += kTK) {
+      __syncthreads();  // the previous k-tile's weights are consumed
+      for (int e = tid; e < 64 * kTK; e += 256) {
+        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
+        ws[k * kGRow + f] = ff < F && kk < K ? (float)W[(int64_t)ff * K + kk] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int k = 0; k < kTK; ++k) {
+        f32x4 x = *reinterpret_cast<const f32x4*>(&a[(k0 + k) * kGRow + 4 * ty]);
+        if constexpr (ROUND) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) x[u] = (float)(T)x[u];
+        }
+        const f32x4 w = *reinterpret_cast<const f32x4*>(&ws[k * kGRow + 4 * tx]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(x[u], w[v], acc[u][v]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = 4 * ty + u, f = f0 + 4 * tx + v;
+        if (t < ntok && f < F) epi(t, f, acc[u][v]);
+      }
+  }
+}
+
+// LayerNorm (optionally with the affine w, b) of the kGT token columns of a k-major tile, in place
+// (fp32, two-pass, 4 threads per token); rows [C, CK) are set to zero.
+template <typename T>
+__device__ __attribute__((always_inline)) inline void tiled_ln_affine(float* xs, int C, int CK, const T* __restrict__ w, const T* __restrict__ b,
+                                       float eps) {
+  const int t = threadIdx.x >> 2, part = threadIdx.x & 3;
+  float s = 0.f;
+  for (int k = part; k < C; k += 4) s += xs[k * kGRow + t];
+  const float mean = group_sum<4>(s) / (float)C;
+  float q = 0.f;
+  for (int k = part; k < C; k += 4) {
+    const float d = xs[k * kGRow + t] - mean;
+    q = fmaf(d, d, q);
+  }
+  const float rstd = rsqrtf(group_sum<4>(q) / (float)C + eps);
+  for (int k = part; k < CK; k += 4) {
+    float v = 0.f;
+    if (k < C) {
+      v = (xs[k * kGRow + t] - mean) * rstd;
+      if (w) v = v * (float)w[k] + (b ? (float)b[k] : 0.f);
+    }
+    xs[k * kGRow + t] = v;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tri_gen_prep_tiled_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
+                                                                const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                                int apply_ln, const T* __restrict__ wqkv,
+                                                                const T* __restrict__ WZ, const float* __restrict__ BZ,
+                                                                T* __restrict__ xln, T* __restrict__ qo,
+                                                                T* __restrict__ ko, T* __restrict__ vo,
+                                                                float* __restrict__ bias, int64_t N, int C, int H, int D,
+                                                                float eps) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CK = (C + kTK - 1) / kTK * kTK;
+  float* xs = sm;                  // [CK][kGRow]  (LN(x)), k-major
+  float* ws = xs + CK * kGRow;     // [kTK][kGRow] staged weights
+  const int tid = threadIdx.x;
+  const int64_t ntokall = N * N, tok0 = (int64_t)blockIdx.x * kGT;
+  const int ntok = (int)(ntokall - tok0 < kGT ? ntokall - tok0 : kGT);
+  for (int e = tid; e < kGT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    const int64_t tok = tok0 + t;
+    xs[c * kGRow + t] = t < ntok ? (float)x[(tok / N) * sx0 + (tok % N) * sx1 + c] : 0.f;
+  }
+  __syncthreads();
+  if (apply_ln) {
+    tiled_ln_affine<T>(xs, C, CK, w_ln, b_ln, eps);
+  } else {
+    for (int e = tid; e < (CK - C) * kGT; e += 256) xs[(C + e / kGT) * kGRow + e % kGT] = 0.f;
+  }
+  __syncthreads();
+  for (int e = tid; e < kGT * C; e += 256) {
+    const int t = e / C, c = e % C;
+    if (t < ntok) xln[(tok0 + t) * C + c] = (T)xs[c * kGRow + t];
+  }
+  const int HD = H * D;
+  // Q / K / V of all heads from LN(x) rounded to the I/O type; weight row f = (h, which, d).  The
+  // destination is picked by integer selects on address offsets (a pointer choice among the three
+  // becomes a table in private memory)
+  const uint64_t aq = (uint64_t)qo, dk = (uint64_t)ko - aq, dv = (uint64_t)vo - aq;
+  tiled_gemm64<T, true>(xs, C, CK, wqkv, 3 * HD, ws, ntok, [=](int t, int f, float v) {
+    const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+    const uint64_t base = aq + (which == 1 ? dk : 0) + (which == 2 ? dv : 0);
+    reinterpret_cast<T*>(base)[(tok0 + t) * HD + h * D + d] = (T)v;
+  });
+  // the row-shared pair bias from the unrounded LN(x), fp32
+  tiled_gemm64<T, false>(xs, C, CK, WZ, H, ws, ntok,
+                         [=](int t, int h, float v) { bias[(int64_t)h * ntokall + tok0 + t] = v + (BZ ? BZ[h] : 0.f); });
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gate_gen_tiled_kernel(const T* __restrict__ o, int64_t so0, int64_t so1,
+                                                            const T* __restrict__ gin, int64_t sg0, int64_t sg1,
+                                                            const T* __restrict__ w_ln, const T* __restrict__ b_ln,
+                                                            float eps, int apply_ln, const T* __restrict__ Wg,
+                                                            const T* __restrict__ bg, const T* __restrict__ Wo,
+                                                            const T* __restrict__ bo, const T* __restrict__ res,
+                                                            int64_t sr0, int64_t sr1, T* __restrict__ out,
+                                                            int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int Cin,
+                                                            int HD, int Cout) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CinK = (Cin + kTK - 1) / kTK * kTK, HDK = (HD + kTK - 1) / kTK * kTK;
+  float* gs = sm;                  // [CinK][kGRow] gate input (normalised), k-major
+  float* ys = gs + CinK * kGRow;   // [HDK][kGRow]  o, then the gated activations
+  float* ws = ys + HDK * kGRow;    // [kTK][kGRow]
+  const int tid = threadIdx.x;
+  const int64_t M = M1 * M2, tok0 = (int64_t)blockIdx.x * kGT;
+  const int ntok = (int)(M - tok0 < kGT ? M - tok0 : kGT);
+  for (int e = tid; e < kGT * Cin; e += 256) {
+    const int t = e / Cin, c = e % Cin;
+    const int64_t tok = tok0 + t;
+    gs[c * kGRow + t] = t < ntok ? (float)gin[(tok / M2) * sg0 + (tok % M2) * sg1 + c] : 0.f;
+  }
+  for (int e = tid; e < kGT * HD; e += 256) {
+    const int t = e / HD, j = e % HD;
+    const int64_t tok = tok0 + t;
+    ys[j * kGRow + t] = t < ntok ? (float)o[(tok / M2) * so0 + (tok % M2) * so1 + j] : 0.f;
+  }
+  for (int e = tid; e < (HDK - HD) * kGT; e += 256) ys[(HD + e / kGT) * kGRow + e % kGT] = 0.f;
+  __syncthreads();
+  if (apply_ln) {
+    tiled_ln_affine<T>(gs, Cin, CinK, w_ln, b_ln, eps);
+  } else {
+    for (int e = tid; e < (CinK - Cin) * kGT; e += 256) gs[(Cin + e / kGT) * kGRow + e % kGT] = 0.f;
+  }
+  // gate: ys[j][t] = io(o * sigmoid(io(g) . Wg[j] + bg[j])), each element rewritten by the thread that reads it
+  tiled_gemm64<T, true>(gs, Cin, CinK, Wg, HD, ws, kGT, [=](int t, int j, float v) {
+    const float g = v + (bg ? (float)bg[j] : 0.f);
+    ys[j * kGRow + t] = (float)(T)(ys[j * kGRow + t] * sigmoid(g));
+  });
+  // output projection of the gated tile; with a residual, the result is rounded first
+  tiled_gemm64<T, false>(ys, HD, HDK, Wo, Cout, ws, ntok, [=](int t, int c, float v) {
+    const T r = (T)(v + (bo ? (float)bo[c] : 0.f));
+    const int64_t tok = tok0 + t, m1 = tok / M2, m2 = tok % M2;
+    out[m1 * sd0 + m2 * sd1 + c] = res ? (T)((float)res[m1 * sr0 + m2 * sr1 + c] + (float)r) : r;
+  });
+}
+
 template <typename T>
 static int tri_generic_prep_t(const void* x, int64_t sx0, int64_t sx1, const void* w_ln, const void* b_ln,
                               int apply_ln, const void* wqkv, const void* WZ, const float* BZ, void* xln, void* q,
                               void* k, void* v, float* bias, int64_t N, int C, int H, int D, float eps,
                               hipStream_t st) {
+  if (C <= 256) {  // tiled kernel
+    const int64_t tiles = (N * N + kGT - 1) / kGT;
+    if (tiles == 0) return TOPS_OK;
+    const int CK = (C + kTK - 1) / kTK * kTK;
+    const size_t lds = (size_t)(CK + kTK) * kGRow * sizeof(float);
+    hipFuncSetAttribute((const void*)tri_gen_prep_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)lds);
+    hipLaunchKernelGGL((tri_gen_prep_tiled_kernel<T>), dim3((unsigned)tiles), dim3(256), lds, st, (const T*)x, sx0, sx1,
+                       (const T*)w_ln, (const T*)b_ln, apply_ln, (const T*)wqkv, (const T*)WZ, BZ, (T*)xln, (T*)q,
+                       (T*)k, (T*)v, bias, N, C, H, D, eps);
+    return launched("tops_tri_generic_prep");
+  }
   const int64_t blocks = (N * N + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   hipLaunchKernelGGL((tri_generic_prep_kernel<T>), dim3((unsigned)blocks), dim3(256), kGenTok * C * sizeof(float), st,
@@ -342,6 +524,18 @@ static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* g
                           const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
                           int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int Cin, int HD, int Cout,
                           hipStream_t st) {
+  if (Cin <= 256 && HD <= 256) {  // tiled kernel
+    const int64_t tiles = (M1 * M2 + kGT - 1) / kGT;
+    if (tiles == 0) return TOPS_OK;
+    const int CinK = (Cin + kTK - 1) / kTK * kTK, HDK = (HD + kTK - 1) / kTK * kTK;
+    const size_t lds = (size_t)(CinK + HDK + kTK) * kGRow * sizeof(float);
+    hipFuncSetAttribute((const void*)gate_gen_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((gate_gen_tiled_kernel<T>), dim3((unsigned)tiles), dim3(256), lds, st, (const T*)o, so0, so1,
+                       (const T*)gin, sg0, sg1, (const T*)w_ln, (const T*)b_ln, eps, apply_ln, (const T*)Wg,
+                       (const T*)bg, (const T*)Wo, (const T*)bo, (const T*)res, sr0, sr1, (T*)out, sd0, sd1, M1, M2,
+                       Cin, HD, Cout);
+    return launched(res ? "tops_gate_out_generic_residual" : "tops_gate_out_generic");
+  }
   const int64_t blocks = (M1 * M2 + kGenTok - 1) / kGenTok;
   if (blocks == 0) return TOPS_OK;
   hipLaunchKernelGGL((gate_generic_kernel<T>), dim3((unsigned)blocks), dim3(256),
@@ -545,7 +739,6 @@ __global__ __launch_bounds__(256) void tmu_generic_out_kernel(const T* __restric
 constexpr int kTinTok = 64, kTinRow = kTinTok + 4;    // input phase: tokens per tile, LDS row
 constexpr int kToutTok = 32, kToutRow = kToutTok + 4;  // output phase
 constexpr int kTF = 128, kTFRow = kTF + 4;              // output phase: features per chunk, LDS row
-constexpr int kTK = 32;                                 // k-tile of the staged weights
 
 // LayerNorm of the `ntok` token columns of a k-major LDS tile (4 threads per token, two-pass),
 // rounding the normalised values to T; rows k in [C, CK) are set to zero.
