@@ -741,6 +741,48 @@ def sweep(path, sizes, dev):
             f.flush()
             rows.append(r)
             del x, m, z, pm, pre, w_out, w_in, ts, te
+        # fp32 I/O (every value fp32; the fp32 product on the fp32 MFMA, the tiled any-shape phases
+        # and attention) against the torch formulation in fp32
+        f32 = lambda dd: {k: (v.float() if torch.is_tensor(v) and v.is_floating_point() else v)  # noqa: E731
+                          for k, v in dd.items()}
+        for n in [s for s in sizes if s <= 1024]:
+            torch.cuda.empty_cache()
+            it = 10 if n <= 512 else 3
+            x, m, w = tmu_inputs(n)
+            x, m, w = x.float().to(dev), m.to(dev), {k: v.float().to(dev) for k, v in w.items()}
+            pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+            ms = time_ms(lambda: tops.triangle_mul.forward(x, pre, direction="outgoing", mask=m), it, 2)
+            tms = time_ms(lambda: torch_tmu(x, "outgoing", m, **w), it, 2)
+            rows.append({"op": "triangle_multiplicative_update_fp32", "size": n, "ms": round(ms, 4),
+                         "torch_path_ms": round(tms, 4), "kernels": {}})
+            f.write(json.dumps(rows[-1]) + "\n")
+            del x, m, w, pre
+            torch.cuda.empty_cache()
+            d = to_dev(f32(tri_inputs(n)), dev)
+            pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                                d["B_proj_z"], H, D)
+            ms = time_ms(lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=D**-0.5,
+                                                            W_proj_g=d["W_proj_g"], B_proj_g=None,
+                                                            W_proj_o=d["W_proj_o"], B_proj_o=None), it, 1)
+            tms = time_ms(lambda: torch_tri(d), max(2, it // 3), 1)
+            rows.append({"op": "triangle_attention_fp32", "size": n, "ms": round(ms, 4), "torch_path_ms": round(tms, 4),
+                         "kernels": {}})
+            f.write(json.dumps(rows[-1]) + "\n")
+            del d, pre
+            torch.cuda.empty_cache()
+            d = to_dev(f32(apb_inputs(n)), dev)
+            pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                                 d["B_proj_z"], H, D)
+            ms = time_ms(lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5,
+                                                             W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"],
+                                                             W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"],
+                                                             mask=d["mask"]), it, 2)
+            tms = time_ms(lambda: torch_apb(d), it, 2)
+            rows.append({"op": "attention_pair_bias_fp32", "size": n, "ms": round(ms, 4),
+                         "torch_path_ms": round(tms, 4), "kernels": {}})
+            f.write(json.dumps(rows[-1]) + "\n")
+            f.flush()
+            del d, pre
     return rows
 
 

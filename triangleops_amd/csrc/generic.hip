@@ -377,6 +377,20 @@ __device__ __attribute__((always_inline)) inline void tiled_ln_affine(float* xs,
   }
 }
 
+// Loads the rows of kGT tokens into a k-major tile dst[c][t] (c < C; rows [C, CK) and tokens
+// t >= ntok are zeros): wave w takes tokens w, w + 4, ..., its lanes consecutive channels, and
+// row(t) gives the element offset of token t's row (computed once per token, wave-uniform).
+template <typename T, typename Row>
+__device__ __attribute__((always_inline)) inline void tiled_load_rows(float* dst, const T* __restrict__ src, int C,
+                                                                      int CK, int ntok, Row row) {
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int t = wave; t < kGT; t += 4) {
+    const bool ok = t < ntok;
+    const int64_t r0 = ok ? row(t) : 0;
+    for (int c = lane; c < CK; c += 64) dst[c * kGRow + t] = ok && c < C ? (float)src[r0 + c] : 0.f;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void tri_gen_prep_tiled_kernel(const T* __restrict__ x, int64_t sx0, int64_t sx1,
                                                                 const T* __restrict__ w_ln, const T* __restrict__ b_ln,
@@ -393,17 +407,12 @@ __global__ __launch_bounds__(256) void tri_gen_prep_tiled_kernel(const T* __rest
   const int tid = threadIdx.x;
   const int64_t ntokall = N * N, tok0 = (int64_t)blockIdx.x * kGT;
   const int ntok = (int)(ntokall - tok0 < kGT ? ntokall - tok0 : kGT);
-  for (int e = tid; e < kGT * C; e += 256) {
-    const int t = e / C, c = e % C;
+  tiled_load_rows<T>(xs, x, C, CK, ntok, [=](int t) {
     const int64_t tok = tok0 + t;
-    xs[c * kGRow + t] = t < ntok ? (float)x[(tok / N) * sx0 + (tok % N) * sx1 + c] : 0.f;
-  }
+    return (tok / N) * sx0 + (tok % N) * sx1;
+  });
   __syncthreads();
-  if (apply_ln) {
-    tiled_ln_affine<T>(xs, C, CK, w_ln, b_ln, eps);
-  } else {
-    for (int e = tid; e < (CK - C) * kGT; e += 256) xs[(C + e / kGT) * kGRow + e % kGT] = 0.f;
-  }
+  if (apply_ln) tiled_ln_affine<T>(xs, C, CK, w_ln, b_ln, eps);
   __syncthreads();
   for (int e = tid; e < kGT * C; e += 256) {
     const int t = e / C, c = e % C;
@@ -442,23 +451,16 @@ __global__ __launch_bounds__(256) void gate_gen_tiled_kernel(const T* __restrict
   const int tid = threadIdx.x;
   const int64_t M = M1 * M2, tok0 = (int64_t)blockIdx.x * kGT;
   const int ntok = (int)(M - tok0 < kGT ? M - tok0 : kGT);
-  for (int e = tid; e < kGT * Cin; e += 256) {
-    const int t = e / Cin, c = e % Cin;
+  tiled_load_rows<T>(gs, gin, Cin, CinK, ntok, [=](int t) {
     const int64_t tok = tok0 + t;
-    gs[c * kGRow + t] = t < ntok ? (float)gin[(tok / M2) * sg0 + (tok % M2) * sg1 + c] : 0.f;
-  }
-  for (int e = tid; e < kGT * HD; e += 256) {
-    const int t = e / HD, j = e % HD;
+    return (tok / M2) * sg0 + (tok % M2) * sg1;
+  });
+  tiled_load_rows<T>(ys, o, HD, HDK, ntok, [=](int t) {
     const int64_t tok = tok0 + t;
-    ys[j * kGRow + t] = t < ntok ? (float)o[(tok / M2) * so0 + (tok % M2) * so1 + j] : 0.f;
-  }
-  for (int e = tid; e < (HDK - HD) * kGT; e += 256) ys[(HD + e / kGT) * kGRow + e % kGT] = 0.f;
+    return (tok / M2) * so0 + (tok % M2) * so1;
+  });
   __syncthreads();
-  if (apply_ln) {
-    tiled_ln_affine<T>(gs, Cin, CinK, w_ln, b_ln, eps);
-  } else {
-    for (int e = tid; e < (CinK - Cin) * kGT; e += 256) gs[(Cin + e / kGT) * kGRow + e % kGT] = 0.f;
-  }
+  if (apply_ln) tiled_ln_affine<T>(gs, Cin, CinK, w_ln, b_ln, eps);
   // gate: ys[j][t] = io(o * sigmoid(io(g) . Wg[j] + bg[j])), each element rewritten by the thread that reads it
   tiled_gemm64<T, true>(gs, Cin, CinK, Wg, HD, ws, kGT, [=](int t, int j, float v) {
     const float g = v + (bg ? (float)bg[j] : 0.f);
@@ -477,9 +479,8 @@ static int tri_generic_prep_t(const void* x, int64_t sx0, int64_t sx1, const voi
                               int apply_ln, const void* wqkv, const void* WZ, const float* BZ, void* xln, void* q,
                               void* k, void* v, float* bias, int64_t N, int C, int H, int D, float eps,
                               hipStream_t st) {
-  if (C <= 256) {  // tiled kernel
-    const int64_t tiles = (N * N + kGT - 1) / kGT;
-    if (tiles == 0) return TOPS_OK;
+  const int64_t tiles = (N * N + kGT - 1) / kGT;
+  if (C <= 256 && tiles >= num_cus()) {  // tiled kernel: 64 tokens per block
     const int CK = (C + kTK - 1) / kTK * kTK;
     const size_t lds = (size_t)(CK + kTK) * kGRow * sizeof(float);
     hipFuncSetAttribute((const void*)tri_gen_prep_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -524,9 +525,8 @@ static int gate_generic_t(const void* o, int64_t so0, int64_t so1, const void* g
                           const void* Wo, const void* bo, const void* res, int64_t sr0, int64_t sr1, void* out,
                           int64_t sd0, int64_t sd1, int64_t M1, int64_t M2, int Cin, int HD, int Cout,
                           hipStream_t st) {
-  if (Cin <= 256 && HD <= 256) {  // tiled kernel
-    const int64_t tiles = (M1 * M2 + kGT - 1) / kGT;
-    if (tiles == 0) return TOPS_OK;
+  const int64_t tiles = (M1 * M2 + kGT - 1) / kGT;
+  if (Cin <= 256 && HD <= 256 && tiles >= num_cus()) {  // tiled kernel: 64 tokens per block
     const int CinK = (Cin + kTK - 1) / kTK * kTK, HDK = (HD + kTK - 1) / kTK * kTK;
     const size_t lds = (size_t)(CinK + HDK + kTK) * kGRow * sizeof(float);
     hipFuncSetAttribute((const void*)gate_gen_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -596,16 +596,88 @@ __global__ __launch_bounds__(256) void apb_generic_bias_kernel(const T* __restri
   }
 }
 
+// Tiled apb pre-pass kernels (C_s, C_z <= 256): Q / K / V as a block GEMM over 64 tokens; the
+// pair bias as a LayerNorm of 64 pairs in LDS followed by one thread per (pair, head) dot product.
+template <typename T>
+__global__ __launch_bounds__(256) void apb_gen_qkv_tiled_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
+                                                               T* __restrict__ qo, T* __restrict__ ko,
+                                                               T* __restrict__ vo, int64_t M, int C, int H, int D) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CK = (C + kTK - 1) / kTK * kTK;
+  float* xs = sm;               // [CK][kGRow]  X, k-major
+  float* ws = xs + CK * kGRow;  // [kTK][kGRow]
+  const int tid = threadIdx.x;
+  const int64_t tok0 = (int64_t)blockIdx.x * kGT;
+  const int ntok = (int)(M - tok0 < kGT ? M - tok0 : kGT);
+  tiled_load_rows<T>(xs, X, C, CK, ntok, [=](int t) { return (tok0 + t) * (int64_t)C; });
+  const int HD = H * D;
+  const uint64_t aq = (uint64_t)qo, dk = (uint64_t)ko - aq, dv = (uint64_t)vo - aq;
+  tiled_gemm64<T, false>(xs, C, CK, wqkv, 3 * HD, ws, ntok, [=](int t, int f, float v) {
+    const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+    const uint64_t base = aq + (which == 1 ? dk : 0) + (which == 2 ? dv : 0);
+    reinterpret_cast<T*>(base)[(tok0 + t) * HD + h * D + d] = (T)v;
+  });
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void apb_gen_bias_tiled_kernel(const T* __restrict__ Z, int64_t sz0, int64_t sz1,
+                                                                const float* __restrict__ Wc,
+                                                                const float* __restrict__ Bc, float* __restrict__ bias,
+                                                                int64_t M, int Cz, int H, float eps) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];
+  const int CzK = (Cz + kTK - 1) / kTK * kTK;
+  float* zs = sm;  // [CzK][kGRow]  LN(Z) of 64 pairs, k-major
+  const int tid = threadIdx.x;
+  const int64_t npair = M * M, p0 = (int64_t)blockIdx.x * kGT;
+  const int np = (int)(npair - p0 < kGT ? npair - p0 : kGT);
+  tiled_load_rows<T>(zs, Z, Cz, CzK, np, [=](int t) {
+    const int64_t pr = p0 + t;
+    return (pr / M) * sz0 + (pr % M) * sz1;
+  });
+  __syncthreads();
+  tiled_ln_affine<T>(zs, Cz, CzK, nullptr, nullptr, eps);
+  __syncthreads();
+  for (int e = tid; e < kGT * H; e += 256) {
+    const int t = e % kGT, h = e / kGT;
+    if (t >= np) continue;
+    const float* w = Wc + (int64_t)h * Cz;
+    float acc = Bc[h];
+    for (int c = 0; c < Cz; ++c) acc = fmaf(zs[c * kGRow + t], w[c], acc);
+    bias[(int64_t)h * npair + p0 + t] = acc;
+  }
+}
+
 template <typename T>
 static int apb_generic_prep_t(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
                               const float* Wc, const float* Bc, void* q, void* k, void* v, float* bias, int64_t M,
                               int C, int Cz, int H, int D, float eps, hipStream_t st) {
-  const int64_t b1 = (M * 3 * H * D + 255) / 256, b2 = (M * M + kGenTok - 1) / kGenTok;
-  if (b1 == 0) return TOPS_OK;
-  hipLaunchKernelGGL((apb_generic_qkv_kernel<T>), dim3((unsigned)b1), dim3(256), 0, st, (const T*)X,
-                     (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
-  hipLaunchKernelGGL((apb_generic_bias_kernel<T>), dim3((unsigned)b2), dim3(256), (size_t)kGenTok * Cz * sizeof(float),
-                     st, (const T*)Z, sz0, sz1, Wc, Bc, bias, M, Cz, H, eps);
+  // the tiled kernels take 64 tokens (pairs) per block: used where that still gives every CU a
+  // block (Q / K / V has only M tokens), the per-output kernels otherwise
+  const int64_t t1 = (M + kGT - 1) / kGT, t2 = (M * M + kGT - 1) / kGT;
+  if (t1 == 0) return TOPS_OK;
+  if (C <= 256 && t1 >= num_cus()) {
+    const int CK = (C + kTK - 1) / kTK * kTK;
+    const size_t l1 = (size_t)(CK + kTK) * kGRow * sizeof(float);
+    hipFuncSetAttribute((const void*)apb_gen_qkv_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1);
+    hipLaunchKernelGGL((apb_gen_qkv_tiled_kernel<T>), dim3((unsigned)t1), dim3(256), l1, st, (const T*)X,
+                       (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
+  } else {
+    const int64_t b1 = (M * 3 * H * D + 255) / 256;
+    hipLaunchKernelGGL((apb_generic_qkv_kernel<T>), dim3((unsigned)b1), dim3(256), 0, st, (const T*)X,
+                       (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
+  }
+  if (Cz <= 256 && t2 >= num_cus()) {
+    const int CzK = (Cz + kTK - 1) / kTK * kTK;
+    const size_t l2 = (size_t)CzK * kGRow * sizeof(float);
+    hipFuncSetAttribute((const void*)apb_gen_bias_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)l2);
+    hipLaunchKernelGGL((apb_gen_bias_tiled_kernel<T>), dim3((unsigned)t2), dim3(256), l2, st, (const T*)Z, sz0, sz1, Wc,
+                       Bc, bias, M, Cz, H, eps);
+  } else {
+    const int64_t b2 = (M * M + kGenTok - 1) / kGenTok;
+    hipLaunchKernelGGL((apb_generic_bias_kernel<T>), dim3((unsigned)b2), dim3(256),
+                       (size_t)kGenTok * Cz * sizeof(float), st, (const T*)Z, sz0, sz1, Wc, Bc, bias, M, Cz, H, eps);
+  }
   return launched("tops_apb_generic_prep");
 }
 
