@@ -314,42 +314,78 @@ constexpr int kGT = 64, kGRow = kGT + 4;  // tokens per tile, LDS row of the k-m
 
 // out[t][f] = sum_k a[k][t] * W[f][k] (a: k-major LDS tile of kGT tokens, K valid rows of CK;
 // W: F x K row-major in global memory), handed to epi(t, f, value) for t < ntok, f < F.  With
-// ROUND the activations are rounded to T as the products' operand.
-template <typename T, bool ROUND, typename Epi>
-__device__ __attribute__((always_inline)) inline void tiled_gemm64(const float* a, int K, int CK, const T* __restrict__ W, int F, float* ws,
-                                    int ntok, Epi epi) {
+// ROUND the activations are rounded to T as the products' operand.  The (64-feature chunk,
+// 32-deep k-tile) steps run as one sequence; each step's weights go k-major into LDS (ws: NBUF x
+// kTK x kGRow floats) from registers loaded during the previous step, so the loads' latency
+// overlaps the products.  One block barrier per step with two buffers, two with one (which
+// leaves more LDS for the caller's tiles and more blocks per CU).
+template <typename T, bool ROUND, int NBUF = 2, typename Epi>
+__device__ __attribute__((always_inline)) inline void tiled_gemm64(const float* a, int K, int CK,
+                                                                   const T* __restrict__ W, int F, float* ws,
+                                                                   int ntok, Epi epi) {
   const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  for (int f0 = 0; f0 < F; f0 += 64) {
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < CK; k0 += kTK) {
-      __syncthreads();  // the previous k-tile's weights are consumed
-      for (int e = tid; e < 64 * kTK; e += 256) {
-        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
-        ws[k * kGRow + f] = ff < F && kk < K ? (float)W[(int64_t)ff * K + kk] : 0.f;
-      }
-      __syncthreads();
-#pragma unroll 8
-      for (int k = 0; k < kTK; ++k) {
-        f32x4 x = *reinterpret_cast<const f32x4*>(&a[(k0 + k) * kGRow + 4 * ty]);
-        if constexpr (ROUND) {
+  const int nk = CK / kTK, nsteps = ((F + 63) / 64) * nk;
+  // staging: thread tid moves weights (f, k) = (e / kTK, e % kTK), e = tid + 256 i, i < 8
+  float wr[8];
+  auto wload = [&](int step) __attribute__((always_inline)) {
+    const int f0 = (step / nk) * 64, k0 = (step % nk) * kTK;
 #pragma unroll
-          for (int u = 0; u < 4; ++u) x[u] = (float)(T)x[u];
-        }
-        const f32x4 w = *reinterpret_cast<const f32x4*>(&ws[k * kGRow + 4 * tx]);
+    for (int i = 0; i < 8; ++i) {
+      const int e = tid + 256 * i, ff = f0 + e / kTK, kk = k0 + e % kTK;
+      wr[i] = ff < F && kk < K ? (float)W[(int64_t)ff * K + kk] : 0.f;
+    }
+  };
+  auto wstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(x[u], w[v], acc[u][v]);
+    for (int i = 0; i < 8; ++i) {
+      const int e = tid + 256 * i;
+      ws[(buf * kTK + e % kTK) * kGRow + e / kTK] = wr[i];
+    }
+  };
+  __syncthreads();  // the caller's tile is complete; ws is free
+  wload(0);
+  wstore(0);
+  float acc[4][4] = {};
+  for (int step = 0; step < nsteps; ++step) {
+    if constexpr (NBUF == 1) {
+      if (step > 0) {
+        __syncthreads();  // every thread is done with the previous step's weights
+        wstore(0);
       }
     }
+    __syncthreads();  // this step's buffer is filled (two buffers: the other one is no longer read)
+    if (step + 1 < nsteps) wload(step + 1);
+    const int k0 = (step % nk) * kTK;
+    const float* wb = ws + (NBUF == 1 ? 0 : (step & 1)) * kTK * kGRow;
+#pragma unroll 8
+    for (int k = 0; k < kTK; ++k) {
+      f32x4 x = *reinterpret_cast<const f32x4*>(&a[(k0 + k) * kGRow + 4 * ty]);
+      if constexpr (ROUND) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int t = 4 * ty + u, f = f0 + 4 * tx + v;
-        if (t < ntok && f < F) epi(t, f, acc[u][v]);
+        for (int u = 0; u < 4; ++u) x[u] = (float)(T)x[u];
       }
+      const f32x4 w = *reinterpret_cast<const f32x4*>(&wb[k * kGRow + 4 * tx]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(x[u], w[v], acc[u][v]);
+    }
+    if constexpr (NBUF == 2) {
+      if (step + 1 < nsteps) wstore((step + 1) & 1);
+    }
+    if (step % nk == nk - 1) {  // the chunk's last k-tile: epilogue, fresh accumulators
+      const int f0 = (step / nk) * 64;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = 4 * ty + u, f = f0 + 4 * tx + v;
+          if (t < ntok && f < F) epi(t, f, acc[u][v]);
+          acc[u][v] = 0.f;
+        }
+    }
   }
+  __syncthreads();  // ws and the caller's tile may be reused after return
 }
 
 // LayerNorm (optionally with the affine w, b) of the kGT token columns of a k-major tile, in place
@@ -378,16 +414,33 @@ __device__ __attribute__((always_inline)) inline void tiled_ln_affine(float* xs,
 }
 
 // Loads the rows of kGT tokens into a k-major tile dst[c][t] (c < C; rows [C, CK) and tokens
-// t >= ntok are zeros): wave w takes tokens w, w + 4, ..., its lanes consecutive channels, and
-// row(t) gives the element offset of token t's row (computed once per token, wave-uniform).
+// t >= ntok are zeros; CK <= 256): wave w takes tokens w, w + 4, ..., its lanes consecutive
+// channels, and row(t) gives the element offset of token t's row (once per token, wave-uniform).
+// Four tokens' loads are issued before their LDS stores, so their latencies overlap.
 template <typename T, typename Row>
 __device__ __attribute__((always_inline)) inline void tiled_load_rows(float* dst, const T* __restrict__ src, int C,
                                                                       int CK, int ntok, Row row) {
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int t = wave; t < kGT; t += 4) {
-    const bool ok = t < ntok;
-    const int64_t r0 = ok ? row(t) : 0;
-    for (int c = lane; c < CK; c += 64) dst[c * kGRow + t] = ok && c < C ? (float)src[r0 + c] : 0.f;
+  for (int t0 = wave; t0 < kGT; t0 += 16) {
+    float v[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int t = t0 + 4 * a;
+      const bool ok = t < ntok;
+      const int64_t r0 = ok ? row(t) : 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int c = lane + 64 * b;
+        v[a][b] = ok && c < C ? (float)src[r0 + c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int c = lane + 64 * b;
+        if (c < CK) dst[c * kGRow + t0 + 4 * a] = v[a][b];
+      }
   }
 }
 
@@ -403,7 +456,7 @@ __global__ __launch_bounds__(256) void tri_gen_prep_tiled_kernel(const T* __rest
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int CK = (C + kTK - 1) / kTK * kTK;
   float* xs = sm;                  // [CK][kGRow]  (LN(x)), k-major
-  float* ws = xs + CK * kGRow;     // [kTK][kGRow] staged weights
+  float* ws = xs + CK * kGRow;     // [2][kTK][kGRow] staged weights
   const int tid = threadIdx.x;
   const int64_t ntokall = N * N, tok0 = (int64_t)blockIdx.x * kGT;
   const int ntok = (int)(ntokall - tok0 < kGT ? ntokall - tok0 : kGT);
@@ -462,12 +515,12 @@ __global__ __launch_bounds__(256) void gate_gen_tiled_kernel(const T* __restrict
   __syncthreads();
   if (apply_ln) tiled_ln_affine<T>(gs, Cin, CinK, w_ln, b_ln, eps);
   // gate: ys[j][t] = io(o * sigmoid(io(g) . Wg[j] + bg[j])), each element rewritten by the thread that reads it
-  tiled_gemm64<T, true>(gs, Cin, CinK, Wg, HD, ws, kGT, [=](int t, int j, float v) {
+  tiled_gemm64<T, true, 1>(gs, Cin, CinK, Wg, HD, ws, kGT, [=](int t, int j, float v) {
     const float g = v + (bg ? (float)bg[j] : 0.f);
     ys[j * kGRow + t] = (float)(T)(ys[j * kGRow + t] * sigmoid(g));
   });
   // output projection of the gated tile; with a residual, the result is rounded first
-  tiled_gemm64<T, false>(ys, HD, HDK, Wo, Cout, ws, ntok, [=](int t, int c, float v) {
+  tiled_gemm64<T, false, 1>(ys, HD, HDK, Wo, Cout, ws, ntok, [=](int t, int c, float v) {
     const T r = (T)(v + (bo ? (float)bo[c] : 0.f));
     const int64_t tok = tok0 + t, m1 = tok / M2, m2 = tok % M2;
     out[m1 * sd0 + m2 * sd1 + c] = res ? (T)((float)res[m1 * sr0 + m2 * sr1 + c] + (float)r) : r;
@@ -482,7 +535,7 @@ static int tri_generic_prep_t(const void* x, int64_t sx0, int64_t sx1, const voi
   const int64_t tiles = (N * N + kGT - 1) / kGT;
   if (C <= 256 && tiles >= num_cus()) {  // tiled kernel: 64 tokens per block
     const int CK = (C + kTK - 1) / kTK * kTK;
-    const size_t lds = (size_t)(CK + kTK) * kGRow * sizeof(float);
+    const size_t lds = (size_t)(CK + 2 * kTK) * kGRow * sizeof(float);
     hipFuncSetAttribute((const void*)tri_gen_prep_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
                         (int)lds);
     hipLaunchKernelGGL((tri_gen_prep_tiled_kernel<T>), dim3((unsigned)tiles), dim3(256), lds, st, (const T*)x, sx0, sx1,
@@ -596,8 +649,9 @@ __global__ __launch_bounds__(256) void apb_generic_bias_kernel(const T* __restri
   }
 }
 
-// Tiled apb pre-pass kernels (C_s, C_z <= 256): Q / K / V as a block GEMM over 64 tokens; the
-// pair bias as a LayerNorm of 64 pairs in LDS followed by one thread per (pair, head) dot product.
+// Tiled apb pre-pass kernels (C_s, C_z <= 256): Q / K / V as a block GEMM over 64 tokens and 64
+// weight rows; the pair bias as a LayerNorm of 64 pairs in LDS, then per head (one wave each) the
+// dot products of its 64 pairs (lanes) with the head's weights (wave-uniform: scalar loads).
 template <typename T>
 __global__ __launch_bounds__(256) void apb_gen_qkv_tiled_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
                                                                T* __restrict__ qo, T* __restrict__ ko,
@@ -605,15 +659,17 @@ __global__ __launch_bounds__(256) void apb_gen_qkv_tiled_kernel(const T* __restr
   extern __shared__ __attribute__((aligned(16))) float sm[];
   const int CK = (C + kTK - 1) / kTK * kTK;
   float* xs = sm;               // [CK][kGRow]  X, k-major
-  float* ws = xs + CK * kGRow;  // [kTK][kGRow]
+  float* ws = xs + CK * kGRow;  // [2][kTK][kGRow]
   const int tid = threadIdx.x;
   const int64_t tok0 = (int64_t)blockIdx.x * kGT;
   const int ntok = (int)(M - tok0 < kGT ? M - tok0 : kGT);
   tiled_load_rows<T>(xs, X, C, CK, ntok, [=](int t) { return (tok0 + t) * (int64_t)C; });
   const int HD = H * D;
   const uint64_t aq = (uint64_t)qo, dk = (uint64_t)ko - aq, dv = (uint64_t)vo - aq;
-  tiled_gemm64<T, false>(xs, C, CK, wqkv, 3 * HD, ws, ntok, [=](int t, int f, float v) {
-    const int h = f / (3 * D), which = (f / D) % 3, d = f % D;
+  // this block's 64 weight rows (blockIdx.y): more blocks than tokens / 64 alone would give
+  const int fb = 64 * (int)blockIdx.y, nf = 3 * HD - fb < 64 ? 3 * HD - fb : 64;
+  tiled_gemm64<T, false>(xs, C, CK, wqkv + (int64_t)fb * C, nf, ws, ntok, [=](int t, int fl, float v) {
+    const int f = fb + fl, h = f / (3 * D), which = (f / D) % 3, d = f % D;
     const uint64_t base = aq + (which == 1 ? dk : 0) + (which == 2 ? dv : 0);
     reinterpret_cast<T*>(base)[(tok0 + t) * HD + h * D + d] = (T)v;
   });
@@ -637,13 +693,16 @@ __global__ __launch_bounds__(256) void apb_gen_bias_tiled_kernel(const T* __rest
   __syncthreads();
   tiled_ln_affine<T>(zs, Cz, CzK, nullptr, nullptr, eps);
   __syncthreads();
-  for (int e = tid; e < kGT * H; e += 256) {
-    const int t = e % kGT, h = e / kGT;
-    if (t >= np) continue;
+  const int lane = tid & 63;
+  for (int h = __builtin_amdgcn_readfirstlane(tid >> 6); h < H; h += 4) {
     const float* w = Wc + (int64_t)h * Cz;
-    float acc = Bc[h];
-    for (int c = 0; c < Cz; ++c) acc = fmaf(zs[c * kGRow + t], w[c], acc);
-    bias[(int64_t)h * npair + p0 + t] = acc;
+    float acc[4] = {Bc[h], 0.f, 0.f, 0.f};
+    int c = 0;
+    for (; c + 4 <= Cz; c += 4)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = fmaf(zs[(c + j) * kGRow + lane], w[c + j], acc[j]);
+    for (; c < Cz; ++c) acc[0] = fmaf(zs[c * kGRow + lane], w[c], acc[0]);
+    if (lane < np) bias[(int64_t)h * npair + p0 + lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
 }
 
@@ -651,16 +710,15 @@ template <typename T>
 static int apb_generic_prep_t(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
                               const float* Wc, const float* Bc, void* q, void* k, void* v, float* bias, int64_t M,
                               int C, int Cz, int H, int D, float eps, hipStream_t st) {
-  // the tiled kernels take 64 tokens (pairs) per block: used where that still gives every CU a
-  // block (Q / K / V has only M tokens), the per-output kernels otherwise
+  // the tiled bias kernel takes 64 pairs per block: used where that still gives every CU a block
   const int64_t t1 = (M + kGT - 1) / kGT, t2 = (M * M + kGT - 1) / kGT;
   if (t1 == 0) return TOPS_OK;
-  if (C <= 256 && t1 >= num_cus()) {
+  if (C <= 256) {
     const int CK = (C + kTK - 1) / kTK * kTK;
-    const size_t l1 = (size_t)(CK + kTK) * kGRow * sizeof(float);
+    const size_t l1 = (size_t)(CK + 2 * kTK) * kGRow * sizeof(float);
     hipFuncSetAttribute((const void*)apb_gen_qkv_tiled_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)l1);
-    hipLaunchKernelGGL((apb_gen_qkv_tiled_kernel<T>), dim3((unsigned)t1), dim3(256), l1, st, (const T*)X,
-                       (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
+    hipLaunchKernelGGL((apb_gen_qkv_tiled_kernel<T>), dim3((unsigned)t1, (unsigned)((3 * H * D + 63) / 64)), dim3(256),
+                       l1, st, (const T*)X, (const T*)wqkv, (T*)q, (T*)k, (T*)v, M, C, H, D);
   } else {
     const int64_t b1 = (M * 3 * H * D + 255) / 256;
     hipLaunchKernelGGL((apb_generic_qkv_kernel<T>), dim3((unsigned)b1), dim3(256), 0, st, (const T*)X,
