@@ -918,40 +918,60 @@ __global__ __launch_bounds__(256) void tmu_gen_in_tiled_kernel(const T* __restri
 
   const int ty = tid >> 4, tx = tid & 15;  // tokens 4 ty .. + 3, chunk features 4 tx .. + 3
   T* abt = ab + (b * L + r) * ld + c0 + 4 * ty;
-  for (int f0 = 0; f0 < Cout; f0 += 64) {
-    float ap[4][4] = {}, ag[4][4] = {};
-    for (int k0 = 0; k0 < CK; k0 += kTK) {
-      __syncthreads();  // the previous k-tile's weights are consumed (first time: the tile is normalised)
-      for (int e = tid; e < 64 * kTK; e += 256) {
-        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
-        const bool ok = ff < Cout && kk < C;
-        wps[k * kTinRow + f] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
-        wgs[k * kTinRow + f] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
-      }
-      __syncthreads();
-#pragma unroll 8
-      for (int k = 0; k < kTK; ++k) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kTinRow + 4 * ty]);
-        const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTinRow + 4 * tx]);
-        const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTinRow + 4 * tx]);
+  // (64-feature chunk, 32-deep k-tile) steps in one sequence; each step's P and G weights are
+  // loaded into registers during the previous step and stored k-major into LDS after a barrier
+  const int nk = CK / kTK, nsteps = ((Cout + 63) / 64) * nk;
+  float wr[16];  // P (0-7) and G (8-15) weights (f, k) = (e / kTK, e % kTK), e = tid + 256 i
+  auto wload = [&](int step) __attribute__((always_inline)) {
+    const int f0 = (step / nk) * 64, k0 = (step % nk) * kTK;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
-            ag[u][v] = fmaf(a[u], wg[v], ag[u][v]);
-          }
-      }
+    for (int i = 0; i < 8; ++i) {
+      const int e = tid + 256 * i, ff = f0 + e / kTK, kk = k0 + e % kTK;
+      const bool ok = ff < Cout && kk < C;
+      wr[i] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
+      wr[8 + i] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
     }
+  };
+  wload(0);
+  float ap[4][4] = {}, ag[4][4] = {};
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();  // the previous step's weights are consumed (step 0: the tile is normalised)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = tid + 256 * i;
+      wps[(e % kTK) * kTinRow + e / kTK] = wr[i];
+      wgs[(e % kTK) * kTinRow + e / kTK] = wr[8 + i];
+    }
+    __syncthreads();
+    if (step + 1 < nsteps) wload(step + 1);
+    const int k0 = (step % nk) * kTK;
+#pragma unroll 8
+    for (int k = 0; k < kTK; ++k) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kTinRow + 4 * ty]);
+      const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTinRow + 4 * tx]);
+      const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTinRow + 4 * tx]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
+          ag[u][v] = fmaf(a[u], wg[v], ag[u][v]);
+        }
+    }
+    if (step % nk != nk - 1) continue;
+    const int f0 = (step / nk) * 64;  // the chunk's last k-tile: bias, gate, mask, store
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int f = f0 + 4 * tx + v;
-      if (f >= Cout) break;
-      const float bp = Bp[f], bg = Bg[f];
-      vec<T, 4> o;
+      if (f < Cout) {
+        const float bp = Bp[f], bg = Bg[f];
+        vec<T, 4> o;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) o[u] = (T)((ap[u][v] + bp) * sigmoid(ag[u][v] + bg) * msk[4 * ty + u]);
-      *reinterpret_cast<vec<T, 4>*>(abt + (int64_t)f * fstride) = o;
+        for (int u = 0; u < 4; ++u) o[u] = (T)((ap[u][v] + bp) * sigmoid(ag[u][v] + bg) * msk[4 * ty + u]);
+        *reinterpret_cast<vec<T, 4>*>(abt + (int64_t)f * fstride) = o;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ap[u][v] = ag[u][v] = 0.f;
     }
   }
 }
@@ -986,43 +1006,60 @@ __global__ __launch_bounds__(256) void tmu_gen_out_tiled_kernel(const T* __restr
   tiled_layer_norm<T>(xs, kToutRow, kToutTok, C, CK, eps);
 
   const int ty = tid >> 5, tx = tid & 31;  // tokens 4 ty .. + 3, chunk features 4 tx .. + 3
-  for (int f0 = 0; f0 < Cout; f0 += kTF) {
-    float ap[4][4] = {}, ag[4][4] = {};
-    for (int k0 = 0; k0 < CK; k0 += kTK) {
-      __syncthreads();
-      for (int e = tid; e < kTF * kTK; e += 256) {
-        const int f = e / kTK, k = e % kTK, ff = f0 + f, kk = k0 + k;
-        const bool ok = ff < Cout && kk < C;
-        wps[k * kTFRow + f] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
-        wgs[k * kTFRow + f] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
-      }
-      __syncthreads();
-#pragma unroll 8
-      for (int k = 0; k < kTK; ++k) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(&ys[(k0 + k) * kToutRow + 4 * ty]);
-        const f32x4 g = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kToutRow + 4 * ty]);
-        const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTFRow + 4 * tx]);
-        const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTFRow + 4 * tx]);
+  // (128-feature chunk, 32-deep k-tile) steps in one sequence, weights prefetched into registers
+  const int nk = CK / kTK, nsteps = ((Cout + kTF - 1) / kTF) * nk;
+  float wr[32];  // P (0-15) and G (16-31) weights (f, k) = (e / kTK, e % kTK), e = tid + 256 i
+  auto wload = [&](int step) __attribute__((always_inline)) {
+    const int f0 = (step / nk) * kTF, k0 = (step % nk) * kTK;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
-            ag[u][v] = fmaf(g[u], wg[v], ag[u][v]);
-          }
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int e = tid + 256 * i, ff = f0 + e / kTK, kk = k0 + e % kTK;
+      const bool ok = ff < Cout && kk < C;
+      wr[i] = ok ? (float)Wp[(int64_t)ff * C + kk] : 0.f;
+      wr[16 + i] = ok ? (float)Wg[(int64_t)ff * C + kk] : 0.f;
     }
+  };
+  wload(0);
+  float ap[4][4] = {}, ag[4][4] = {};
+  for (int step = 0; step < nsteps; ++step) {
+    __syncthreads();  // the previous step's weights are consumed (step 0: the tiles are normalised)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = tid + 256 * i;
+      wps[(e % kTK) * kTFRow + e / kTK] = wr[i];
+      wgs[(e % kTK) * kTFRow + e / kTK] = wr[16 + i];
+    }
+    __syncthreads();
+    if (step + 1 < nsteps) wload(step + 1);
+    const int k0 = (step % nk) * kTK;
+#pragma unroll 8
+    for (int k = 0; k < kTK; ++k) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&ys[(k0 + k) * kToutRow + 4 * ty]);
+      const f32x4 g = *reinterpret_cast<const f32x4*>(&xs[(k0 + k) * kToutRow + 4 * ty]);
+      const f32x4 wp = *reinterpret_cast<const f32x4*>(&wps[k * kTFRow + 4 * tx]);
+      const f32x4 wg = *reinterpret_cast<const f32x4*>(&wgs[k * kTFRow + 4 * tx]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          ap[u][v] = fmaf(a[u], wp[v], ap[u][v]);
+          ag[u][v] = fmaf(g[u], wg[v], ag[u][v]);
+        }
+    }
+    if (step % nk != nk - 1) continue;
+    const int f0 = (step / nk) * kTF;  // the chunk's last k-tile: bias, gate, residual, store
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * ty + u;
-      if (t >= ntok) break;
       const int64_t o = (bi * L + j0 + t) * Cout;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int f = f0 + 4 * tx + v;
-        if (f >= Cout) break;
-        const T rv = (T)((ap[u][v] + Bp[f]) * sigmoid(ag[u][v] + Bg[f]));
-        out[o + f] = res ? (T)((float)res[o + f] + (float)rv) : rv;
+        if (t < ntok && f < Cout) {
+          const T rv = (T)((ap[u][v] + Bp[f]) * sigmoid(ag[u][v] + Bg[f]));
+          out[o + f] = res ? (T)((float)res[o + f] + (float)rv) : rv;
+        }
+        ap[u][v] = ag[u][v] = 0.f;
       }
     }
   }
