@@ -395,6 +395,16 @@ def test_tri_large_n_kernel(device, N, mask):
     _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} mask={mask}")
 
 
+@pytest.mark.parametrize("N,mask", [(2100, "random"), (2049, "pad")])
+def test_tri_eight_wave_blocks(device, N, mask):
+    """From N = 2048 on the attention runs 8-wave blocks of 512 queries: ragged N (the last block's
+    query tiles lie partly or wholly past N), sampled rows and query columns across the last block."""
+    inp = tri_inputs(N, seed=N + 3, mask=mask, bias_z=True)
+    out = _tri_call(inp, device)
+    rows = torch.tensor([0, N // 2, N - N // 10 - 1, N - 1])
+    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri 8-wave N={N} mask={mask}")
+
+
 @pytest.mark.parametrize("masked", [False, True])
 def test_tri_apo_d16(device, masked):
     """The Apo shape of the reference's tests/test_triangle_attn.py:137-192 (N=33, H=4, D=16, C_in=64)

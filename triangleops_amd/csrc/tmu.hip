@@ -911,7 +911,12 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
   }
   __syncthreads();  // cst
 
-  auto yswz = [](int t) { return (t ^ (t >> 3)) & 7; };
+  // 16-byte chunk swizzle of a ys row (16 chunks): distinct over any 16 consecutive tokens of an
+  // aligned group of 16 (the writers' operand and statistics reads), and distinct in its top three
+  // bits over the tokens 8 g + e, g < 8 (the loaders' 8-byte transposed stores, 32 lanes at a
+  // time), so neither access pattern puts two lanes of a group on one LDS bank.  (A 3-bit swizzle
+  // gave both patterns 2-way conflicts.)
+  auto yswz = [](int t) { return (t & 15) ^ ((t >> 3) & 14); };
   const uint32_t G = gridDim.x;
   uint32_t t = blockIdx.x;
   if (wave < 4) {

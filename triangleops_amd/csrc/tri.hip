@@ -38,6 +38,9 @@ constexpr int kMaxN = 16384;    // largest N of the tuned kernels (per-row key-b
 constexpr int kMaxKB = kMaxN / 64;
 
 // The pre-pass buffers' key stride: N rounded up to a multiple of 64 (at least 64).
+#ifndef TRI_NW8_MIN_N
+#define TRI_NW8_MIN_N 2048  // from this N on, 8-wave attention blocks (half the KV block copies per query)
+#endif
 static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 * 64; }
 
 // ---------------------------------------------------------------------------------------------
@@ -259,8 +262,9 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 }
 
 // ---------------------------------------------------------------------------------------------
-// Attention core.  4 waves, QT query tiles (32 queries) per wave, 64-key blocks of two 32-key
-// tiles.
+// Attention core.  NW waves (4, two blocks per CU; or 8 from N = TRI_NW8_MIN_N on, one block per
+// CU: each KV block copied into LDS then serves twice the queries), QT query tiles (32 queries)
+// per wave, 64-key blocks of two 32-key tiles.  Both block sizes give the same bits.
 //
 // Per (32-key tile, query tile) a wave runs
 //     S^T  = C0 + I . bias^T          2 MFMAs, A = identity, B = 16 bias bytes per lane
@@ -288,13 +292,15 @@ constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
-template <typename T, int QT>
-__global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
+template <typename T, int QT, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
                                                          int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
                                                          int64_t so1, int64_t N, int64_t ldn, int H, int nqc,
                                                          int dv) {
-  constexpr int D = 32, NW = 4;
+  constexpr int D = 32;
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves per block");
+  constexpr int KVR = 8 / NW;  // 16-byte chunks of a KV block per thread
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
 
@@ -337,16 +343,20 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
     bq[t] = bias + ((int64_t)h * nqt + q / 32) * (2 * nkb) * 1024 + (32 * hl + q % 32) * 8;
   }
 
-  // KV block copy: thread t moves 16-byte chunks t (K: row t / 4) and 256 + t (V^T: row t / 8);
-  // each load instruction of a wave reads 1 KB contiguous.
+  // KV block copy (8 KiB: 256 chunks of K, then 256 of V^T, 16 bytes each): with 4 waves thread t
+  // moves chunks t (K: row t / 4) and 256 + t (V^T: row t / 8); with 8 waves, chunk t (waves 0-3
+  // K, waves 4-7 V^T).  Each load instruction of a wave reads 1 KB contiguous.
   auto kv_load = [&](int kb, V8* r) {
     const T* src = kvrow + (int64_t)kb * kKVBlock + 8 * tid;
     r[0] = ldg<V8>(src);
-    r[1] = ldg<V8>(src + 64 * D);
+    if constexpr (KVR == 2) r[1] = ldg<V8>(src + 64 * D);
   };
   auto kv_store = [&](int buf, const V8* r) {
-    *reinterpret_cast<V8*>(&kvs[buf][(tid / 4) * kKPad + 8 * (tid % 4)]) = r[0];
-    *reinterpret_cast<V8*>(&kvs[buf][64 * kKPad + (tid / 8) * kVPad + 8 * (tid % 8)]) = r[1];
+    if (KVR == 2 || tid < 256)  // wave-uniform
+      *reinterpret_cast<V8*>(&kvs[buf][(tid / 4) * kKPad + 8 * (tid % 4)]) = r[0];
+    const int tv = KVR == 2 ? tid : tid - 256;  // V^T chunk of this thread
+    if (KVR == 2 || tid >= 256)
+      *reinterpret_cast<V8*>(&kvs[buf][64 * kKPad + (tv / 8) * kVPad + 8 * (tv % 8)]) = r[KVR - 1];
   };
   // bias B operands of one 32-key tile: [query tile t][half j], 16 bytes per lane
   auto load_bias = [&](int kb, int kt, V8 (*bb)[2]) {
@@ -358,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn_kernel(const T* __restrict__ 
   // The first visited block is block 0 unless all its keys are masked: its KV and bias operands
   // are loaded now, speculatively, and reloaded below in the rare other case.
   V8 bA[QT][2], bB[QT][2];
-  V8 kvA[2], kvB[2];
+  V8 kvA[KVR], kvB[KVR];
   kv_load(0, kvA);
   load_bias(0, 0, bA);
   load_bias(0, 1, bB);
@@ -1041,18 +1051,21 @@ static int tri_attention_t(const void* Qp, const void* KV, const void* bias, con
   }
 #endif
   const int qt = N <= 128 ? 1 : 2;
-  const int64_t per_block = 4 * 32 * qt;
+  const int nw = N >= TRI_NW8_MIN_N ? 8 : 4;  // waves (query tiles of 32 x qt) per block
+  const int64_t per_block = nw * 32 * qt;
   const int nqc = (int)((N + per_block - 1) / per_block);
   const int64_t grid = N * H * nqc;
   if (grid == 0) return TOPS_OK;
-#define TOPS_TRI(QTV)                                                                                     \
-  hipLaunchKernelGGL((tri_attn_kernel<T, QTV>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Qp,      \
-                     (const T*)KV, (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, ldn, \
+#define TOPS_TRI(QTV, NWV)                                                                                    \
+  hipLaunchKernelGGL((tri_attn_kernel<T, QTV, NWV>), dim3((unsigned)grid), dim3(64 * NWV), 0, st, (const T*)Qp, \
+                     (const T*)KV, (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, N, ldn,     \
                      (int)H, nqc, (int)dv)
   if (qt == 1)
-    TOPS_TRI(1);
+    TOPS_TRI(1, 4);
+  else if (nw == 4)
+    TOPS_TRI(2, 4);
   else
-    TOPS_TRI(2);
+    TOPS_TRI(2, 8);
 #undef TOPS_TRI
   return launched("tops_tri_attention");
 }
