@@ -43,6 +43,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 import triangleops_amd as tops  # noqa: E402
+from triangleops_amd import _native  # noqa: E402
 from triangleops_amd.attn_pair_bias.kernel import apb_forward_qkv, apb_qkn_prep  # noqa: E402
 from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, prep_forward  # noqa: E402
 from triangleops_amd.triangle_mul.kernel import input_phase, output_phase, triangle_einsum  # noqa: E402
@@ -393,32 +394,44 @@ def tri_work(N, c=C, h=H, dh=D):
 
 
 def apb_phases(d, pre):
-    """apb_forward's two halves as forward() runs them: the Q / K / V pre-pass (apb_qkv_kernel, which
-    tops_apb_qkn_prep runs at the tuned shape without a Q bias or qk-norm, exactly as
-    tops_apb_forward does), then the attention kernel with its split-key combine; then the gate."""
+    """forward()'s three launches at the tuned shape (tops_apb_forward_gated), each as its own call on
+    the same workspace layout: the Q / K / V pre-pass (apb_qkv_kernel, which tops_apb_qkn_prep runs
+    at the tuned shape without a Q bias or qk-norm, exactly as the fused call does), the attention
+    kernel alone (tops_apb_forward_qkv with Og = NULL leaves the split partials in the workspace),
+    then the split merge fused with the gate and W_o (tops_apb_merge_gate)."""
     st = {}
     M = d["X"].shape[0]
-    og = torch.empty(M, H * D, device=d["X"].device, dtype=d["X"].dtype)
+    dev, dt = d["X"].device, d["X"].dtype
     m8 = d["mask"].view(torch.int8) if d["mask"].dtype == torch.bool else d["mask"]
+    work = torch.empty(max(_native.apb_workspace_bytes(M, H, D), 1), device=dev, dtype=torch.uint8)
+    Wc, sWc, Bc = (pre[k].float().contiguous() for k in ("W_combined", "sum_W_combined", "B_const"))
+    wg, bg, wo, bo = (d[k].to(dt).contiguous() for k in ("W_proj_g", "B_proj_g", "W_proj_o", "B_proj_o"))
+    out = torch.empty(M, C, device=dev, dtype=dt)
+    code = 1 if dt == torch.float16 else 2
 
     def p_qkv():
         st["qkv"] = apb_qkn_prep(d["X"], pre["wqkv_hm"], None, None, qscale=D**-0.5)
 
     def p_att():
-        apb_forward_qkv(*st["qkv"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], og,
-                        scale=1.0, mask=m8)
+        q, k, v = st["qkv"]
+        _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), d["Z"].data_ptr(),
+                     d["Z"].stride(0), d["Z"].stride(1), Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), m8.data_ptr(),
+                     None, work.data_ptr(), M, H * D, C, H, D, 1.0, 1e-5, code, _native.stream_of(q))
 
-    def p_gate():
-        st["out"] = gate_out_forward(og.view(M, 1, H * D), d["X"], d["W_proj_g"], d["B_proj_g"],
-                                     d["W_proj_o"], d["B_proj_o"])
+    def p_mg():
+        _native.call("tops_apb_merge_gate", work.data_ptr(), d["X"].data_ptr(), wg.data_ptr(), bg.data_ptr(),
+                     wo.data_ptr(), bo.data_ptr(), None, out.data_ptr(), M, H, D, code, _native.stream_of(out))
+        st["out"] = out
 
-    return [p_qkv, p_att, p_gate]
+    return [p_qkv, p_att, p_mg]
 
 
 def apb_work(M):
-    """apb_attention: Z read once (2 M^2 C bytes); the phase is apb_attn_kernel + apb_combine_kernel."""
+    """apb_attention: Z read once (2 M^2 C bytes) by apb_attn_kernel; apb_merge_gate reads the split
+    partials (nsplit M H (D + 2) fp32) and X and writes the output."""
+    part = _native.apb_workspace_bytes(M, H, D) - ((3 * M * H * D * 2 + 255) // 256 * 256)
     return {"apb_qkv": ("hbm", 2 * M * C + 3 * 2 * M * H * D), "apb_attention": ("hbm", 2 * M * M * C),
-            "apb_gate_out": ("hbm", 3 * 2 * M * C)}
+            "apb_merge_gate": ("hbm", part + 2 * 2 * M * C)}
 
 
 def apb_qkn_phases(d, pre, p):
@@ -580,7 +593,7 @@ def op_entry_apb(M, dev, iters, warmup, cpu):
     ka = kern["apb_attention"]
     e = {"config": f"attention_pair_bias bf16, M={M}, H={H}, D={D}, C_s=C_z={C}, key mask (last 5% padded)",
          "ms_per_call": round(ms, 4), "calls_per_s": round(1e3 / ms, 2),
-         "roofline": {"kernel": "apb_attention (apb_attn_kernel + its split-key apb_combine_kernel)", "bound": "hbm", "achieved": ka["achieved"], "peak": ka["peak"],
+         "roofline": {"kernel": "apb_attention (apb_attn_kernel)", "bound": "hbm", "achieved": ka["achieved"], "peak": ka["peak"],
                       "unit": ka["unit"], "frac": ka["frac"], "traffic": None},
          "kernels": kern}
     e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)

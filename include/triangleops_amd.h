@@ -184,12 +184,46 @@ int tops_gate_out_generic_residual(const void* o, int64_t so0, int64_t so1, cons
  *   mask   int8 (M,) key mask (nonzero = valid) or NULL; masked keys get -inf
  *   Og     io   (M, H*D) contiguous: softmax_k(scale * Q.K + LN(Z[q,k]) . W + b) V
  *   work   device scratch of tops_apb_workspace_bytes(M, H, D) bytes (caller-owned): the
- *          projected Q / K / V (3 * M * 128 * 2 bytes) and the split partials
+ *          projected Q / K / V (3 * M * 128 * 2 bytes, rounded up to 256) and the split partials
+ * Og may be NULL when the keys are split (tops_apb_workspace_bytes exceeds the Q / K / V region):
+ * the attention's fp32 split partials then stay in `work` right after Q / K / V, the input of
+ * tops_apb_merge_gate.
  */
 int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D);
 int tops_apb_forward(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
                      const float* sWc, const float* Bc, const void* mask, void* Og, void* work, int64_t M, int64_t C,
                      int64_t Cz, int64_t H, int64_t D, float scale, float eps, int dtype, void* stream);
+
+/*
+ * attention_pair_bias forward with the gate and output projection fused after the attention:
+ * replaces `apb_forward` followed by attn_pair_bias/module.py:69-70
+ *   out = ((Og * sigmoid(X . Wg^T + bg)) -> io) . Wo^T + bo   (+ res when res != NULL)
+ * with Og as tops_apb_forward computes it (same bits).  Same arguments as tops_apb_forward plus
+ *   Wg, Wo io (128, 128) nn.Linear (out, in) weights;  bg, bo io (128,) or NULL (zero)
+ *   res    io (M, 128) contiguous or NULL: the residual added before the single rounding
+ *   out    io (M, 128) contiguous
+ *   work   tops_apb_gated_workspace_bytes(M, H, D) bytes (Q / K / V, then the split partials,
+ *          or Og when the keys are not split)
+ * C == Cz == C_out == 128, H == 4, D == 32, 16-bit I/O.  With split keys the split merge, gate and
+ * output projection are one kernel (apb_merge_gate_kernel), otherwise tops_gate_out runs.
+ */
+int64_t tops_apb_gated_workspace_bytes(int64_t M, int64_t H, int64_t D);
+int tops_apb_forward_gated(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1, const float* Wc,
+                           const float* sWc, const float* Bc, const void* mask, const void* Wg, const void* bg,
+                           const void* Wo, const void* bo, const void* res, void* out, void* work, int64_t M,
+                           int64_t C, int64_t Cz, int64_t H, int64_t D, int64_t Cout, float scale, float eps,
+                           int dtype, void* stream);
+
+/*
+ * The last launch of tops_apb_forward_gated on its own (no separate counterpart in the reference:
+ * the split merge of the attention's partials, then attn_pair_bias/module.py:69-70's gate and W_o):
+ * part = the fp32 split partials as the attention left them (tops_apb_forward_qkv with Og == NULL
+ * leaves them at the head of its `work`), X / Wg / bg / Wo / bo / res / out as in
+ * tops_apb_forward_gated.  Only for M whose keys are split (TOPS_EINVAL otherwise).
+ */
+int tops_apb_merge_gate(const float* part, const void* X, const void* Wg, const void* bg, const void* Wo,
+                        const void* bo, const void* res, void* out, int64_t M, int64_t H, int64_t D, int dtype,
+                        void* stream);
 
 /*
  * tops_apb_forward without allocation: no counterpart in the reference.  For callers that cannot
@@ -225,7 +259,9 @@ int tops_apb_forward_noalloc(const void* X, const void* wqkv, const void* Z, int
  *               one rounding)
  * tops_apb_forward_qkv, the tuned shape (H*D == Cz == 128, H == 4, D == 32), bf16 / fp16: as
  *   tops_apb_forward with Q, K, V (M, H*D) contiguous taken as they are: Og = softmax_k(scale *
- *   q.k + LN(Z[q,k]) . W + b, masked keys -inf) v;  work as for tops_apb_forward.
+ *   q.k + LN(Z[q,k]) . W + b, masked keys -inf) v;  work as for tops_apb_forward.  With Og == NULL
+ *   (only for M whose keys are split) the attention kernel runs alone and leaves its fp32 split
+ *   partials at the head of `work` (the input of tops_apb_merge_gate).
  */
 int tops_apb_qkn_prep(const void* X, const void* wqkv, const void* bq, int qkn, const void* gq, const void* bqn,
                       const void* gk, const void* bkn, void* q, void* k, void* v, int64_t M, int64_t C, int64_t H,

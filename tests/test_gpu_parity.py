@@ -635,6 +635,114 @@ def test_apb_forward_matches_forward_qkv_bitwise(device, M, mask):
         assert torch.equal(again, og_fused), f"M={M}: repeated call differs"
 
 
+def _apb_unfused(d, pre, mask, residual=None):
+    """apb_forward then the gate kernel: the composition tops_apb_forward_gated replaces"""
+    from triangleops_amd.attn_pair_bias.kernel import apb_forward
+    from triangleops_amd.triangle_attn.kernel import gate_out_forward
+
+    M = d["X"].shape[0]
+    og = torch.empty(M, 128, device=d["X"].device, dtype=d["X"].dtype)
+    apb_forward(d["X"], pre["W_QKV"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], og,
+                scale=d["scale"], mask=mask, wqkv_hm=pre["wqkv_hm"])
+    res = None if residual is None else residual.view(M, 1, -1)
+    return gate_out_forward(og.view(M, 1, 128), d["X"], d["W_proj_g"], d["B_proj_g"], d["W_proj_o"], d["B_proj_o"],
+                            residual=res).view(M, -1)
+
+
+@pytest.mark.parametrize("M,mask,biases", [(40, "pad", True), (200, "random", False), (1024, "pad", True),
+                                           (2048, "random", True)])
+@pytest.mark.parametrize("residual", [False, True])
+def test_apb_gated_matches_unfused_bitwise(device, M, mask, biases, residual):
+    """forward() at the tuned shape runs tops_apb_forward_gated (split merge + gate + W_o in one kernel):
+    bitwise equal to apb_forward followed by the gate kernel, with and without the residual add."""
+    from triangleops_amd.attn_pair_bias.kernel import apb_forward_gated, gated_ok
+
+    inp = apb_inputs(M, seed=M + 11, mask=mask, biases=biases)
+    d = to_dev(inp, device)
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], 4, 32)
+    res = torch.randn(M, 128, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(device) if residual \
+        else None
+    assert gated_ok(d["X"], d["Z"], pre["W_combined"], d["W_proj_g"], d["W_proj_o"], res)
+    a = tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=d["scale"], W_proj_g=d["W_proj_g"],
+                                    B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"],
+                                    mask=d["mask"], residual=res)
+    b = apb_forward_gated(d["X"], d["Z"], pre["W_combined"], pre["sum_W_combined"], pre["B_const"], pre["wqkv_hm"],
+                          d["W_proj_g"], d["B_proj_g"], d["W_proj_o"], d["B_proj_o"], scale=d["scale"],
+                          mask=d["mask"], residual=res)
+    ref_ = _apb_unfused(d, pre, d["mask"], residual=res)
+    assert torch.equal(a, b) and torch.equal(a, ref_), f"M={M}: fused gate path differs from the unfused one"
+
+
+def test_apb_merge_gate_entry_points(device):
+    """The fused call's launches one by one through the C ABI (the pre-pass, tops_apb_forward_qkv with Og =
+    NULL leaving the split partials, tops_apb_merge_gate) give forward()'s bits; the entry points refuse
+    what they cannot do (NULL Og without split keys, merge on unsplit keys)."""
+    from triangleops_amd import _native
+    from triangleops_amd.attn_pair_bias.kernel import apb_qkn_prep
+
+    M = 512
+    inp = apb_inputs(M, seed=13, mask="random", biases=True)
+    d = to_dev(inp, device)
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], 4, 32)
+    want = tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=d["scale"], W_proj_g=d["W_proj_g"],
+                                       B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"],
+                                       mask=d["mask"])
+    q, k, v = apb_qkn_prep(d["X"], pre["wqkv_hm"], None, None, qscale=d["scale"])
+    work = torch.empty(_native.apb_workspace_bytes(M, 4, 32), device=device, dtype=torch.uint8)
+    Wc, sWc, Bc = (pre[n].float().contiguous() for n in ("W_combined", "sum_W_combined", "B_const"))
+    m8 = d["mask"].view(torch.int8)
+    st = _native.stream_of(q)
+    _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), d["Z"].data_ptr(), d["Z"].stride(0),
+                 d["Z"].stride(1), Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), m8.data_ptr(), None, work.data_ptr(),
+                 M, 128, 128, 4, 32, 1.0, 1e-5, 2, st)
+    out = torch.empty(M, 128, device=device, dtype=torch.bfloat16)
+    _native.call("tops_apb_merge_gate", work.data_ptr(), d["X"].data_ptr(), d["W_proj_g"].data_ptr(),
+                 d["B_proj_g"].data_ptr(), d["W_proj_o"].data_ptr(), d["B_proj_o"].data_ptr(), None, out.data_ptr(), M,
+                 4, 32, 2, st)
+    assert torch.equal(out, want)
+    # the one-call entry point (all three launches inside the library)
+    gwork = torch.empty(_native.apb_gated_workspace_bytes(M, 4, 32), device=device, dtype=torch.uint8)
+    out1 = torch.empty_like(out)
+    _native.call("tops_apb_forward_gated", d["X"].data_ptr(), pre["wqkv_hm"].data_ptr(), d["Z"].data_ptr(),
+                 d["Z"].stride(0), d["Z"].stride(1), Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), m8.data_ptr(),
+                 d["W_proj_g"].data_ptr(), d["B_proj_g"].data_ptr(), d["W_proj_o"].data_ptr(), d["B_proj_o"].data_ptr(),
+                 None, out1.data_ptr(), gwork.data_ptr(), M, 128, 128, 4, 32, 128, d["scale"], 1e-5, 2, st)
+    assert torch.equal(out1, want)
+    with pytest.raises(RuntimeError, match="keys unsplit"):
+        _native.call("tops_apb_merge_gate", work.data_ptr(), d["X"].data_ptr(), d["W_proj_g"].data_ptr(), None,
+                     d["W_proj_o"].data_ptr(), None, None, out.data_ptr(), 20000, 4, 32, 2, st)
+    with pytest.raises(RuntimeError, match="Og may be NULL only"):
+        _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), d["Z"].data_ptr(), 0, 0,
+                     Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), None, None, work.data_ptr(), 20000, 128, 128, 4, 32,
+                     1.0, 1e-5, 2, st)
+
+
+def test_apb_gated_unsplit_keys_bitwise(device):
+    """M = 16400 (at least 512 query blocks: no key split, so the fused path writes Og to its workspace and
+    runs the gate kernel) on a broadcast Z (every pair shares one 128-channel row: strides (0, 0, 1)),
+    bitwise against the unfused composition, with the residual."""
+    M = 16400
+    inp = apb_inputs(8, seed=5, mask="none", biases=True)
+    g = torch.Generator().manual_seed(6)
+    d = to_dev(inp, device)
+    d["X"] = torch.randn(M, 128, generator=g).to(torch.bfloat16).to(device)
+    d["Z"] = torch.randn(1, 1, 128, generator=g).to(torch.bfloat16).to(device).expand(M, M, 128)
+    kmask = (torch.arange(M) < M - 37).to(device)
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], 4, 32)
+    from triangleops_amd import _native
+
+    assert _native.apb_gated_workspace_bytes(M, 4, 32) > _native.apb_workspace_bytes(M, 4, 32)  # unsplit: Og region
+    res = torch.randn(M, 128, generator=g).to(torch.bfloat16).to(device)
+    a = tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=d["scale"], W_proj_g=d["W_proj_g"],
+                                    B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"],
+                                    mask=kmask, residual=res)
+    ref_ = _apb_unfused(d, pre, kmask, residual=res)
+    assert torch.isfinite(a.float()).all() and torch.equal(a, ref_), "unsplit fused path differs from the unfused one"
+
+
 def _apb_perturbed(inp, kmask, seed):
     """inputs with X rows and Z key columns replaced at the masked keys"""
     g = torch.Generator().manual_seed(seed)

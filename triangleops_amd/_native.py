@@ -37,6 +37,11 @@ _SIGNATURES = {
     "tops_apb_forward": [
         _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],
+    "tops_apb_forward_gated": [
+        _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+        _f32, _i32, _p,
+    ],
+    "tops_apb_merge_gate": [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p],
     "tops_apb_forward_noalloc": [
         _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _i32, _p,
     ],
@@ -74,6 +79,7 @@ _OTHER = {
     "tops_last_error": ([], ctypes.c_char_p),
     "tops_abi_version": ([], ctypes.c_int),
     "tops_apb_workspace_bytes": ([_i64, _i64, _i64], ctypes.c_int64),
+    "tops_apb_gated_workspace_bytes": ([_i64, _i64, _i64], ctypes.c_int64),
 }
 
 EXPORTED = tuple(_SIGNATURES) + tuple(_OTHER)
@@ -121,6 +127,11 @@ def call(name: str, *args) -> None:
 def apb_workspace_bytes(M: int, H: int, D: int) -> int:
     lib = _lib if _lib is not None else load()
     return int(lib.tops_apb_workspace_bytes(M, H, D))
+
+
+def apb_gated_workspace_bytes(M: int, H: int, D: int) -> int:
+    lib = _lib if _lib is not None else load()
+    return int(lib.tops_apb_gated_workspace_bytes(M, H, D))
 
 
 def stream_of(t: torch.Tensor) -> int:

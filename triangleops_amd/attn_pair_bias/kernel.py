@@ -74,6 +74,66 @@ def apb_forward(X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0,
     return Og
 
 
+def gated_ok(X, Z, W_combined, W_g, W_o, residual=None):
+    """True when apb_forward_gated applies: the tuned shape (C_s = C_z = 128, H = 4, D = 32) with
+    C_out = 128 and 16-bit I/O (the residual, if any, (M, 128) with unit channel stride)."""
+    M, C = X.shape
+    H = W_combined.shape[0]
+    ok = (C == 128 and Z.shape[2] == 128 and H == 4 and W_combined.shape[1] == 128 and X.dtype != torch.float32
+          and tuple(W_g.shape) == (128, 128) and tuple(W_o.shape) == (128, 128))
+    return ok and (residual is None or tuple(residual.shape) == (M, 128))
+
+
+def apb_forward_gated(X, Z, W_combined, sum_W_combined, B_const, wqkv_hm, W_g, b_g, W_o, b_o, *, scale=1.0,
+                      eps=1e-5, mask=None, residual=None):
+    """out = ((Og * sigmoid(X W_g^T + b_g)) -> io) W_o^T + b_o (+ residual), Og = apb_forward(...):
+    the attention with the gate and output projection of attn_pair_bias/module.py:69-70 fused.  With
+    split keys: tops_apb_forward (Og = NULL) then tops_apb_merge_gate (the split merge, gate and W_o in
+    one kernel); otherwise tops_apb_forward_gated.  Requires gated_ok(...); returns (M, 128)."""
+    M, C = X.shape
+    H = W_combined.shape[0]
+    D = wqkv_hm.shape[2]
+    assert gated_ok(X, Z, W_combined, W_g, W_o, residual) and D == 32
+    code = io_dtype_code(X.dtype)
+    _native.check_device(X, Z, wqkv_hm, W_combined, W_g, W_o, mask, residual)
+    X = _native.vec16(X)
+    Z = _native.vec16(Z)
+    dt = X.dtype
+    cast = lambda t: None if t is None else _native.vec16(t.to(dt))  # noqa: E731  (contiguous, 16-byte aligned)
+    wqkv_hm = cast(wqkv_hm)
+    Wc = W_combined.float().contiguous()
+    sWc = sum_W_combined.float().contiguous()
+    Bc = B_const.float().contiguous()
+    m8 = _native.mask_i8(mask)
+    if m8 is not None:
+        assert m8.numel() == M, "mask must be (M,)"
+    st = _native.stream_of(X)
+    nqkv = (3 * M * H * D * 2 + 255) // 256 * 256
+    nbytes = _native.apb_workspace_bytes(M, H, D)
+    if nbytes > nqkv:
+        # split keys: the pre-pass and attention are launched first (tops_apb_forward with Og = NULL
+        # leaves the split partials after Q / K / V), the gate's arguments are prepared while they
+        # run, then tops_apb_merge_gate; the same kernels as tops_apb_forward_gated
+        work = torch.empty(nbytes, device=X.device, dtype=torch.uint8)
+        _native.call("tops_apb_forward", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
+                     Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), _native.ptr(m8), None, work.data_ptr(), M, C,
+                     Z.shape[2], H, D, float(scale), float(eps), code, st)
+        W_g, b_g, W_o, b_o, res = (cast(t) for t in (W_g, b_g, W_o, b_o, residual))
+        out = torch.empty(M, 128, device=X.device, dtype=dt)
+        _native.call("tops_apb_merge_gate", work.data_ptr() + nqkv, X.data_ptr(), W_g.data_ptr(), _native.ptr(b_g),
+                     W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), M, H, D, code, st)
+        return out
+    W_g, b_g, W_o, b_o, res = (cast(t) for t in (W_g, b_g, W_o, b_o, residual))
+    out = torch.empty(M, 128, device=X.device, dtype=dt)
+    nbytes = _native.apb_gated_workspace_bytes(M, H, D)
+    work = torch.empty(max(nbytes, 1), device=X.device, dtype=torch.uint8) if nbytes else None
+    _native.call("tops_apb_forward_gated", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
+                 Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), _native.ptr(m8), W_g.data_ptr(), _native.ptr(b_g),
+                 W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), _native.ptr(work), M, C,
+                 Z.shape[2], H, D, 128, float(scale), float(eps), code, st)
+    return out
+
+
 def _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm, H, D):
     """apb_forward at any (C_s, C_z, H, D) or with fp32 I/O (tops_apb_generic_prep / _attention);
     the Q/K/V and bias scratch is allocated here."""

@@ -2,9 +2,10 @@
 
 Drop-in for `triangle_ops/attn_pair_bias/module.py` of the reference: same `precompute`,
 `forward` and one-shot signatures and precompute keys (W_QKV, W_combined, sum_W_combined,
-B_const), plus `wqkv_hm` (the head-major weight the kernel loads).  Two launches per call
-(three when the key range is split for parallelism): the fused QKV + LN(Z) bias + attention
-kernel, and the gate + W_o kernel.
+B_const), plus `wqkv_hm` (the head-major weight the kernel loads).  Three launches per call at the
+tuned shape (C_s = C_z = C_out = 128, H = 4, D = 32): the Q / K / V pre-pass, the LN(Z) bias +
+attention kernel, and the split merge fused with the gate + W_o (tops_apb_forward_gated; the gate
+kernel itself when the keys are not split); other shapes run `apb_forward` then the gate.
 
 Additive extension: `forward(..., mask=None)` / `attention_pair_bias(..., mask=None)` take an
 optional (M,) key mask (masked keys -> -inf, as the reference's K-Fold variant does at
@@ -24,7 +25,7 @@ import torch
 from .._common.layouts import interleave_qkv, qkv_head_major
 from .._common.ln_absorption import absorb_ln_matmul
 from ..triangle_attn.kernel import gate_out_forward
-from .kernel import apb_forward, apb_forward_qkv, apb_qkn_prep
+from .kernel import apb_forward, apb_forward_gated, apb_forward_qkv, apb_qkn_prep, gated_ok
 
 
 def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
@@ -49,6 +50,10 @@ def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_p
     M = X.shape[0]
     H = pre["sum_W_combined"].shape[0]
     D = pre["W_QKV"].shape[1] // (3 * H)
+    if D == 32 and pre.get("wqkv_hm") is not None and gated_ok(X, Z, pre["W_combined"], W_proj_g, W_proj_o, residual):
+        return apb_forward_gated(X, Z, pre["W_combined"], pre["sum_W_combined"], pre["B_const"], pre["wqkv_hm"],
+                                 W_proj_g, B_proj_g, W_proj_o, B_proj_o, scale=scale, eps=eps, mask=mask,
+                                 residual=residual)
     Og = torch.empty(M, H * D, device=X.device, dtype=X.dtype)
     apb_forward(
         X,

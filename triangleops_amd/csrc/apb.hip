@@ -12,13 +12,15 @@
 //   * per (query, 16 keys) the 16 x 128 Z slice is an MFMA A operand loaded straight from HBM;
 //     a 16x16x32 MFMA against [Wc_hi; Wc_lo] (the fp32 LN-folded weight split into two
 //     io-typed terms, accumulated into the same tile) gives z . Wc_h for the 4 heads, and the
-//     LayerNorm statistics are reduced from the same registers (two-pass, fp32);
+//     LayerNorm statistics are reduced from the same registers (sum and sum of squares, fp32);
 //   * bias[h,q,k] = rstd * (z . Wc_h - mean * sum(Wc_h)) + Bc_h goes through LDS to the wave
 //     of head h, which runs S^T = bias + K . Q^T, the online softmax and O^T += V^T . P^T.  The
 //     wave brings head h's Q, K and V into MFMA operand layout with two MFMA k-steps against a
 //     block-identity operand built in registers (an exact transpose through the matrix core),
 //     so there is no LDS traffic for Q/K/V/P.
-// Split partials (running max m, sum l, unnormalised O) are merged by apb_combine_kernel.
+// Split partials (running max m, sum l, unnormalised O) are merged by apb_combine_kernel into Og,
+// or, on the fused path (tops_apb_forward_gated), by apb_merge_gate_kernel, which goes on to the
+// gate and the output projection of attn_pair_bias/module.py:69-70 in the same launch.
 //
 // Reference: attn_pair_bias/kernel.py:24-202 (`_apb_kernel`), :205-257 (`apb_forward`);
 // the key mask follows benchmarks/references.py:273-274 (masked keys -> -inf).
@@ -135,25 +137,26 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
     };
     auto zbias = [&](int u, const V8* za) {
       const int lq = 8 * wave + (u >> 1), kh = u & 1;
-      float sum = 0.f;
+      // LayerNorm statistics in one pass, sum and sum of squares with clamped variance, as the
+      // reference accumulates them (attn_pair_bias/kernel.py:168-173): packed dot products take two
+      // channels per instruction with fp32 products and sums
+      const vec<T, 2> one = {(T)1.0f, (T)1.0f};
+      float sum = 0.f, sq = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sum += (float)za[s][e];
-      sum += __shfl_xor(sum, 16);
-      sum += __shfl_xor(sum, 32);
-      const float mean = sum * (1.0f / C);
-      float sq = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float d = (float)za[s][e] - mean;
-          sq += d * d;
+        for (int e = 0; e < 8; e += 2) {
+          const vec<T, 2> pr = {za[s][e], za[s][e + 1]};
+          sum = Mma<T>::dot2(pr, one, sum);
+          sq = Mma<T>::dot2(pr, pr, sq);
         }
+      sum += __shfl_xor(sum, 16);
       sq += __shfl_xor(sq, 16);
+      sum += __shfl_xor(sum, 32);
       sq += __shfl_xor(sq, 32);
-      const float rstd = rsqrtf(sq * (1.0f / C) + eps);
+      const float mean = sum * (1.0f / C);
+      const float var = fmaxf(sq * (1.0f / C) - mean * mean, 0.f);
+      const float rstd = rsqrtf(var + eps);
       f32x4 acc = {};
 #pragma unroll
       for (int s = 0; s < 4; ++s) acc = Mma<T>::m16(za[s], whi[s], acc);
@@ -301,6 +304,183 @@ __global__ __launch_bounds__(256) void apb_combine_kernel(const float* __restric
   Og[q * (H * D) + hd] = (T)(ot / lt);
 }
 
+// Split merge fused with the gate and output projection of attention_pair_bias
+// (attn_pair_bias/module.py:69-70: out = ((Og * sigmoid(X . Wg^T + bg)) -> io) . Wo^T + bo), C = 128:
+// one block per 32 queries, 4 waves.  Thread t merges the split partials of query t / 8, channels
+// 32 g + 4 (t % 8) + e of every head g, in apb_combine_kernel's arithmetic and order, so the merged
+// Og has the same bits, and stages it in LDS beside the block's 32 rows of X; then wave w computes
+// features [32 w, +32) of both GEMMs for the 32 queries exactly as gate_out_kernel does (weight
+// rows in registers, permuted so each lane holds 16 consecutive features of one query; the gated
+// values overwrite Og in LDS; the output goes through a query-major LDS tile to whole-row stores).
+// RES: out = res + result, the single-representation residual of a Pairformer block, rounded once.
+template <typename T, bool RES>
+__global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __restrict__ ws, const T* __restrict__ X,
+                                                            const T* __restrict__ Wg, const T* __restrict__ bg,
+                                                            const T* __restrict__ Wo, const T* __restrict__ bo,
+                                                            const T* __restrict__ res, T* __restrict__ out,
+                                                            int64_t M, int nsplit) {
+  constexpr int C = 128, H = 4, TOK = 32, ROW = C * 2, KS = C / 16;
+  using V8 = vec<T, 8>;
+  __shared__ __attribute__((aligned(16))) char og_s[TOK * ROW];  // merged Og, then the gated values
+  __shared__ __attribute__((aligned(16))) char x_s[TOK * ROW];   // gate input X
+  __shared__ __attribute__((aligned(16))) T o_s[TOK * C];         // output tile, query-major
+  __shared__ __attribute__((aligned(16))) float cst[2][C];        // -log2(e) bg, bo
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int64_t q0 = (int64_t)blockIdx.x * TOK;
+  auto swz = [](int t, int chunk) { return (chunk ^ row_key<C>(t)) << 4; };
+
+  for (int i = tid; i < C; i += 256) {
+    cst[0][i] = bg ? -kLog2e * (float)bg[i] : 0.f;
+    cst[1][i] = bo ? (float)bo[i] : 0.f;
+  }
+  // X rows of the block's queries (rows past M repeat row M - 1; their results are not stored)
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int ci = k * 256 + tid, t = ci >> 4, c = ci & 15;
+    const int64_t q = q0 + t < M ? q0 + t : M - 1;
+    *reinterpret_cast<V8*>(&x_s[t * ROW + swz(t, c)]) = ldg<V8>(X + q * C + 8 * c);
+  }
+  // weight rows as MFMA A operands: row col of wave w is feature 32 w + prow
+  const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
+  V8 wg[KS], wo[KS];
+  {
+    const int64_t frow = (int64_t)(32 * wave + prow) * C;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+      wo[s] = ldg<V8>(Wo + frow + 16 * s + 8 * hl);
+    }
+  }
+  // ---- merge the split partials ----
+  // thread t: query t / 8, channels 32 g + 4 (t % 8) + e of head g (g, e < 4): the 8 threads of a
+  // query read one whole 128-byte line of head g per load instruction, and each thread needs the
+  // (m, l) pairs of all four heads (32 contiguous bytes per split, broadcast to the 8 threads)
+  {
+    const int t = tid >> 3, j = tid & 7;
+    const int64_t q = q0 + t < M ? q0 + t : M - 1;
+    const float* ml = ws + (int64_t)nsplit * M * C + q * H * 2;  // split s: + s * M * H * 2
+    const float* op = ws + q * C + 4 * j;                         // split s: + s * M * C; head g: + 32 g
+    const int64_t sml = M * H * 2, so = M * C;
+    // batches of 16 splits with every load of a batch issued before its first use; per element the
+    // sums run in split order with apb_combine_kernel's arithmetic, so Og gets the same bits
+    constexpr int SB = 16;
+    float mx[H];
+#pragma unroll
+    for (int g = 0; g < H; ++g) mx[g] = -INFINITY;
+    for (int s0 = 0; s0 < nsplit; s0 += SB) {
+      f32x4 mb[SB][2];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int s = s0 + i < nsplit ? s0 + i : s0;  // past the batch: split s0 again (unused)
+        mb[i][0] = ldg<f32x4>(ml + s * sml);
+        mb[i][1] = ldg<f32x4>(ml + s * sml + 4);
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        if (s0 + i < nsplit) {
+          mx[0] = fmaxf(mx[0], mb[i][0][0]);
+          mx[1] = fmaxf(mx[1], mb[i][0][2]);
+          mx[2] = fmaxf(mx[2], mb[i][1][0]);
+          mx[3] = fmaxf(mx[3], mb[i][1][2]);
+        }
+    }
+    float mu[H], lt[H], ot[H][4];
+#pragma unroll
+    for (int g = 0; g < H; ++g) {
+      mu[g] = mx[g] == -INFINITY ? 0.f : mx[g];
+      lt[g] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ot[g][e] = 0.f;
+    }
+    for (int s0 = 0; s0 < nsplit; s0 += SB) {
+      f32x4 mb[SB][2], ob[SB][H];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int s = s0 + i < nsplit ? s0 + i : s0;
+        mb[i][0] = ldg<f32x4>(ml + s * sml);
+        mb[i][1] = ldg<f32x4>(ml + s * sml + 4);
+#pragma unroll
+        for (int g = 0; g < H; ++g) ob[i][g] = ldg<f32x4>(op + s * so + 32 * g);
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        if (s0 + i < nsplit) {
+#pragma unroll
+          for (int g = 0; g < H; ++g) {
+            const float m = mb[i][g >> 1][2 * (g & 1)], l = mb[i][g >> 1][2 * (g & 1) + 1];
+            const float w = fast_exp2((m - mu[g]) * kLog2e);
+            lt[g] += w * l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ot[g][e] += w * ob[i][g][e];
+          }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < H; ++g) {  // channels 32 g + 4 j .. + 3: half of 16-byte chunk 4 g + j / 2
+      vec<T, 4> r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = (T)(ot[g][e] / lt[g]);
+      *reinterpret_cast<vec<T, 4>*>(&og_s[t * ROW + swz(t, 4 * g + (j >> 1)) + 8 * (j & 1)]) = r;
+    }
+  }
+  __syncthreads();  // cst, X and Og staged
+
+  const int tok = col, f0 = 32 * wave + 16 * hl;
+  {  // GEMM 1, sigmoid gate, Og * gate -> in place over the Og tile
+    const char* grow = &x_s[tok * ROW];
+    char* orow = &og_s[tok * ROW];
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      acc = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(grow + swz(tok, 2 * k + hl)), acc);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = f0 / 8 + h;
+      V8* p = reinterpret_cast<V8*>(orow + swz(tok, c));
+      const V8 ov = *p;
+      V8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(acc[8 * h + e], -kLog2e, cst[0][f0 + 8 * h + e])));
+        r[e] = (T)((float)ov[e] * gate);
+      }
+      *p = r;
+    }
+  }
+  __syncthreads();  // gated tile complete
+  {  // GEMM 2 on the gated tile -> query-major output tile
+    const char* trow = &og_s[tok * ROW];
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      acc = Mma<T>::m32(wo[k], *reinterpret_cast<const V8*>(trow + swz(tok, 2 * k + hl)), acc);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      V8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[1][f0 + 8 * h + e]);
+      const int c = f0 / 8 + h;
+      *reinterpret_cast<V8*>(&o_s[tok * C + ((c ^ row_key<C>(tok)) << 3)]) = r;
+    }
+  }
+  __syncthreads();  // output tile complete
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int ci = k * 256 + tid, t = ci >> 4, c = ci & 15;
+    const int64_t q = q0 + t;
+    if (q >= M) continue;
+    V8 v = *reinterpret_cast<const V8*>(&o_s[t * C + ((c ^ row_key<C>(t)) << 3)]);
+    if constexpr (RES) {
+      const V8 r = ldg<V8>(res + q * C + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (T)((float)r[e] + (float)v[e]);
+    }
+    stg<V8>(out + q * C + 8 * c, v);
+  }
+}
+
 // Q / K / V pre-pass at the tuned shape (C = H*D = 128, H = 4, D = 32): 32 tokens per block,
 // wave h computes head h's 32 channels of q, k and v (8 MFMA k-steps each; lane col holds 16 of
 // the 32 channels of token q0 + col, the other 16 in lane col + 32).  With QKN the per-token
@@ -416,10 +596,11 @@ static int apb_qkv_t(const void* X, const void* wqkv, const void* bq, int qkn, c
   return launched("apb_qkv_kernel");
 }
 
+// The attention kernel alone: Og when the keys are not split, else the split partials in `part`.
 template <typename T>
-static int apb_attention_t(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0, int64_t sz1,
-                           const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og, void* part,
-                           int64_t M, float scale, float eps, hipStream_t st) {
+static int apb_attention_core_t(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0, int64_t sz1,
+                                const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og,
+                                void* part, int64_t M, float scale, float eps, hipStream_t st) {
   if (M == 0) return TOPS_OK;
   const ApbSplit sp = apb_split(M);
   const int64_t qblocks = (M + 31) / 32;
@@ -427,7 +608,16 @@ static int apb_attention_t(const void* Q, const void* K, const void* V, const vo
   hipLaunchKernelGGL((apb_attn_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Q, (const T*)K,
                      (const T*)V, (const T*)Z, sz0, sz1, Wc, sWc, Bc, (const int8_t*)mask, (T*)Og, (float*)part, M,
                      sp.nsplit, sp.keys_per_split, scale, eps);
-  int rc = launched("apb_attn_kernel");
+  return launched("apb_attn_kernel");
+}
+
+template <typename T>
+static int apb_attention_t(const void* Q, const void* K, const void* V, const void* Z, int64_t sz0, int64_t sz1,
+                           const float* Wc, const float* sWc, const float* Bc, const void* mask, void* Og, void* part,
+                           int64_t M, float scale, float eps, hipStream_t st) {
+  if (M == 0) return TOPS_OK;
+  const ApbSplit sp = apb_split(M);
+  int rc = apb_attention_core_t<T>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, scale, eps, st);
   if (rc != TOPS_OK || sp.nsplit == 1) return rc;
   const int64_t n = M * 128;
   hipLaunchKernelGGL((apb_combine_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
@@ -547,6 +737,91 @@ extern "C" int64_t tops_apb_workspace_bytes(int64_t M, int64_t H, int64_t D) {
   return apb_qkv_bytes(M) + part;
 }
 
+extern "C" int64_t tops_apb_gated_workspace_bytes(int64_t M, int64_t H, int64_t D) {
+  if (M <= 0) return 0;
+  const ApbSplit sp = apb_split(M);
+  // without a key split the attention writes Og (M x H*D io values) after Q / K / V instead
+  return sp.nsplit == 1 ? apb_qkv_bytes(M) + (M * H * D * 2 + 255) / 256 * 256 : tops_apb_workspace_bytes(M, H, D);
+}
+
+template <typename T>
+static int apb_merge_gate_t(const float* part, const void* X, const void* Wg, const void* bg, const void* Wo,
+                            const void* bo, const void* res, void* out, int64_t M, int nsplit, hipStream_t st) {
+  const int64_t blocks = (M + 31) / 32;
+  if (res)
+    hipLaunchKernelGGL((apb_merge_gate_kernel<T, true>), dim3((unsigned)blocks), dim3(256), 0, st, part, (const T*)X,
+                       (const T*)Wg, (const T*)bg, (const T*)Wo, (const T*)bo, (const T*)res, (T*)out, M, nsplit);
+  else
+    hipLaunchKernelGGL((apb_merge_gate_kernel<T, false>), dim3((unsigned)blocks), dim3(256), 0, st, part, (const T*)X,
+                       (const T*)Wg, (const T*)bg, (const T*)Wo, (const T*)bo, (const T*)res, (T*)out, M, nsplit);
+  return launched("apb_merge_gate_kernel");
+}
+
+extern "C" int tops_apb_forward_gated(const void* X, const void* wqkv, const void* Z, int64_t sz0, int64_t sz1,
+                                      const float* Wc, const float* sWc, const float* Bc, const void* mask,
+                                      const void* Wg, const void* bg, const void* Wo, const void* bo, const void* res,
+                                      void* out, void* work, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D,
+                                      int64_t Cout, float scale, float eps, int dtype, void* stream) {
+  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc && Wg && Wo && out, "tops_apb_forward_gated: null pointer argument");
+  TOPS_REQUIRE(C == 128 && Cz == 128 && H == 4 && D == 32 && Cout == 128,
+               "tops_apb_forward_gated: supports C == Cz == C_out == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld "
+               "D=%lld C_out=%lld)", (long long)C, (long long)Cz, (long long)H, (long long)D, (long long)Cout);
+  TOPS_REQUIRE(M >= 0 && M < (1LL << 31), "tops_apb_forward_gated: bad M");
+  TOPS_REQUIRE(work || M == 0, "tops_apb_forward_gated: workspace of tops_apb_gated_workspace_bytes(M, H, D) bytes required");
+  TOPS_REQUIRE(sz0 % 8 == 0 && sz1 % 8 == 0 && (uintptr_t)Z % 16 == 0 && (uintptr_t)X % 16 == 0 &&
+                   (uintptr_t)work % 16 == 0 && (uintptr_t)out % 16 == 0 && (uintptr_t)res % 16 == 0,
+               "tops_apb_forward_gated: Z needs token strides that are multiples of 8, and Z, X, res, out and the "
+               "workspace 16-byte aligned base pointers");
+  TOPS_REQUIRE(dtype == TOPS_DTYPE_BF16 || dtype == TOPS_DTYPE_F16,
+               "tops_apb_forward_gated: unsupported dtype code %d", dtype);
+  if (M == 0) return TOPS_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const ApbSplit sp = apb_split(M);
+  char* w = (char*)work;
+  char *q = w, *k = w + M * 128 * 2, *v = w + 2 * M * 128 * 2, *part = w + apb_qkv_bytes(M);
+  int rc;
+  if (sp.nsplit == 1) {  // no split partials: Og in the workspace, then the gate kernel
+    rc = tops_apb_forward(X, wqkv, Z, sz0, sz1, Wc, sWc, Bc, mask, part, work, M, C, Cz, H, D, scale, eps, dtype,
+                          stream);
+    if (rc != TOPS_OK) return rc;
+    if (res)
+      return tops_gate_out_residual(part, 128, 128, X, 128, 128, nullptr, nullptr, 1e-5f, 0, Wg, bg, Wo, bo, res, 128,
+                                    128, out, 128, 128, M, 1, 128, dtype, stream);
+    return tops_gate_out(part, 128, 128, X, 128, 128, nullptr, nullptr, 1e-5f, 0, Wg, bg, Wo, bo, out, M, 1, 128,
+                         dtype, stream);
+  }
+  if (dtype == TOPS_DTYPE_BF16) {
+    rc = apb_qkv_t<__bf16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
+    if (rc == TOPS_OK)  // Og unused with a split: the partials go to `part`
+      rc = apb_attention_core_t<__bf16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, part, M, 1.0f, eps, st);
+    return rc != TOPS_OK ? rc : apb_merge_gate_t<__bf16>((const float*)part, X, Wg, bg, Wo, bo, res, out, M, sp.nsplit, st);
+  }
+  rc = apb_qkv_t<_Float16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
+  if (rc == TOPS_OK)
+    rc = apb_attention_core_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, part, M, 1.0f, eps, st);
+  return rc != TOPS_OK ? rc : apb_merge_gate_t<_Float16>((const float*)part, X, Wg, bg, Wo, bo, res, out, M, sp.nsplit, st);
+}
+
+extern "C" int tops_apb_merge_gate(const float* part, const void* X, const void* Wg, const void* bg, const void* Wo,
+                                   const void* bo, const void* res, void* out, int64_t M, int64_t H, int64_t D,
+                                   int dtype, void* stream) {
+  TOPS_REQUIRE(part && X && Wg && Wo && out, "tops_apb_merge_gate: null pointer argument");
+  TOPS_REQUIRE(H == 4 && D == 32, "tops_apb_merge_gate: supports H == 4, D == 32 (got H=%lld D=%lld)", (long long)H,
+               (long long)D);
+  TOPS_REQUIRE(M >= 0 && M < (1LL << 31), "tops_apb_merge_gate: bad M");
+  TOPS_REQUIRE(M == 0 || apb_split(M).nsplit > 1, "tops_apb_merge_gate: M = %lld leaves the keys unsplit (no partials)",
+               (long long)M);
+  TOPS_REQUIRE((uintptr_t)part % 16 == 0 && (uintptr_t)X % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+                   (uintptr_t)res % 16 == 0,
+               "tops_apb_merge_gate: part, X, res and out must be 16-byte aligned");
+  if (M == 0) return TOPS_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int ns = apb_split(M).nsplit;
+  if (dtype == TOPS_DTYPE_BF16) return apb_merge_gate_t<__bf16>(part, X, Wg, bg, Wo, bo, res, out, M, ns, st);
+  if (dtype == TOPS_DTYPE_F16) return apb_merge_gate_t<_Float16>(part, X, Wg, bg, Wo, bo, res, out, M, ns, st);
+  return fail(TOPS_EUNSUPPORTED, "tops_apb_merge_gate: unsupported dtype code %d", dtype);
+}
+
 // The workspace of tops_apb_forward_noalloc: a library-owned array in device memory (one copy per
 // GPU the library runs on, held until the process ends).  Host code never uses the array's name
 // as an address: its device address comes from hipGetSymbolAddress, once per device.
@@ -610,7 +885,9 @@ static int apb_forward_impl(const char* who, const void* X, const void* wqkv, co
                             int64_t sz1, const float* Wc, const float* sWc, const float* Bc, const void* mask,
                             void* Og, void* work, int64_t M, int64_t C, int64_t Cz, int64_t H, int64_t D, float scale,
                             float eps, int dtype, void* stream) {
-  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc && Og, "%s: null pointer argument", who);
+  TOPS_REQUIRE(X && wqkv && Z && Wc && sWc && Bc, "%s: null pointer argument", who);
+  TOPS_REQUIRE(Og || M == 0 || apb_split(M).nsplit > 1,
+               "%s: Og may be NULL only when the keys are split (the partials stay in work)", who);
   TOPS_REQUIRE(C == 128 && Cz == 128 && H == 4 && D == 32,
                "%s: supports C == Cz == 128, H == 4, D == 32 (got C=%lld Cz=%lld H=%lld D=%lld)", who, (long long)C,
                (long long)Cz, (long long)H, (long long)D);
@@ -625,13 +902,19 @@ static int apb_forward_impl(const char* who, const void* X, const void* wqkv, co
   char* w = (char*)work;
   char *q = w, *k = w + M * 128 * 2, *v = w + 2 * M * 128 * 2, *part = w + apb_qkv_bytes(M);
   int rc;
+  // Og == NULL: the attention's split partials stay in `part` (tops_apb_merge_gate reads them)
   if (dtype == TOPS_DTYPE_BF16) {
     rc = apb_qkv_t<__bf16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
-    return rc != TOPS_OK ? rc : apb_attention_t<__bf16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st);
+    if (rc != TOPS_OK) return rc;
+    return Og ? apb_attention_t<__bf16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st)
+              : apb_attention_core_t<__bf16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, part, M, 1.0f, eps, st);
   }
   if (dtype == TOPS_DTYPE_F16) {
     rc = apb_qkv_t<_Float16>(X, wqkv, nullptr, 0, nullptr, nullptr, nullptr, nullptr, q, k, v, M, scale, eps, st);
-    return rc != TOPS_OK ? rc : apb_attention_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st);
+    if (rc != TOPS_OK) return rc;
+    return Og ? apb_attention_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, part, M, 1.0f, eps, st)
+              : apb_attention_core_t<_Float16>(q, k, v, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, part, M, 1.0f, eps,
+                                               st);
   }
   return fail(TOPS_EUNSUPPORTED, "%s: unsupported dtype code %d", who, dtype);
 }
@@ -640,7 +923,9 @@ extern "C" int tops_apb_forward_qkv(const void* Q, const void* K, const void* V,
                                     int64_t sz1, const float* Wc, const float* sWc, const float* Bc, const void* mask,
                                     void* Og, void* work, int64_t M, int64_t HD, int64_t Cz, int64_t H, int64_t D,
                                     float scale, float eps, int dtype, void* stream) {
-  TOPS_REQUIRE(Q && K && V && Z && Wc && sWc && Bc && Og, "tops_apb_forward_qkv: null pointer argument");
+  TOPS_REQUIRE(Q && K && V && Z && Wc && sWc && Bc, "tops_apb_forward_qkv: null pointer argument");
+  TOPS_REQUIRE(Og || M == 0 || apb_split(M).nsplit > 1,
+               "tops_apb_forward_qkv: Og may be NULL only when the keys are split (the partials stay in work)");
   TOPS_REQUIRE(HD == 128 && Cz == 128 && H == 4 && D == 32,
                "tops_apb_forward_qkv: supports H*D == Cz == 128, H == 4, D == 32 (got H*D=%lld Cz=%lld H=%lld D=%lld)",
                (long long)HD, (long long)Cz, (long long)H, (long long)D);
@@ -653,9 +938,12 @@ extern "C" int tops_apb_forward_qkv(const void* Q, const void* K, const void* V,
   if (M == 0) return TOPS_OK;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TOPS_DTYPE_BF16)
-    return apb_attention_t<__bf16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
+    return Og ? apb_attention_t<__bf16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st)
+              : apb_attention_core_t<__bf16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, work, M, scale, eps, st);
   if (dtype == TOPS_DTYPE_F16)
-    return apb_attention_t<_Float16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st);
+    return Og ? apb_attention_t<_Float16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, Og, work, M, scale, eps, st)
+              : apb_attention_core_t<_Float16>(Q, K, V, Z, sz0, sz1, Wc, sWc, Bc, mask, nullptr, work, M, scale, eps,
+                                               st);
   return fail(TOPS_EUNSUPPORTED, "tops_apb_forward_qkv: unsupported dtype code %d", dtype);
 }
 
