@@ -292,6 +292,57 @@ constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
+// A row whose keys are all masked: with Q and the bias identity zeroed, every score of the main
+// loop is C0 = 0, so each key k < N gets weight exp2(0) = 1 and each key >= N weight 0, in every
+// query column alike.  The PV products alone, over the same visited tiles in the main loop's order
+// with the same P operands, give the main loop's O bit for bit (and l = N exactly), without the
+// score MFMAs, exponentials, LDS staging and barriers.  Kept out of line so the main loop's
+// register allocation does not see it.
+template <typename T, int QT>
+__device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const short* vblk, int nv, int64_t N,
+                                             T* __restrict__ out, int64_t i, int64_t so0, int64_t so1, int h,
+                                             int dv, int64_t qbase, int lane) {
+  constexpr int D = 32;
+  using V8 = vec<T, 8>;
+  using V4 = vec<T, 4>;
+  const int hl = lane >> 5, col = lane & 31;
+  f32x16 acc = {};
+  for (int j = 0; j < nv; ++j) {
+    const int kb = vblk[j];
+    const T* vt = kvrow + (int64_t)kb * kKVBlock + 64 * D + col * 64 + 8 * hl;  // V^T row col
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int64_t nk = N - 64LL * kb - 32 * kt;  // keys < N in this 32-key tile (may be <= 0)
+      V8 pone[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int v = 8 * jj + e;  // D slot v of the score tile: key 8 (v / 4) + 4 hl + v % 4
+          pone[jj][e] = (T)(8 * (v / 4) + 4 * hl + (v % 4) < nk ? 1.0f : 0.0f);
+        }
+      acc = Mma<T>::m32(ldg<V8>(vt + 32 * kt), pone[0], acc);
+      acc = Mma<T>::m32(ldg<V8>(vt + 32 * kt + 16), pone[1], acc);
+    }
+  }
+  // O = acc / N for every query of the wave (l = N, as halves_sum gives it in the main loop)
+  const float inv = 1.0f / (float)N;
+#pragma unroll
+  for (int t = 0; t < QT; ++t) {
+    const int64_t q = qbase + 32 * t + col;
+    if (q < N) {
+      T* dst = out + i * so0 + q * so1 + (int64_t)h * dv + 4 * hl;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (8 * g >= dv) break;
+        V4 w4 = {(T)(acc[4 * g] * inv), (T)(acc[4 * g + 1] * inv), (T)(acc[4 * g + 2] * inv),
+                 (T)(acc[4 * g + 3] * inv)};
+        stg<V4>(dst + 8 * g, w4);
+      }
+    }
+  }
+}
+
 template <typename T, int QT, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
@@ -409,9 +460,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
   __syncthreads();
   const bool uniform = row_any == 0;  // no valid key: every score is -1e9, weights 1/N
   const int nv = nvblk;               // >= 1 whenever N >= 1
-  if (uniform) {
-#pragma unroll
-    for (int t = 0; t < QT; ++t) qop[t][0] = qop[t][1] = V8{};
+  if (uniform) {  // block-uniform: the mean of V over the N keys, without the main loop
+    tri_uniform_row<T, QT>(kvrow, vblk, nv, N, out, i, so0, so1, h, dv, qbase, lane);
+    return;
   }
 
   // identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j
