@@ -891,7 +891,7 @@ __global__ __launch_bounds__(256, 2) void tmu_einsum_f32_kernel(const float* __r
 //   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
 //   registers (4 channels x 8 tokens per thread) into a token-major tile; x (token-major) is
-//   normalised on the way in (16 lanes per token, two-pass statistics);
+//   normalised on the way in (16 lanes per token, one-pass statistics, `ln_stats16`);
 //   waves 4-11 (writers) compute features [32 (w & 3), +32) for the 32 tokens [32 (w >> 2), +32)
 //   (w = wave - 4) with their Wp / Wg rows in registers (rows permuted so each lane ends up with
 //   16 consecutive features of one token), take the LN statistics of y from LDS and apply them
