@@ -615,7 +615,10 @@ __global__ __launch_bounds__(512) void tmu_einsum_large_kernel(const T* __restri
 // ~2.4 / ~0.6 us per 256 x 256 tile, against ~32 us of k-loop at L = 1024).  The first k-step of
 // a tile starts from zero accumulators.  Requires L % 256 == 0 (no row of a block tile lies past
 // L) and an even k-tile count (two static stages per tile); with gridDim.x a multiple of 8 block
-// tile t stays on XCD t % 8 under the XCD-major tile order.
+// tile t stays on XCD t % 8 under the XCD-major tile order.  A k-tile's copy is issued in two
+// halves, the A operand right after the barrier and the B operand after the k-step that follows
+// (one burst of all eight copy instructions per wave measured 2 % / 6 % slower at L = 1024 / 2048;
+// quarters spread further, into the next k-tile, leave the late ones too little time).
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
@@ -673,7 +676,8 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
     abase = reinterpret_cast<const char*>(A + (slab * L + (int64_t)tm * BM) * ld);
     bbase = reinterpret_cast<const char*>(Bmat + (slab * L + (int64_t)tn * BM) * ld);
   };
-  auto gload = [&](int kt, auto S) {
+  // operand part: 0 = A, 1 = B, 2 = both
+  auto gload = [&](int kt, auto S, int part = 2) {
     const char* ak = abase + (int64_t)kt * BK * sizeof(T);
     const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
     const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 4 * 1024);
@@ -681,8 +685,8 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t va = aoff[j], vb = boff[j], ma = as + 1024 * j, mb = bs + 1024 * j;
-      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
-      asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
+      if (part != 1) asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(ak), "{m0}"(ma) : "memory");
+      if (part != 0) asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(vb), "s"(bk), "{m0}"(mb) : "memory");
     }
   };
   struct Frags {
@@ -735,15 +739,19 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
     frags(S, 3, fb);
     interleave();
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // the copy of k-tile kt + 2 into the stage just drained: A now, B after this k-step's MFMAs
+    int lk = -1;
     if (kt + 2 < nk) {
-      gload(kt + 2, S);
+      lk = kt + 2;
     } else if (has_next) {  // the next block tile's k-tiles 0 and 1
       if (kt + 2 == nk) setup(t + G);
-      gload(kt + 2 - nk, S);
+      lk = kt + 2 - nk;
     }
+    if (lk >= 0) gload(lk, S, 0);
     mfmas(fb, NO{});
     frags(N{}, 0, fa);  // after the block's last k-tile: stale contents, never used
     interleave();
+    if (lk >= 0) gload(lk, S, 1);
   };
 
   setup(t);
