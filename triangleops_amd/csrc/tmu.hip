@@ -960,7 +960,8 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
       const int64_t rowbase = g.b * L + g.r;
       const T* ysrc = y + rowbase * ldy + g.c0 + 8 * tg;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sg.y[r] = ldg<V8>(ysrc + (int64_t)(4 * cq + r) * cstride);
+      for (int r = 0; r < 4; ++r)  // y is read once: non-temporal, so it does not displace x in the caches
+        sg.y[r] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(ysrc + (int64_t)(4 * cq + r) * cstride));
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int ci = k * NL + tid;  // token ci / 16, chunk ci % 16
