@@ -20,7 +20,10 @@ Prints ONE JSON line with the contract fields plus:
                 ms per call, per-kernel figures, the dominant kernel's roofline (the attention
                 kernel's MFMA fraction; apb's HBM fraction), the torch path on the same GPU and
                 its own CPU baseline (the fp32 oracle; triangle attention timed on sampled rows
-                and scaled, rows being independent).
+                and scaled, rows being independent);
+  config0       BASELINE.json configs[0], the reference's CPU-runnable case (tmu outgoing,
+                L = 128, all-ones mask): ms per call with bf16 and fp32 I/O and the fp32 oracle's
+                calls/s on the host.
 `--sweep FILE` additionally times all three ops, the apb qk-norm variant and a Pairformer pair stack at sizes 128..2048 (ours, the torch path and
 per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
 """
@@ -514,6 +517,28 @@ def cpu_baseline_tmu(x, m, w, L, min_s=10.0):
             "sample": f"{calls} full outgoing call(s) at L={L} (fp32 torch oracle), {dt:.1f} s"}
 
 
+def config0_entry(dev, cpu):
+    """BASELINE configs[0], the reference's CPU-runnable case: triangle_multiplicative_update
+    outgoing at L = 128 with an all-ones mask (the seed-0 inputs of tmu_inputs).  The HIP path's ms
+    per call with bf16 and with fp32 I/O (the config's dtype, on the any-shape fp32 path) beside the
+    fp32 oracle on the host cores, whole calls on the same inputs."""
+    L = 128
+    x_c, _, w_c = tmu_inputs(L)
+    m_c = torch.ones(1, L, L, dtype=torch.bool)
+    x, m = x_c.to(dev), m_c.to(dev)
+    e = {"workload": f"triangle_multiplicative_update outgoing, L={L}, C={C}, B=1, all-ones mask"}
+    w = {k: v.to(dev) for k, v in w_c.items()}
+    pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+    e["ms_per_call_bf16"] = round(time_ms(lambda: tops.triangle_mul.forward(x, pre, direction="outgoing", mask=m),
+                                          50, 10), 4)
+    xf, wf = x.float(), {k: v.float() for k, v in w.items()}
+    pref = tops.triangle_mul.precompute(*[wf[k] for k in TMU_KEYS])
+    e["ms_per_call_fp32"] = round(time_ms(lambda: tops.triangle_mul.forward(xf, pref, direction="outgoing", mask=m),
+                                          50, 10), 4)
+    e["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L, min_s=5.0) if cpu else None
+    return e
+
+
 def cpu_baseline_tri(d, N, min_s=8.0):
     """fp32 oracle triangle attention on sampled rows: rows are independent, so a call over R rows
     costs a + b R (a: LayerNorm and pair bias of the whole grid, b: one row's projections, attention
@@ -978,6 +1003,7 @@ def main():
             "triangle_attention": op_entry_tri(args.ops_size, dev, 10, 3, cpu),
             "attention_pair_bias": op_entry_apb(args.ops_size, dev, 20, 5, cpu),
         }
+        out["config0"] = config0_entry(dev, cpu)
     if args.sweep:
         sweep(args.sweep, [int(s) for s in args.sweep_sizes.split(",")], dev)
     out["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L) if cpu else None
