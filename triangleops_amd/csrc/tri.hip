@@ -77,7 +77,10 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];    // normalised x tiles
   __shared__ __attribute__((aligned(16))) char os[H][3 * PART];   // per writer wave: Q | K | V^T
-  __shared__ __attribute__((aligned(16))) T bs[2][H * 64];         // pair bias [head][position]
+  // pair bias [head][position]: head rows 72 elements apart (dword banks 0 / 36 / 8 / 44), so the
+  // four heads' stores of a pass fall in distinct banks
+  constexpr int BSR = 72;
+  __shared__ __attribute__((aligned(16))) T bs[2][H * BSR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t nkb = ldn / 64, nkt = ldn / 32, nqt = (N + 31) / 32;
@@ -130,8 +133,8 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = (v[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e];
         }
-        // pair bias of the 4 heads (fp32 dot products); lanes ch, ch + 4, ... all store head
-        // ch & 3 (the same value), keeping the loop free of divergent branches
+        // pair bias of the 4 heads (fp32 dot products); lanes ch, ch + 4, ... all hold head ch & 3,
+        // and lane ch < 4 stores it
         float bsel = 0.f;
 #pragma unroll
         for (int hh = 0; hh < H; ++hh) {
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
           d = group_sum<LPT>(d);
           bsel = (ch & 3) == hh ? d : bsel;
         }
-        bs[bb][(ch & 3) * 64 + tk] = valid ? (T)((bsel + bz) * bias_scale) : (T)0.f;
+        if (ch < 4) bs[bb][ch * BSR + tk] = valid ? (T)((bsel + bz) * bias_scale) : (T)0.f;
         V8 o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (T)v[e];
@@ -254,7 +257,7 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
         const int g = lane;
         const uint64_t off = (((uint64_t)h * nqt + i / 32) * nkt + 2 * kb + (g >> 2)) * 1024 +
                              (((g >> 1) & 1) * 64 + (g & 1) * 32 + (i & 31)) * 8;
-        stg<V8>(bias + off, *reinterpret_cast<const V8*>(&bs[bb][h * 64 + 8 * g]));
+        stg<V8>(bias + off, *reinterpret_cast<const V8*>(&bs[bb][h * BSR + 8 * g]));
       }
       bb ^= 1;
     }
