@@ -23,7 +23,11 @@ Prints ONE JSON line with the contract fields plus:
                 and scaled, rows being independent);
   config0       BASELINE.json configs[0], the reference's CPU-runnable case (tmu outgoing,
                 L = 128, all-ones mask): ms per call with bf16 and fp32 I/O and the fp32 oracle's
-                calls/s on the host.
+                calls/s on the host;
+  size_sweep    the metric's other config sizes (tmu L = 512, 2048; triangle attention N = 256,
+                512, 2048; apb M = 128, 512, 2048): ms per call, the dominant kernel's roofline
+                fraction, every kernel's ms and fraction, the torch path on the same GPU, and the
+                HIP-graph replay time at sizes <= 512.
 `--sweep FILE` additionally times all three ops, the apb qk-norm variant and a Pairformer pair stack at sizes 128..2048 (ours, the torch path and
 per-kernel roofline fractions) and writes one JSON line per (op, size) to FILE.
 """
@@ -593,7 +597,7 @@ def op_entry_tri(N, dev, iters, warmup, cpu):
     e = {"config": f"triangle_attention bf16, N={N}, H={H}, D={D}, C={C}, pad mask (last 10% rows/cols)",
          "ms_per_call": round(ms, 4), "ms_per_call_ending_node": round(ms_end, 4), "calls_per_s": round(1e3 / ms, 2),
          "roofline": {"kernel": "tri_attention", "bound": "mfma", "achieved": ka["achieved"], "peak": ka["peak"],
-                      "unit": ka["unit"], "frac": ka["frac"], "traffic": None},
+                      "unit": ka["unit"], "frac": ka["frac"], "traffic": measured_traffic("tri_attention", N)},
          "kernels": kern}
     e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), 3, 1), 4)
     del d, pre
@@ -619,13 +623,99 @@ def op_entry_apb(M, dev, iters, warmup, cpu):
     e = {"config": f"attention_pair_bias bf16, M={M}, H={H}, D={D}, C_s=C_z={C}, key mask (last 5% padded)",
          "ms_per_call": round(ms, 4), "calls_per_s": round(1e3 / ms, 2),
          "roofline": {"kernel": "apb_attention (apb_attn_kernel)", "bound": "hbm", "achieved": ka["achieved"], "peak": ka["peak"],
-                      "unit": ka["unit"], "frac": ka["frac"], "traffic": None},
+                      "unit": ka["unit"], "frac": ka["frac"], "traffic": measured_traffic("apb_attention", M)},
          "kernels": kern}
     e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)
     del d, pre
     torch.cuda.empty_cache()
     e["cpu_baseline"] = cpu_baseline_apb(d_c, M) if cpu else None
     return e
+
+
+SIZE_SWEEP = {"triangle_multiplicative_update": (512, 2048), "triangle_attention": (256, 512, 2048),
+              "attention_pair_bias": (128, 512, 2048)}
+
+
+def _compact(kern):
+    """The dominant kernel of a call (largest average time) and every kernel's ms and roofline fraction."""
+    dom = max(kern, key=lambda n: kern[n]["ms"])
+    return {"dominant": dom, "frac": kern[dom]["frac"], "bound": kern[dom]["bound"],
+            "kernels": {n: {"ms": k["ms"], "frac": k["frac"]} for n, k in kern.items()}}
+
+
+def size_sweep_entries(dev):
+    """BASELINE.json's metric across its config sizes other than the 1024 entries above (tmu
+    L = 512, 2048; triangle attention N = 256, 512, 2048; apb M = 128, 512, 2048): per op and size the
+    ms per call (both directions / nodes), the dominant kernel's roofline fraction, every kernel's
+    ms and fraction, the reference's torch path on the same GPU (NaN = out of memory), and at sizes
+    <= 512 the same call replayed as one HIP graph (host launch overhead removed)."""
+    out = []
+    for L in SIZE_SWEEP["triangle_multiplicative_update"]:
+        torch.cuda.empty_cache()
+        x, m, w = tmu_inputs(L)
+        x, m, w = x.to(dev), m.to(dev), {k: v.to(dev) for k, v in w.items()}
+        pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+        it, wu = (20, 5) if L <= 1024 else (8, 3)
+        e = {"op": "triangle_multiplicative_update", "size": L}
+        for direction in ("outgoing", "incoming"):
+            e[f"ms_per_call_{direction}"] = round(time_ms(
+                lambda: tops.triangle_mul.forward(x, pre, direction=direction, mask=m), it, wu), 4)
+        work = tmu_work(L)
+        ph = run_phases([tmu_phases(x, m, pre, "outgoing"), tmu_phases(x, m, pre, "incoming")], list(work), it, wu)
+        e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
+        e["torch_path_ms"] = round(time_ms(lambda: torch_tmu(x, "outgoing", m, **w), 5 if L <= 1024 else 3, 1), 4)
+        if L <= 512:
+            e["ms_graph"] = round(graph_ms(lambda xx: tops.triangle_mul.forward(xx, pre, direction="outgoing",
+                                                                                mask=m), x), 4)
+        out.append(e)
+        print(f"size sweep: tmu L={L} done", file=sys.stderr, flush=True)
+        del x, m, w, pre
+    for N in SIZE_SWEEP["triangle_attention"]:
+        torch.cuda.empty_cache()
+        d = to_dev(tri_inputs(N), dev)
+        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                            d["B_proj_z"], H, D)
+        kw = dict(scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None)
+        it, wu = (20, 5) if N <= 1024 else (6, 2)
+        e = {"op": "triangle_attention", "size": N,
+             "ms_per_call": round(time_ms(lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], **kw), it,
+                                          wu), 4),
+             "ms_per_call_ending_node": round(time_ms(lambda: tops.triangle_attn.forward(
+                 d["X"].transpose(0, 1), pre, mask=d["mask"].T, **kw), it, wu), 4)}
+        work = tri_work(N)
+        ph = run_phases([tri_phases(d, pre)], list(work), it, wu)
+        e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
+        # N = 2048: the (N, H, N, N) bf16 scores are 64 GiB per intermediate; timed once after one
+        # warmup call (out of memory is reported as NaN, not skipped)
+        e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), 3 if N <= 1024 else 1, 1), 4)
+        torch.cuda.empty_cache()
+        if N <= 512:
+            e["ms_graph"] = round(graph_ms(lambda X: tops.triangle_attn.forward(X, pre, mask=d["mask"], **kw),
+                                           d["X"]), 4)
+        out.append(e)
+        print(f"size sweep: tri N={N} done", file=sys.stderr, flush=True)
+        del d, pre
+    for M in SIZE_SWEEP["attention_pair_bias"]:
+        torch.cuda.empty_cache()
+        d = to_dev(apb_inputs(M), dev)
+        pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                             d["B_proj_z"], H, D)
+        kw = dict(scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"],
+                  B_proj_o=d["B_proj_o"], mask=d["mask"])
+        e = {"op": "attention_pair_bias", "size": M,
+             "ms_per_call": round(time_ms(lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, **kw), 20, 5), 4)}
+        work = apb_work(M)
+        ph = run_phases([apb_phases(d, pre)], list(work), 20, 5)
+        e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
+        e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)
+        if M <= 512:
+            e["ms_graph"] = round(graph_ms(lambda X, Z: tops.attn_pair_bias.forward(X, Z, pre, **kw), d["X"], d["Z"]),
+                                  4)
+        out.append(e)
+        print(f"size sweep: apb M={M} done", file=sys.stderr, flush=True)
+        del d, pre
+    torch.cuda.empty_cache()
+    return out
 
 
 # --------------------------------------------------------------------------- #
@@ -824,27 +914,65 @@ def sweep(path, sizes, dev):
     return rows
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "tmu_L1024_hbm_traffic.md")
+TRAFFIC_PROFILES = [os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f)
+                    for f in ("tmu_L1024_hbm_traffic.md", "ops_1024_hbm_traffic.md")]
 
 
-def measured_traffic(kernel, L):
-    """HBM bytes per launch of `kernel` at the default workload, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known size); None otherwise."""
-    if L != 1024 or not os.path.exists(TRAFFIC_PROFILE):
+def measured_traffic(kernel, n):
+    """HBM bytes per launch of `kernel` at size 1024, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summaries (calibrated against a copy of known size); None otherwise."""
+    if n != 1024:
         return None
-    for line in open(TRAFFIC_PROFILE):
-        cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) >= 5 and cells[0] == kernel:
-            try:
-                return int(cells[4])
-            except ValueError:
-                return None
+    for path in TRAFFIC_PROFILES:
+        if not os.path.exists(path):
+            continue
+        for line in open(path):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) >= 5 and cells[0] == kernel:
+                try:
+                    return int(cells[4])
+                except ValueError:
+                    return None
     return None
 
 
-def traffic_run(L):
-    """Workload for the HBM-traffic counter runs (no timing): a 256 MiB bf16 negation whose bytes
-    are known (calibration), then two default steps (outgoing + incoming)."""
+def _op_call(op, n, dev):
+    """One call of an op at size n on seeded inputs (`tri`: starting-node triangle attention; `tri_apo`:
+    the same at the Apo shape C_in = 64, H = 4, D = 16; `apb`: attention_pair_bias; `tmu`: outgoing
+    tmu; `tmu2`: outgoing then incoming tmu)."""
+    if op == "tri_apo":
+        d = to_dev(tri_inputs_shape(n, 64, 4, 16), dev)
+        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                            d["B_proj_z"], 4, 16)
+        return lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=16**-0.5,
+                                                  W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
+                                                  B_proj_o=None)
+    if op == "tri":
+        d = to_dev(tri_inputs(n), dev)
+        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                            d["B_proj_z"], H, D)
+        return lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=D**-0.5,
+                                                  W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
+                                                  B_proj_o=None)
+    if op == "apb":
+        d = to_dev(apb_inputs(n), dev)
+        pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                             d["B_proj_z"], H, D)
+        return lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5, W_proj_g=d["W_proj_g"],
+                                                   B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"],
+                                                   B_proj_o=d["B_proj_o"], mask=d["mask"])
+    x_c, m_c, w_c = tmu_inputs(n)
+    x, m = x_c.to(dev), m_c.to(dev)
+    w = {k: v.to(dev) for k, v in w_c.items()}
+    pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+    dirs = ("outgoing", "incoming") if op == "tmu2" else ("outgoing",)
+    return lambda: [tops.triangle_mul.forward(x, pre, direction=dd, mask=m) for dd in dirs]
+
+
+def traffic_run(n, op="tmu2"):
+    """Workload of the HBM-traffic counter runs (no timing): a 256 MiB bf16 negation whose bytes are
+    known (calibration), then two calls of `op` at size n (default: two tmu steps, outgoing +
+    incoming; `tri` / `apb`: two calls of triangle attention / attention_pair_bias)."""
     dev = torch.device("cuda:0")
     src = torch.randn(128 * 1024 * 1024, device=dev).to(torch.bfloat16)
     dst = torch.empty_like(src)
@@ -852,49 +980,16 @@ def traffic_run(L):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
-    x_c, m_c, w_c = tmu_inputs(L)
-    x, m = x_c.to(dev), m_c.to(dev)
-    w = {k: v.to(dev) for k, v in w_c.items()}
-    pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
+    fn = _op_call(op, n, dev)
     for _ in range(2):
-        for d in ("outgoing", "incoming"):
-            tops.triangle_mul.forward(x, pre, direction=d, mask=m)
+        fn()
     torch.cuda.synchronize()
-    print("traffic run done", flush=True)
+    print(f"traffic run {op} n={n} done", flush=True)
 
 
 def op_run(op, n):
-    """Workload of the counter runs (no timing): 5 calls of one op at size n after 2 warmup calls
-    (`tri`: starting-node triangle attention; `tri_apo`: the same at the Apo shape C_in = 64, H = 4,
-    D = 16; `apb`: attention_pair_bias; `tmu`: outgoing tmu)."""
-    dev = torch.device("cuda:0")
-    if op == "tri_apo":
-        d = to_dev(tri_inputs_shape(n, 64, 4, 16), dev)
-        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
-                                            d["B_proj_z"], 4, 16)
-        fn = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=16**-0.5,  # noqa: E731
-                                                W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
-                                                B_proj_o=None)
-    elif op == "tri":
-        d = to_dev(tri_inputs(n), dev)
-        pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
-                                            d["B_proj_z"], H, D)
-        fn = lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], scale=D**-0.5,  # noqa: E731
-                                                W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"],
-                                                B_proj_o=None)
-    elif op == "apb":
-        d = to_dev(apb_inputs(n), dev)
-        pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
-                                             d["B_proj_z"], H, D)
-        fn = lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, scale=D**-0.5,  # noqa: E731
-                                                 W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"],
-                                                 W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"], mask=d["mask"])
-    else:
-        x_c, m_c, w_c = tmu_inputs(n)
-        x, m = x_c.to(dev), m_c.to(dev)
-        w = {k: v.to(dev) for k, v in w_c.items()}
-        pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
-        fn = lambda: tops.triangle_mul.forward(x, pre, direction="outgoing", mask=m)  # noqa: E731
+    """Workload of the counter runs (no timing): 7 calls of one op at size n (see _op_call)."""
+    fn = _op_call(op, n, torch.device("cuda:0"))
     for _ in range(7):
         fn()
     torch.cuda.synchronize()
@@ -913,10 +1008,13 @@ def main():
     ap.add_argument("--no-torch", action="store_true", help="skip the torch-path reference timing")
     ap.add_argument("--no-ops", action="store_true", help="skip the triangle_attention / attention_pair_bias entries")
     ap.add_argument("--ops-size", type=int, default=1024, help="N = M of the triangle_attention / apb entries")
+    ap.add_argument("--no-size-sweep", action="store_true",
+                    help="skip the compact per-size entries (tmu 512/2048, tri 256/512/2048, apb 128/512/2048)")
     ap.add_argument("--op-run", choices=("tri", "tri_apo", "apb", "tmu"), default=None,
                     help="only run 7 calls of one op at --size (workload of rocprofv3 counter runs)")
-    ap.add_argument("--traffic-run", action="store_true",
-                    help="only run the workload of the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic-run", nargs="?", const="tmu2", default=None, choices=("tmu2", "tri", "apb"),
+                    help="only run the workload of the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE): tmu2 (default, two tmu steps), tri or apb at --size")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -929,7 +1027,7 @@ def main():
     dev = torch.device("cuda:0")
     L = args.size
     if args.traffic_run:
-        traffic_run(L)
+        traffic_run(L, args.traffic_run)
         return
     if args.op_run:
         op_run(args.op_run, L)
@@ -1004,6 +1102,8 @@ def main():
             "attention_pair_bias": op_entry_apb(args.ops_size, dev, 20, 5, cpu),
         }
         out["config0"] = config0_entry(dev, cpu)
+    if not args.no_size_sweep:
+        out["size_sweep"] = size_sweep_entries(dev)
     if args.sweep:
         sweep(args.sweep, [int(s) for s in args.sweep_sizes.split(",")], dev)
     out["cpu_baseline"] = cpu_baseline_tmu(x_c, m_c, w_c, L) if cpu else None

@@ -186,14 +186,26 @@ def test_tmu_precompute_forward_matches_oneshot(device):
 
 @pytest.mark.parametrize("L", [512, 1024])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-def test_tmu_config_sizes_sampled_rows(device, L, direction):
-    """BASELINE config 1 sizes (pad mask), checked on 6 sampled output rows."""
+def test_tmu_config_sizes_whole_output(device, L, direction):
+    """BASELINE config 1 sizes (pad mask): the whole output against the fp32 oracle."""
     x, m, w = tmu_inputs(L, seed=0, mask="pad")
     out = tops.triangle_multiplicative_update(to_dev(x, device), direction=direction, mask=m.to(device),
+                                              **to_dev(w, device)).cpu()
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.bfloat16, f"tmu L={L} {direction}")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_tmu_fp16_large_offset(device, direction):
+    """fp16 tokens with a large common offset (x = 300 + N(0, 0.5), quantised to 0.25): the
+    LayerNorm statistics must not cancel (E[x^2] - mean^2 in fp32 would lose the variance)."""
+    x, m, w = tmu_inputs(64, seed=31, mask="random", dtype=torch.float32)
+    x = (300.0 + 0.5 * x).to(torch.float16)
+    w = {k: v.to(torch.float16) for k, v in w.items()}
+    out = tops.triangle_multiplicative_update(x.to(device), direction=direction, mask=m.to(device),
                                               **to_dev(w, device))
-    rows = torch.tensor([0, 1, L // 3, L // 2, L - L // 10 - 1, L - 1])
-    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, rows=rows, **w)
-    _check(out[:, rows].cpu(), expect, torch.bfloat16, f"tmu L={L} {direction}")
+    expect = ref.triangle_multiplicative_update(x, direction=direction, mask=m, **w)
+    _check(out, expect, torch.float16, f"tmu fp16 offset {direction}")
 
 
 @pytest.mark.parametrize("L,nslab,dtype", [(400, 8, torch.bfloat16), (600, 64, torch.bfloat16),
@@ -325,18 +337,68 @@ def test_tri_low_level_entry_points(device):
     _check(out, _tri_ref(to_dev(inp, "cpu")), torch.bfloat16, "tri low-level")
 
 
+def _config_rows(n, k=32):
+    """k rows spread over [0, n) plus the last valid / first padded row of the pad mask."""
+    v = n - n // 10
+    return torch.unique(torch.cat([torch.linspace(0, n - 1, k).round().long(), torch.tensor([v - 1, v])]))
+
+
 @pytest.mark.parametrize("N", [512, 1024, 2048])
-def test_tri_config_sizes_sampled_rows(device, N):
-    """BASELINE configs 3/4 sizes (pad mask): starting and ending node on sampled rows."""
+def test_tri_config_sizes(device, N):
+    """BASELINE configs 3/4 sizes (pad mask), starting and ending node: the whole output at
+    N <= 1024; at 2048 (8-wave blocks) 34 rows spread over the grid, every query of each."""
     inp = tri_inputs(N, seed=0, mask="pad")
+    rows = None if N <= 1024 else _config_rows(N)
     out = _tri_call(inp, device)
-    rows = torch.tensor([0, N // 2, N - N // 10 - 1, N - 1])
-    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} start")
+    out = (out if rows is None else out[rows.to(device)]).cpu()
+    _check(out, _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} start")
     del out
     Xd = inp["X"].to(device)
     out_e = _tri_call(inp, device, X=Xd.transpose(0, 1), mask=inp["mask"].to(device).T)
+    out_e = (out_e if rows is None else out_e[rows.to(device)]).cpu()
     exp_e = _tri_ref(inp, X=inp["X"].transpose(0, 1), mask=inp["mask"].T, rows=rows)
-    _check(out_e[rows].cpu(), exp_e, torch.bfloat16, f"tri N={N} end")
+    _check(out_e, exp_e, torch.bfloat16, f"tri N={N} end")
+
+
+def test_tri_padded_heads_not_multiple_of_8(device):
+    """Heads of D = 12 (not a multiple of 8) in bf16 run the MFMA attention kernel on 32-wide zero-padded
+    heads written to a scratch output whose first D columns of each head are kept."""
+    inp = tri_inputs(130, C=48, H=4, D=12, seed=12, mask="random", bias_z=True)
+    _check(_tri_call(inp, device), _tri_ref(inp), torch.bfloat16, "tri D=12")
+
+
+@pytest.mark.parametrize("N,shift", [(200, 150.0), (200, -200.0), (520, 150.0), (2100, -200.0)])
+def test_tri_shift_free_softmax_fallback(device, N, shift):
+    """bf16 triangle attention takes the weights as 2^s without the row max and recomputes a wave's
+    query tiles with an exact running max when its row sums leave [2^-60, 2^100].  Softmax is
+    shift-invariant, so adding a constant to every score of a (head, query tile) must leave its
+    output unchanged.  The pre-pass bias tiles (log2 units) are rounded to integers, which bf16 holds
+    exactly up to 256, and head 0's tiles (every query tile) and head 2's tiles of query tiles 2 and 3
+    are shifted by +150 (the shift-free weights overflow) or -200 (they underflow): those heads must
+    match the unshifted run to the bf16 bar, while heads 1 and 3, which run the shift-free path in the
+    same launch, must match it bitwise.  N = 2100 runs the 8-wave blocks."""
+    from triangleops_amd.triangle_attn.kernel import attention_core, prep_forward
+
+    inp = to_dev(tri_inputs(N, seed=N + 7, mask="random", bias_z=True), device)
+    pre = tops.triangle_attn.precompute(inp["W_ln"], inp["B_ln"], inp["WQ"], inp["WK"], inp["WV"], inp["W_proj_z"],
+                                        inp["B_proj_z"], 4, 32)
+    Qp, KV, bias, ldn = prep_forward(inp["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"],
+                                     scale=inp["scale"])
+    b0 = bias.float().round()
+    b1 = b0.clone()
+    b1[0] += shift
+    b1[2, 2:4] += shift
+    assert b1.abs().max().item() < 256
+    outs = []
+    for b in (b0, b1):
+        o = torch.empty(N, N, 128, device=device, dtype=torch.bfloat16)
+        attention_core(Qp, KV, b.to(torch.bfloat16), o, N=N, ldn=ldn, mask=inp["mask"])
+        outs.append(o.view(N, N, 4, 32).cpu())
+    a, b = outs
+    assert torch.isfinite(b.float()).all(), "non-finite output after the fallback"
+    assert torch.equal(a[:, :, 1], b[:, :, 1]) and torch.equal(a[:, :, 3], b[:, :, 3])
+    for h in (0, 2):
+        _check(b[:, :, h], a[:, :, h].float(), torch.bfloat16, f"tri fallback N={N} shift={shift} head {h}")
 
 
 @pytest.mark.parametrize("N", [100, 384])
@@ -792,11 +854,48 @@ def test_apb_qknorm_first_key_masked(device, M, shape, dtype):
 
 
 @pytest.mark.parametrize("M", [1024, 2048])
-def test_apb_config_sizes_sampled_rows(device, M):
+def test_apb_config_sizes(device, M):
+    """BASELINE config 2 sizes (key padding mask): the whole output against the fp32 oracle."""
     inp = apb_inputs(M, seed=0, mask="pad")
-    out = _apb_call(inp, device)
-    rows = torch.tensor([0, 1, M // 2, M - M // 20 - 1, M - 1])
-    _check(out[rows].cpu(), _apb_ref(inp, rows=rows), torch.bfloat16, f"apb M={M}")
+    _check(_apb_call(inp, device).cpu(), _apb_ref(inp), torch.bfloat16, f"apb M={M}")
+
+
+@pytest.mark.parametrize("M", [200, 1024])
+@pytest.mark.parametrize("residual", [False, True])
+def test_apb_column_sliced_inputs(device, M, residual):
+    """X, the residual and W_g as column slices of wider tensors (row stride 256, not dense): the
+    kernels that index them without strides must get dense copies.  Through forward() (the gated
+    path at the tuned shape), against the fp32 oracle (+ residual)."""
+    inp = apb_inputs(M, seed=M + 3, mask="pad", biases=True)
+    d = to_dev(inp, device)
+    g = torch.Generator().manual_seed(M)
+    wide_x = torch.randn(M, 256, generator=g).to(torch.bfloat16).to(device)
+    wide_x[:, :128] = d["X"]
+    wide_g = torch.randn(128, 256, generator=g).to(torch.bfloat16).to(device)
+    wide_g[:, :128] = d["W_proj_g"]
+    X, W_g = wide_x[:, :128], wide_g[:, :128]
+    assert not X.is_contiguous() and not W_g.is_contiguous()
+    res_cpu = torch.randn(M, 128, generator=g).to(torch.bfloat16)
+    res = None
+    if residual:
+        wide_r = torch.randn(M, 256, generator=g).to(torch.bfloat16).to(device)
+        wide_r[:, 128:] = res_cpu.to(device)
+        res = wide_r[:, 128:]
+    pre = tops.attn_pair_bias.precompute(d["WQ"], d["WK"], d["WV"], d["W_ln"], d["B_ln"], d["W_proj_z"],
+                                         d["B_proj_z"], 4, 32)
+    out = tops.attn_pair_bias.forward(X, d["Z"], pre, scale=d["scale"], W_proj_g=W_g, B_proj_g=d["B_proj_g"],
+                                      W_proj_o=d["W_proj_o"], B_proj_o=d["B_proj_o"], mask=d["mask"], residual=res)
+    expect = _apb_ref(inp)
+    if not residual:
+        _check(out.cpu(), expect, torch.bfloat16, f"apb sliced M={M}")
+        return
+    # residual + result rounded once in bf16: the bar plus half a bf16 step of the sum
+    expect = expect + res_cpu.float()
+    e = expect.double()
+    ulp = torch.exp2(torch.floor(torch.log2(e.abs().clamp_min(1e-30))) - 7)  # bf16 step at |expect|
+    diff = ((out.cpu().double() - e).abs() - 0.5 * ulp).max().item()
+    cos = torch.nn.functional.cosine_similarity(out.cpu().double().flatten(), expect.double().flatten(), dim=0).item()
+    assert diff <= TOL_MAX_ABS[torch.bfloat16] and cos >= TOL_COS, f"apb sliced M={M} residual: {diff:.3e} {cos:.6f}"
 
 
 # --------------------------------------------------------------------------- #

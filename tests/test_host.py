@@ -290,6 +290,25 @@ def test_vec16_copies_misaligned_views():
     assert _native.vec16_ok(t) and _native.vec16(t).data_ptr() == t.data_ptr()
 
 
+def test_dense_copies_strided_and_misaligned_views():
+    """dense(): the tensors the kernels index without strides are made dense and 16-byte aligned.
+    A column slice (row stride 256, unit last stride) passes vec16_ok but is not dense."""
+    wide = torch.arange(64 * 256, dtype=torch.float32).reshape(64, 256).to(torch.bfloat16)
+    s = wide[:, :128]
+    assert _native.vec16_ok(s) and not s.is_contiguous()
+    d = _native.dense(s)
+    assert d.is_contiguous() and d.data_ptr() % 16 == 0 and torch.equal(d, s)
+    flat = torch.zeros(1000, dtype=torch.bfloat16)
+    mis = flat[1:129]
+    assert mis.is_contiguous() and mis.data_ptr() % 16 != 0
+    assert _native.dense(mis).data_ptr() % 16 == 0
+    ok = torch.zeros(64, 128, dtype=torch.bfloat16)
+    assert _native.dense(ok).data_ptr() == ok.data_ptr()
+    f = _native.dense(ok, torch.float32)
+    assert f.dtype == torch.float32 and f.is_contiguous()
+    assert _native.dense(None) is None
+
+
 @pytest.mark.skipif(not os.path.exists(_native.LIB_PATH), reason="HIP library not built")
 def test_apb_noalloc_rejects_oversized_call_cpu():
     """tops_apb_forward_noalloc refuses a call whose workspace exceeds its 16 MiB static array before

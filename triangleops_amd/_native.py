@@ -165,8 +165,21 @@ def vec16_ok(t: torch.Tensor) -> bool:
 
 def vec16(t: torch.Tensor) -> torch.Tensor:
     """`t` itself when vec16_ok(t), else a fresh contiguous copy (which is 16-byte aligned;
-    `.contiguous()` alone would return a contiguous but misaligned view unchanged)."""
+    `.contiguous()` alone would return a contiguous but misaligned view unchanged).  Only for
+    tensors whose strides are passed to the kernel; see `dense` for the others."""
     return t if vec16_ok(t) else t.clone(memory_format=torch.contiguous_format)
+
+
+def dense(t: torch.Tensor | None, dtype: torch.dtype | None = None) -> torch.Tensor | None:
+    """`t` (cast to `dtype` if given) as a dense row-major tensor with a 16-byte aligned base:
+    itself when it already is one, else a fresh contiguous copy.  For every tensor the kernels
+    index without strides (activations such as X or a residual, weights, bias vectors): a
+    column slice such as S[:, :128] of a wider tensor is not dense and is copied."""
+    if t is None:
+        return None
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t if (t.is_contiguous() and t.data_ptr() % 16 == 0) else t.clone(memory_format=torch.contiguous_format)
 
 
 def mask_i8(mask: torch.Tensor | None) -> torch.Tensor | None:

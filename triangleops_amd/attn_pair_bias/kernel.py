@@ -33,19 +33,18 @@ def apb_forward(X, W_QKV, Z, W_combined, sum_W_combined, B_const, Og, scale=1.0,
         return _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm, H, D)
     code = io_dtype_code(X.dtype)
     _native.check_device(X, W_QKV, Z, W_combined, Og, mask)
-    X = _native.vec16(X)
-    Z = _native.vec16(Z)
+    X = _native.dense(X)  # the kernels index X rows without a stride
+    Z = _native.vec16(Z)  # Z's strides are passed
     if wqkv_hm is None:
         wqkv_hm = wqkv_from_interleaved(W_QKV, H, D)
-    if wqkv_hm.dtype != X.dtype:
-        wqkv_hm = wqkv_hm.to(X.dtype)
-    Wc = W_combined.float().contiguous()
-    sWc = sum_W_combined.float().contiguous()
-    Bc = B_const.float().contiguous()
+    wqkv_hm = _native.dense(wqkv_hm, X.dtype)
+    Wc = _native.dense(W_combined, torch.float32)
+    sWc = _native.dense(sum_W_combined, torch.float32)
+    Bc = _native.dense(B_const, torch.float32)
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
-    assert Og.is_contiguous()
+    assert Og.is_contiguous() and Og.data_ptr() % 16 == 0, "Og must be contiguous and 16-byte aligned"
     nbytes = _native.apb_workspace_bytes(M, H, D)
     work = torch.empty(max(nbytes, 1), device=X.device, dtype=torch.uint8) if nbytes else None
     _native.call(
@@ -96,14 +95,14 @@ def apb_forward_gated(X, Z, W_combined, sum_W_combined, B_const, wqkv_hm, W_g, b
     assert gated_ok(X, Z, W_combined, W_g, W_o, residual) and D == 32
     code = io_dtype_code(X.dtype)
     _native.check_device(X, Z, wqkv_hm, W_combined, W_g, W_o, mask, residual)
-    X = _native.vec16(X)
-    Z = _native.vec16(Z)
+    X = _native.dense(X)  # X, the weights, biases and residual are indexed without strides
+    Z = _native.vec16(Z)  # Z's strides are passed
     dt = X.dtype
-    cast = lambda t: None if t is None else _native.vec16(t.to(dt))  # noqa: E731  (contiguous, 16-byte aligned)
+    cast = lambda t: _native.dense(t, dt)  # noqa: E731  (dense rows, 16-byte aligned)
     wqkv_hm = cast(wqkv_hm)
-    Wc = W_combined.float().contiguous()
-    sWc = sum_W_combined.float().contiguous()
-    Bc = B_const.float().contiguous()
+    Wc = _native.dense(W_combined, torch.float32)
+    sWc = _native.dense(sum_W_combined, torch.float32)
+    Bc = _native.dense(B_const, torch.float32)
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
@@ -141,20 +140,18 @@ def _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm
     Cz = Z.shape[2]
     code = any_shape_dtype_code(X.dtype)
     _native.check_device(X, W_QKV, Z, W_combined, Og, mask)
-    X = X if X.is_contiguous() else X.contiguous()
+    X = _native.dense(X)
     if Z.stride(2) != 1:
         Z = Z.contiguous()
     if wqkv_hm is None:
         wqkv_hm = wqkv_from_interleaved(W_QKV, H, D)
-    if wqkv_hm.dtype != X.dtype:
-        wqkv_hm = wqkv_hm.to(X.dtype)
-    wqkv_hm = wqkv_hm.contiguous()
-    Wc = W_combined.float().contiguous()
-    Bc = B_const.float().contiguous()
+    wqkv_hm = _native.dense(wqkv_hm, X.dtype)
+    Wc = _native.dense(W_combined, torch.float32)
+    Bc = _native.dense(B_const, torch.float32)
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
-    assert Og.is_contiguous()
+    assert Og.is_contiguous() and Og.data_ptr() % 16 == 0, "Og must be contiguous and 16-byte aligned"
     q, k, v = (torch.empty(M, H, D, device=X.device, dtype=X.dtype) for _ in range(3))
     bias = torch.empty(H, M, M, device=X.device, dtype=torch.float32)
     st = _native.stream_of(X)
@@ -168,8 +165,8 @@ def _apb_generic(X, W_QKV, Z, W_combined, B_const, Og, scale, eps, mask, wqkv_hm
 
 
 def _io(t, dtype):
-    """A per-channel parameter as a contiguous vector of the I/O dtype (no copy when it already is)."""
-    return None if t is None else t.to(dtype).contiguous()
+    """A per-channel parameter as a dense, aligned vector of the I/O dtype (no copy when it already is)."""
+    return _native.dense(t, dtype)
 
 
 def apb_qkn_prep(X, wqkv_hm, b_q=None, qkn=None, eps=1e-5, qscale=1.0):
@@ -181,8 +178,8 @@ def apb_qkn_prep(X, wqkv_hm, b_q=None, qkn=None, eps=1e-5, qscale=1.0):
     assert three == 3 and C2 == C, "wqkv_hm must be (H, 3, D, C)"
     code = any_shape_dtype_code(X.dtype)
     _native.check_device(X, wqkv_hm, b_q, *(qkn or ()))
-    X = X if X.is_contiguous() else X.contiguous()
-    w = wqkv_hm.to(X.dtype).contiguous()
+    X = _native.dense(X)
+    w = _native.dense(wqkv_hm, X.dtype)
     bq = _io(b_q, X.dtype)
     gq, bqn, gk, bkn = (_io(t, X.dtype) for t in (qkn or (None,) * 4))
     for t in (bq, gq, bqn, gk, bkn):
@@ -207,13 +204,13 @@ def apb_forward_qkv(q, k, v, Z, W_combined, sum_W_combined, B_const, Og, scale=1
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
-    assert Og.is_contiguous()
-    Wc, sWc, Bc = W_combined.float().contiguous(), sum_W_combined.float().contiguous(), B_const.float().contiguous()
-    q, k, v = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
+    assert Og.is_contiguous() and Og.data_ptr() % 16 == 0, "Og must be contiguous and 16-byte aligned"
+    Wc, sWc, Bc = (_native.dense(t, torch.float32) for t in (W_combined, sum_W_combined, B_const))
+    q, k, v = (_native.dense(t) for t in (q, k, v))
     _native.check_device(q, k, v, Z, W_combined, Og, mask)
     st = _native.stream_of(q)
     if HD == 128 and Cz == 128 and H == 4 and D == 32 and q.dtype != torch.float32:
-        q, k, v, Z = (_native.vec16(t) for t in (q, k, v, Z))
+        Z = _native.vec16(Z)
         nbytes = _native.apb_workspace_bytes(M, H, D)
         work = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8) if nbytes else None
         _native.call("tops_apb_forward_qkv", q.data_ptr(), k.data_ptr(), v.data_ptr(), Z.data_ptr(), Z.stride(0),

@@ -38,24 +38,40 @@ __device__ inline GridTile grid_tile(int64_t t, int64_t L, int tiles_per_row) {
   return g;
 }
 
-// LayerNorm statistics of a C-element token held as 8 elements by each of 16 consecutive lanes:
-// one pass of packed dot products (sum and sum of squares, fp32 products and sums; 8 instead of
-// 16 converts + 24 fp32 ops per lane), variance clamped at 0.  The output phase's loaders use it
-// (measured 2 % faster there); the input phase keeps two passes, which measured faster there.  For 16-bit inputs the cancellation
-// in E[x^2] - mean^2 stays below the inputs' own resolution: a token whose mean exceeds its
-// deviation by 2^8 is already quantised to about one 16-bit step of that deviation.
+// LayerNorm statistics of a C-element token held as 8 elements by each of 16 consecutive lanes.
+// bf16: one pass of packed dot products (sum and sum of squares, fp32 products and sums; 8 instead
+// of 16 converts + 24 fp32 ops per lane), variance clamped at 0.  The output phase's loaders use it
+// (measured 2 % faster there); the input phase keeps two passes, which measured faster there.  For
+// bf16 (8 significant bits) the fp32 cancellation in E[x^2] - mean^2 has relative error about
+// (mean / std)^2 * 2^-22 in the variance, at most 2^-6 where a token's mean exceeds its deviation by
+// 2^8, the ratio at which bf16 already quantises the deviation to about one step.  fp16 resolves
+// deviations down to mean / std ~ 2^11, where that error would reach 100 %: fp16 takes two passes
+// (mean, then the sum of squared deviations), as the reference does (triangle_mul/kernel.py:111-113).
 template <typename T, int C>
 __device__ inline void ln_stats16(const vec<T, 8>& x, float eps, float& mean, float& rstd) {
-  const vec<T, 2> one = {(T)1.f, (T)1.f};
-  float s = 0.f, q = 0.f;
+  if constexpr (std::is_same<T, _Float16>::value) {
+    float v[8], s = 0.f, q = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const vec<T, 2> pr = {x[e], x[e + 1]};
-    s = Mma<T>::dot2(pr, one, s);
-    q = Mma<T>::dot2(pr, pr, q);
+    for (int e = 0; e < 8; ++e) {
+      v[e] = (float)x[e];
+      s += v[e];
+    }
+    mean = group_sum<16>(s) * (1.0f / C);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+    rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+  } else {
+    const vec<T, 2> one = {(T)1.f, (T)1.f};
+    float s = 0.f, q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const vec<T, 2> pr = {x[e], x[e + 1]};
+      s = Mma<T>::dot2(pr, one, s);
+      q = Mma<T>::dot2(pr, pr, q);
+    }
+    mean = group_sum<16>(s) * (1.0f / C);
+    rstd = rsqrtf(fmaxf(group_sum<16>(q) * (1.0f / C) - mean * mean, 0.f) + eps);
   }
-  mean = group_sum<16>(s) * (1.0f / C);
-  rstd = rsqrtf(fmaxf(group_sum<16>(q) * (1.0f / C) - mean * mean, 0.f) + eps);
 }
 
 // Tile coordinates with scalar divisions (tile indices are wave-uniform).
@@ -899,7 +915,7 @@ __global__ __launch_bounds__(256, 2) void tmu_einsum_f32_kernel(const float* __r
 //   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
 //   registers (4 channels x 8 tokens per thread) into a token-major tile; x (token-major) is
-//   normalised on the way in (16 lanes per token, one-pass statistics, `ln_stats16`);
+//   normalised on the way in (16 lanes per token, `ln_stats16`: one pass for bf16, two for fp16);
 //   waves 4-11 (writers) compute features [32 (w & 3), +32) for the 32 tokens [32 (w >> 2), +32)
 //   (w = wave - 4) with their Wp / Wg rows in registers (rows permuted so each lane ends up with
 //   16 consecutive features of one token), take the LN statistics of y from LDS and apply them

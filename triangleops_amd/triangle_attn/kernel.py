@@ -15,9 +15,8 @@ from .._common.dtype import any_shape_dtype_code, io_dtype_code
 
 
 def _as(x, t):
-    if t is None:
-        return None
-    return t if (t.dtype == x.dtype and t.is_contiguous()) else t.to(x.dtype).contiguous()
+    """A weight or parameter vector as a dense, 16-byte aligned tensor of x's dtype."""
+    return _native.dense(t, x.dtype)
 
 
 def row_stride(N):
@@ -54,7 +53,7 @@ def prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, scale=1.0, eps=1e-5, apply_ln
     Qp = torch.empty(N, H, ldn, 32, device=X.device, dtype=X.dtype)
     KV = torch.empty(N, H, ldn // 64, 4096, device=X.device, dtype=X.dtype)
     bias = torch.empty(H, (N + 31) // 32, ldn // 32, 1024, device=X.device, dtype=X.dtype)
-    BZf = None if BZ is None else BZ.float().contiguous()
+    BZf = None if BZ is None else _native.dense(BZ, torch.float32)
     _native.call(
         "tops_tri_prep",
         X.data_ptr(),
@@ -113,7 +112,7 @@ def generic_prep_forward(X, W_ln, B_ln, wqkv, WZ_c, BZ, *, eps=1e-5, apply_ln=Tr
     xln = torch.empty(N, N, C, device=X.device, dtype=dt)
     q, k, v = (torch.empty(N, N, H, D, device=X.device, dtype=dt) for _ in range(3))
     bias = torch.empty(H, N, N, device=X.device, dtype=torch.float32)
-    BZf = None if BZ is None else BZ.float().contiguous()
+    BZf = None if BZ is None else _native.dense(BZ, torch.float32)
     _native.call(
         "tops_tri_generic_prep",
         X.data_ptr(),
@@ -160,8 +159,9 @@ def padded_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
     Qp = torch.empty(N, H, ldn, 32, device=dev, dtype=dt)
     KV = torch.empty(N, H, ldn // 64, 4096, device=dev, dtype=dt)
     bt = torch.empty(H, (N + 31) // 32, ldn // 32, 1024, device=dev, dtype=dt)
-    q, k, v = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
-    _native.call("tops_tri_repack", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.float().contiguous().data_ptr(),
+    q, k, v = (_native.dense(t) for t in (q, k, v))
+    bias = _native.dense(bias, torch.float32)
+    _native.call("tops_tri_repack", q.data_ptr(), k.data_ptr(), v.data_ptr(), bias.data_ptr(),
                  Qp.data_ptr(), KV.data_ptr(), bt.data_ptr(), N, ldn, H, D, float(scale), io_dtype_code(dt),
                  _native.stream_of(q))
     if D % 8 == 0:  # the kernel writes heads of D in {8, 16, 24, 32} directly

@@ -16,11 +16,11 @@ from .._common.dtype import any_shape_dtype_code
 
 
 def _prep_weights(x, *ws):
-    return [w if (w.dtype == x.dtype and w.is_contiguous()) else w.to(x.dtype).contiguous() for w in ws]
+    return [_native.dense(w, x.dtype) for w in ws]
 
 
 def _f32(*vs):
-    return [v if (v.dtype == torch.float32 and v.is_contiguous()) else v.float().contiguous() for v in vs]
+    return [_native.dense(v, torch.float32) for v in vs]
 
 
 def input_phase(
@@ -50,7 +50,7 @@ def input_phase(
     ld = max(64, (L + 63) // 64 * 64) if ld is None else int(ld)
     code = any_shape_dtype_code(x.dtype)
     _native.check_device(x, p_in_combined, g_in_combined, mask)
-    x = x if x.is_contiguous() else x.contiguous()
+    x = _native.dense(x)
     Wp, Wg = _prep_weights(x, p_in_combined, g_in_combined)
     sWp, sWg, Bp, Bg = _f32(sum_W_p_in, sum_W_g_in, B_p_in_const, B_g_in_const)
     m8 = _native.mask_i8(mask)
@@ -128,18 +128,16 @@ def output_phase(
     C_out = p_out_combined.shape[0]
     code = any_shape_dtype_code(x.dtype)
     _native.check_device(x, y_t, p_out_combined, g_out_combined)
-    x = x if x.is_contiguous() else x.contiguous()
+    x = _native.dense(x)
     if ldy is None:
         ldy = max(64, (L + 63) // 64 * 64)
         y_t = y_t.reshape(C, B, L, L)
         if ldy != L:
             y_t = torch.nn.functional.pad(y_t, (0, ldy - L))
-        y_t = y_t if y_t.is_contiguous() else y_t.contiguous()
     else:
         ldy = int(ldy)
         assert y_t.is_contiguous() and y_t.numel() == C * B * L * ldy
-    if y_t.dtype != x.dtype:
-        y_t = y_t.to(x.dtype)
+    y_t = _native.dense(y_t, x.dtype)
     Wp, Wg = _prep_weights(x, p_out_combined, g_out_combined)
     sWp, sWg, Bp, Bg = _f32(sum_W_p_out, sum_W_g_out, B_p_out_const, B_g_out_const)
     out = torch.empty(B, L, L, C_out, device=x.device, dtype=x.dtype)
@@ -147,7 +145,7 @@ def output_phase(
     if residual is not None:
         assert residual.shape == out.shape, "residual must have the output's shape (B, L, L, C_out)"
         _native.check_device(x, residual)
-        res = [residual.to(x.dtype).contiguous()]
+        res = [_native.dense(residual, x.dtype)]
     _native.call(
         "tops_tmu_output_phase_residual" if res else "tops_tmu_output_phase",
         y_t.data_ptr(),
