@@ -274,14 +274,20 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 //          + K . Q^T                  2 MFMAs, K from LDS, Q^T in registers
 //     P    = exp2(S^T), l += rowsum   16 v_exp per lane, no max / subtract per element
 //     O^T += V^T . P^T                2 MFMAs, V^T from LDS, P^T = S^T's D registers
-// where C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m
-// is exact from the first tile with a valid key on and is only raised when a tile's
-// probabilities could overflow the I/O type (then O and l are rescaled and the tile
-// recomputed), so the common path needs neither a max nor a subtraction per score.  Masked
-// keys get probability exactly 0 (equal to the reference's exp(-1e9 - m) in fp32 whenever the
-// row has a valid key); a row without valid keys takes the uniform average of V over all N
-// keys, as the reference's -1e9 add gives.  The identity MFMA multiplies every bias element
-// of the tile by 0 or 1, so the bias padding must be finite (the pre-pass writes zeros).
+// Softmax is invariant to a per-row shift m of the scores; m only keeps exp2 in range.
+//   bf16 (OPT): m = 0 throughout.  bf16 has fp32's exponent range, so P = 2^s, the row sums and
+//   O stay exact in relative terms for scores s in about (-60, 100) (log2 units); the row sum l
+//   (fp32 adds of the unrounded weights, as the reference's l += sum(p)) is checked once at the
+//   end, and a wave whose l left [2^-60, 2^100] (or is not finite) recomputes its query tiles
+//   with an exact running max (tri_exact_tile, out of line).  The loop itself then has no max,
+//   no subtraction, no per-tile overflow test and no accumulator initialiser (C0 = 0).
+//   fp16: C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m is
+//   exact from the first tile with a valid key on and is only raised when a tile's
+//   probabilities could overflow fp16 (then O and l are rescaled and the tile recomputed).
+// Masked keys get probability exactly 0 (equal to the reference's exp(-1e9 - m) in fp32
+// whenever the row has a valid key); a row without valid keys takes the uniform average of V
+// over all N keys, as the reference's -1e9 add gives.  The identity MFMA multiplies every bias
+// element of the tile by 0 or 1, so the bias padding must be finite (the pre-pass writes zeros).
 //
 // Each tile is one straight-line phase in which the score MFMAs of the NEXT tile are
 // interleaved (sched_group_barrier) with the exponentials of the current one, so the matrix
@@ -346,6 +352,74 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
   }
 }
 
+// One query tile (32 queries of row i, head h) recomputed with an exact running max: the
+// classic online softmax over the visited tiles in the main loop's order, its operands read from
+// global memory (K and V^T from the row's KV blocks, whose rows are 32 / 64 elements wide there,
+// the bias tile, Q^T in registers).  For the waves of the bf16 kernel whose shift-free row sums
+// left their safe range (scores beyond about +-60 / 100 in log2 units); out of line, so the main
+// loop's register allocation does not see it.  `bqt`: this lane's bias operand address in the
+// tile (query tile, key tile 0), as the main loop's bq.
+template <typename T>
+__device__ __noinline__ void tri_exact_tile(const T* __restrict__ kvrow, const T* __restrict__ bqt,
+                                            vec<T, 8> q0, vec<T, 8> q1, vec<T, 8> id0, vec<T, 8> id1,
+                                            const short* vblk, const unsigned long long* kvalid, int nv, int64_t N,
+                                            T* __restrict__ out, int64_t i, int64_t so0, int64_t so1, int h, int dv,
+                                            int64_t q, int lane) {
+  constexpr int D = 32;
+  using V8 = vec<T, 8>;
+  using V4 = vec<T, 4>;
+  const int hl = lane >> 5, col = lane & 31;
+  f32x16 o = {};
+  float m = -INFINITY, l = 0.f;
+  for (int j = 0; j < nv; ++j) {
+    const int kb = vblk[j];
+    const unsigned long long kbits = kvalid[kb];
+    for (int kt = 0; kt < 2; ++kt) {
+      const unsigned int tb = (unsigned int)(kbits >> (32 * kt));
+      if (tb == 0) continue;  // wave-uniform: no valid key in this tile
+      const T* kr = kvrow + (int64_t)kb * kKVBlock + (32 * kt + col) * D + 8 * hl;
+      const T* vr = kvrow + (int64_t)kb * kKVBlock + 64 * D + col * 64 + 32 * kt + 8 * hl;
+      const T* br = bqt + (int64_t)(2 * kb + kt) * 1024;
+      f32x16 s = Mma<T>::m32(id0, ldg<V8>(br), f32x16{});
+      s = Mma<T>::m32(id1, ldg<V8>(br + 512), s);
+      s = Mma<T>::m32(ldg<V8>(kr), q0, s);
+      s = Mma<T>::m32(ldg<V8>(kr + 16), q1, s);
+      const unsigned int lb = tb >> (4 * hl);
+      float mt = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s[v] = ((lb >> (8 * (v / 4) + (v % 4))) & 1u) ? s[v] : -INFINITY;
+        mt = fmaxf(mt, s[v]);
+      }
+      const float mn = fmaxf(m, halves_max(mt));  // finite: the tile has a valid key
+      const float alpha = fast_exp2(m - mn);      // 0 before the first valid tile (m = -inf)
+      o *= alpha;
+      l *= alpha;
+      V8 p0, p1;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const float e0 = fast_exp2(s[v] - mn), e1 = fast_exp2(s[8 + v] - mn);
+        p0[v] = (T)e0;
+        p1[v] = (T)e1;
+        l += e0 + e1;
+      }
+      o = Mma<T>::m32(ldg<V8>(vr), p0, o);
+      o = Mma<T>::m32(ldg<V8>(vr + 16), p1, o);
+      m = mn;
+    }
+  }
+  const float inv = 1.0f / halves_sum(l);
+  if (q < N) {
+    T* dst = out + i * so0 + q * so1 + (int64_t)h * dv + 4 * hl;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (8 * g >= dv) break;
+      V4 w4 = {(T)(o[4 * g] * inv), (T)(o[4 * g + 1] * inv), (T)(o[4 * g + 2] * inv), (T)(o[4 * g + 3] * inv)};
+      stg<V4>(dst + 8 * g, w4);
+    }
+  }
+}
+
 template <typename T, int QT, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
@@ -355,6 +429,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
   constexpr int D = 32;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves per block");
   constexpr int KVR = 8 / NW;  // 16-byte chunks of a KV block per thread
+#ifndef TOPS_TRI_EXACT_MAX
+  constexpr bool OPT = std::is_same<T, __bf16>::value;  // shift-free softmax (bf16), see above
+#else
+  constexpr bool OPT = false;
+#endif
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
 
@@ -489,7 +568,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
   auto scores = [&](const V8* kop, V8 (*bb)[2], f32x16* s) {
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      s[t] = Mma<T>::m32(ident[0], bb[t][0], cinit[t]);
+      s[t] = Mma<T>::m32(ident[0], bb[t][0], OPT ? f32x16{} : cinit[t]);
       s[t] = Mma<T>::m32(ident[1], bb[t][1], s[t]);
       s[t] = Mma<T>::m32(kop[0], qop[t][0], s[t]);
       s[t] = Mma<T>::m32(kop[1], qop[t][1], s[t]);
@@ -527,32 +606,51 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
     bool over = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
+      if constexpr (OPT) {
+        // weights 2^s and their row sum: fp32 adds of the unrounded weights (full-rate VALU,
+        // which co-issues with the MFMAs; packed dot products stall them)
+        float e[16];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        p[t][0][v] = (T)fast_exp2(s[t][v]);
-        p[t][1][v] = (T)fast_exp2(s[t][8 + v]);
+        for (int v = 0; v < 16; ++v) e[v] = fast_exp2(s[t][v]);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          p[t][0][v] = (T)e[v];
+          p[t][1][v] = (T)e[8 + v];
+        }
+#pragma unroll
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+          for (int v = 0; v < w; ++v) e[v] += e[v + w];
+        ps[t] = e[0];
+      } else {
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          p[t][0][v] = (T)fast_exp2(s[t][v]);
+          p[t][1][v] = (T)fast_exp2(s[t][8 + v]);
+        }
+        // row sum of the rounded weights the PV product uses (packed dot products)
+        ps[t] = sum8<T>(p[t][0], 0.f) + sum8<T>(p[t][1], 0.f);
+        over |= !(ps[t] <= Mma<T>::kMaxP);
       }
-      // row sum of the rounded weights the PV product uses (packed dot products)
-      ps[t] = sum8<T>(p[t][0], 0.f) + sum8<T>(p[t][1], 0.f);
-      over |= !(ps[t] <= Mma<T>::kMaxP);
       pin(p[t][0]);
       pin(p[t][1]);
     }
+    constexpr int VPM = OPT ? 10 : 9;  // VALU instructions per score MFMA in the interleave
     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
     for (int m = 0; m < 2 * QT; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 9, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, VPM, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 2 * QT, 0);
 #pragma unroll
     for (int m = 0; m < 2 * QT; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 9, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, VPM, 0);
     }
-    // ---- rare: the first tile with a valid key sets the exact max; later tiles raise it only
-    // ---- when a probability could overflow the I/O type ----
-    const bool rare = (__ballot(over) != 0) | (first & (tb != 0));
+    // ---- rare (fp16): the first tile with a valid key sets the exact max; later tiles raise it
+    // ---- only when a probability could overflow the I/O type ----
+    const bool rare = !OPT && ((__ballot(over) != 0) | (first & (tb != 0)));
     if (rare) {
 #pragma unroll
       for (int t = 0; t < QT; ++t) {
@@ -624,6 +722,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
     if (j + 1 < nv) block(j + 1, kvB, kvA);
   }
 
+  // ---- bf16: a wave whose shift-free row sums left [2^-60, 2^100] (or are not finite: a
+  // ---- weight overflowed) recomputes its query tiles with an exact running max ----
+  if constexpr (OPT) {
+    bool bad = false;
+#pragma unroll
+    for (int t = 0; t < QT; ++t) {
+      const float lt = halves_sum(l[t]);
+      bad |= !(lt >= 0x1p-60f && lt <= 0x1p100f);
+    }
+    if (__ballot(bad) != 0) {  // wave-uniform
+#pragma unroll
+      for (int t = 0; t < QT; ++t)
+        tri_exact_tile<T>(kvrow, bq[t], qop[t][0], qop[t][1], ident[0], ident[1], vblk,
+                          kvalid, nv, N, out, i, so0, so1, h, dv, qbase + 32 * t + col, lane);
+      return;
+    }
+  }
   // ---- normalise and store O[i, q, h*dv + d], d < dv: the head's first dv of its 32 lanes
   // ---- (dv < 32 when the head is narrower and its Q / K / V are zero-padded to 32) ----
 #pragma unroll
