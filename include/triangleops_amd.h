@@ -114,6 +114,18 @@ int tops_tri_attention(const void* Qp, const void* KV, const void* bias, const v
                        void* stream);
 
 /*
+ * The same attention with two rows per wave (bf16, D = 32 only; other arguments as
+ * tops_tri_attention): each wave takes one 32-query tile of rows i and i + 1, so one bias operand
+ * load serves both rows, and K / V^T are copied into LDS three 64-key blocks ahead.  Replaces the
+ * same reference code as tops_tri_attention (triangle_attn/kernel.py:197-253); its results agree
+ * with tops_tri_attention's to bf16 rounding (the weights of the two kernels round at the same
+ * points).
+ */
+int tops_tri_attention_two_row(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
+                               int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
+                               int64_t D, int dtype, void* stream);
+
+/*
  * Repack for triangle attention at shapes the pre-pass does not cover (any H <= 64, D <= 32; e.g.
  * the D = 16, C_in = 64 "Apo" shape of tests/test_triangle_attn.py:137-192, which the reference runs
  * on its tensor-core kernel: triangle_attn/kernel.py:211-213, :282): the any-shape pre-pass's

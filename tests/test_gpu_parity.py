@@ -8,6 +8,7 @@ Large configurations are checked on a sample of output rows (rows are independen
 """
 
 import math
+import os
 
 import pytest
 import torch
@@ -399,6 +400,115 @@ def test_tri_shift_free_softmax_fallback(device, N, shift):
     assert torch.equal(a[:, :, 1], b[:, :, 1]) and torch.equal(a[:, :, 3], b[:, :, 3])
     for h in (0, 2):
         _check(b[:, :, h], a[:, :, h].float(), torch.bfloat16, f"tri fallback N={N} shift={shift} head {h}")
+
+
+def _two_row_mask(N, seed):
+    """Random mask (80 % valid) with a pair of rows without valid keys (rows 2, 3), and a pair in
+    which only the first row has none (rows 4, 5)."""
+    m = torch.rand(N, N, generator=torch.Generator().manual_seed(seed)) < 0.8
+    if N >= 8:
+        m[2:5] = False
+    return m
+
+
+# tri_attn2_kernel faulted the GPU in an earlier build, whose copies were inline-asm global_load_lds
+# with a base address rebuilt from v_readfirstlane halves.  Its copies now go through the compiler's
+# global_load_lds builtin (the compiler sets M0 and inserts the wait states), and its index
+# arithmetic is checked on the CPU by tests/test_tri_two_row_model.py.  The test stays off until
+# its one GPU run (TOPS_RUN_TWO_ROW=1) has passed.
+@pytest.mark.skipif(os.environ.get("TOPS_RUN_TWO_ROW") != "1",
+                    reason="two-row attention kernel: pending its first GPU run after the copy rewrite")
+@pytest.mark.parametrize("N,mask", [(8, "two_row"), (33, "pad"), (130, "two_row"), (256, "pad"), (520, "two_row"),
+                                    (1024, "pad")])
+def test_tri_two_row_kernel(device, N, mask):
+    """tops_tri_attention_two_row against tops_tri_attention on the same pre-pass buffers (bf16
+    rounding of the weights at the same points; rows without valid keys in pairs and mixed pairs),
+    and through the gate against the fp32 oracle; masked keys carry no weight (perturbing them
+    changes nothing)."""
+    from triangleops_amd import _native
+    from triangleops_amd.triangle_attn.kernel import attention_core, gate_out_forward, prep_forward
+
+    inp = tri_inputs(N, seed=N + 17, mask="pad" if mask == "pad" else "none", bias_z=True)
+    if mask == "two_row":
+        inp["mask"] = _two_row_mask(N, N)
+    d = to_dev(inp, device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], 4, 32)
+    Qp, KV, bias, ldn = prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"],
+                                     scale=d["scale"])
+    one = torch.empty(N, N, 128, device=device, dtype=torch.bfloat16)
+    attention_core(Qp, KV, bias, one, N=N, ldn=ldn, mask=d["mask"])
+    m8 = d["mask"].to(torch.int8).contiguous()
+
+    def two(kv):
+        o = torch.full((N, N, 128), float("nan"), device=device, dtype=torch.bfloat16)
+        _native.call("tops_tri_attention_two_row", Qp.data_ptr(), kv.data_ptr(), bias.data_ptr(), m8.data_ptr(),
+                     m8.stride(0), m8.stride(1), o.data_ptr(), o.stride(0), o.stride(1), N, ldn, 4, 32, 2,
+                     _native.stream_of(Qp))
+        return o
+
+    o2 = two(KV)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o2.float()).all(), f"N={N}: unwritten or non-finite output"
+    _check(o2.cpu(), one.float().cpu(), torch.bfloat16, f"two-row vs one-row N={N} {mask}")
+    out = gate_out_forward(o2, d["X"], d["W_proj_g"], None, d["W_proj_o"], None, ln=(pre["W_ln"], pre["B_ln"], 1e-5))
+    rows = None if N <= 520 else torch.tensor([0, 1, N // 2, N - N // 10 - 1, N - 1])
+    expect = _tri_ref(inp, rows=rows)
+    _check((out if rows is None else out[rows.to(device)]).cpu(), expect, torch.bfloat16, f"two-row oracle N={N}")
+    # masked keys are inert: perturb every K / V row of a key masked in a row (pre-pass layout)
+    if N <= 256:
+        kv2 = KV.clone()
+        kvv = kv2.view(N, 4, ldn // 64, 4096)
+        g = torch.Generator().manual_seed(N)
+        for i in range(N):
+            for k in torch.nonzero(~inp["mask"][i]).flatten().tolist():
+                kb, kk = divmod(k, 64)
+                kvv[i, :, kb, kk * 32:(kk + 1) * 32] = (10 * torch.randn(4, 32, generator=g)).to(kvv.dtype).to(device)
+                # V^T column of key kk: group kk // 32, position x with perm32(x) = kk % 32
+                n = kk % 32
+                j, rem = n >> 4, n & 15
+                x = 32 * (kk // 32) + 16 * j + 8 * ((rem >> 2) & 1) + 4 * (rem >> 3) + (rem & 3)
+                cols = 2048 + 64 * torch.arange(32) + x
+                kvv[i, :, kb, cols.to(device)] = (10 * torch.randn(4, 32, generator=g)).to(kvv.dtype).to(device)
+        o3 = two(kv2)
+        valid_rows = inp["mask"].any(1)
+        assert torch.equal(o3[valid_rows.to(device)], o2[valid_rows.to(device)]), "masked keys changed the output"
+
+
+@pytest.mark.skipif(os.environ.get("TOPS_RUN_TWO_ROW") != "1",
+                    reason="two-row attention kernel: pending its first GPU run after the copy rewrite")
+@pytest.mark.parametrize("shift", [150.0, -200.0])
+def test_tri_two_row_fallback(device, shift):
+    """The two-row kernel's exact-max recomputation: shifted bias tiles (see
+    test_tri_shift_free_softmax_fallback) give the unshifted output to the bf16 bar."""
+    from triangleops_amd import _native
+    from triangleops_amd.triangle_attn.kernel import prep_forward
+
+    N = 200
+    d = to_dev(tri_inputs(N, seed=N + 9, mask="random", bias_z=True), device)
+    pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
+                                        d["B_proj_z"], 4, 32)
+    Qp, KV, bias, ldn = prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"],
+                                     scale=d["scale"])
+    b0 = bias.float().round()
+    b1 = b0.clone()
+    b1[0] += shift
+    b1[2, 2:4] += shift
+    m8 = d["mask"].to(torch.int8).contiguous()
+    outs = []
+    for b in (b0, b1):
+        o = torch.empty(N, N, 128, device=device, dtype=torch.bfloat16)
+        bb = b.to(torch.bfloat16)
+        _native.call("tops_tri_attention_two_row", Qp.data_ptr(), KV.data_ptr(), bb.data_ptr(), m8.data_ptr(),
+                     m8.stride(0), m8.stride(1), o.data_ptr(), o.stride(0), o.stride(1), N, ldn, 4, 32, 2,
+                     _native.stream_of(Qp))
+        torch.cuda.synchronize()
+        outs.append(o.view(N, N, 4, 32).cpu())
+    a, b = outs
+    assert torch.isfinite(b.float()).all()
+    assert torch.equal(a[:, :, 1], b[:, :, 1]) and torch.equal(a[:, :, 3], b[:, :, 3])
+    for h in (0, 2):
+        _check(b[:, :, h], a[:, :, h].float(), torch.bfloat16, f"two-row fallback shift={shift} head {h}")
 
 
 @pytest.mark.parametrize("N", [100, 384])

@@ -31,6 +31,7 @@ _SIGNATURES = {
     ],
     "tops_tri_repack": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f32, _i32, _p],
     "tops_tri_attention": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
+    "tops_tri_attention_two_row": [_p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p],
     "tops_gate_out": [
         _p, _i64, _i64, _p, _i64, _i64, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p,
     ],

@@ -42,6 +42,9 @@ constexpr int kMaxKB = kMaxN / 64;
 #define TRI_NW8_MIN_N 2048  // from this N on, 8-wave attention blocks (half the KV block copies per query)
 #endif
 static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 * 64; }
+#ifndef TRI_WPE
+#define TRI_WPE(QT, NW) (8 / (NW))  // waves per SIMD the attention kernel's registers are sized for
+#endif
 
 // ---------------------------------------------------------------------------------------------
 // Pre-pass.  One tile = (row i, positions [64 kb, 64 kb + 64)), 8 waves in two roles:
@@ -421,7 +424,7 @@ __device__ __noinline__ void tri_exact_tile(const T* __restrict__ kvrow, const T
 }
 
 template <typename T, int QT, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
+__global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
                                                          const T* __restrict__ bias, const int8_t* __restrict__ mask,
                                                          int64_t sm0, int64_t sm1, T* __restrict__ out, int64_t so0,
                                                          int64_t so1, int64_t N, int64_t ldn, int H, int nqc,
@@ -758,27 +761,30 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void tri_attn_kernel(const T* __re
   }
 }
 // ---------------------------------------------------------------------------------------------
-// Attention core, two rows per wave.  A block = 4 waves = rows (i0, i1 = i0 + 1) x 128 queries
-// of one head; wave w owns query tile qt = 4 qc + w of both rows.  Per 32-key tile step the
+// Attention core, two rows per wave (bf16, D = 32).  A block = 4 waves = rows (i0, i1 = i0 + 1) x
+// 128 queries of one head; wave w owns query tile qt = 4 qc + w of both rows.  Per 32-key tile the
 // wave runs, for row r = 0 then 1 (a "stage" each):
-//     S_r^T = C_r + I . B^T + K_r . Q_r^T       4 MFMAs (C_r = -m_r, the lazily raised row max)
-//     P_r   = exp2(S_r^T), l_r += sum P_r        16 v_exp, 8 packed converts, 16 fp32 adds
+//     S_r^T = I . B^T + K_r . Q_r^T              4 MFMAs
+//     P_r   = 2^(S_r^T), l_r += sum P_r          16 v_exp, 8 packed converts, 15 fp32 adds
 //     O_r^T += V_r^T . P_r^T                     2 MFMAs
-// The bias operand B (16 bytes per lane and half) is loaded once per step for both rows, so
-// each bias tile costs 1 KB of L2 reads per 32 x 32 tile instead of 2 KB; K and V of both rows
-// are copied straight into LDS (global_load_lds, 1 KB per wave instruction) with each lane
-// fetching the 16-byte chunk that belongs at its LDS slot under the operand reads' XOR swizzle
-// (K rows 64 B: chunk ^ ((key >> 2) & 3); V^T rows 128 B: chunk ^ ((d >> 1) & 7)), so the
-// operand reads are free of bank conflicts without padding.  A ring of 4 LDS slots per 64-key
-// block, one barrier per block, copies issued three blocks ahead.
-// Stages are software-pipelined: stage (row r, tile t) issues the PV MFMAs of the previous
-// stage and the score MFMAs of the next one (the other row) between its own exponentials, so
-// the matrix cores and the VALU of a wave work together; the row sums are fp32 adds of the
-// unrounded weights (as the reference's l_i += sum(p)), which, unlike packed dot products,
-// co-issue with MFMAs.  Masking, the lazy max and rows without valid keys (uniform average of
-// V over all N keys) follow the one-row kernel above.
+// with the one-row kernel's shift-free softmax (weights 2^s, row sums l checked once at the end;
+// a wave whose l left [2^-60, 2^100] recomputes its tiles with an exact running max).  The bias
+// operand B (16 bytes per lane and half) is loaded once per tile for both rows, so a bias tile costs
+// 1 KB of L2 reads per 32 x 32 (row, query, key) tile instead of 2 KB.  K and V^T of both rows go
+// straight into LDS with the compiler's global_load_lds builtin (1 KB per wave instruction; the
+// compiler sets M0 and inserts the wait states and the waits its own reads of a slot need), each
+// lane fetching the 16-byte chunk that belongs at its LDS position under the operand reads' XOR
+// swizzle (K rows 64 B: chunk ^ ((key >> 2) & 3); V^T rows 128 B: chunk ^ ((d >> 1) & 7)), so the
+// operand reads are free of bank conflicts without padding.  A ring of 4 LDS slots of 64-key
+// blocks, one barrier per block, copies issued three blocks ahead.  Stages are software-pipelined:
+// stage (row r, tile t) issues the PV MFMAs of the previous stage and the score MFMAs of the next
+// one (the other row) between its own exponentials.  A row without valid keys runs with Q and the
+// identity zeroed: every score is 0 and each key < N gets weight exactly 1, the uniform average of
+// V the reference's -1e9 add gives.  Masked keys get weight exactly 0.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRing = 4;  // LDS slots of 64-key KV blocks (per block: 2 rows x 8 KB each)
+template <int V>
+using IC = std::integral_constant<int, V>;
 
 template <typename T>
 __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__ Qp, const T* __restrict__ KV,
@@ -788,9 +794,10 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   constexpr int D = 32, NW = 4, KVB = kKVBlock * 2;  // bytes of one (row, 64-key) KV block
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
+  using LdsPtr = __attribute__((address_space(3))) void*;
 
   // four separate arrays, indexed at compile time: the compiler then sees that the LDS reads of
-  // one slot do not alias the asynchronous copy into another, and does not wait for the copy
+  // one slot do not alias the asynchronous copies into the others
   __shared__ __attribute__((aligned(16))) char slot0[2][KVB];
   __shared__ __attribute__((aligned(16))) char slot1[2][KVB];
   __shared__ __attribute__((aligned(16))) char slot2[2][KVB];
@@ -848,32 +855,39 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   __syncthreads();
   const int nv = nvblk;  // >= 1 whenever N >= 1
 
-  // ---- per-row operands: Q^T (scaled, d-permuted), identity (zero for a uniform row) ----
+  // ---- rows without a valid key take the uniform average of V over the N keys (PV products
+  // ---- alone, tri_uniform_row): a pair of such rows skips the main loop; in a mixed pair the
+  // ---- main loop's result for the uniform row is replaced at the end ----
   const int irow[2] = {i0, i1};
+  const int64_t kvoff[2] = {((int64_t)i0 * H + h) * nkb * kKVBlock, ((int64_t)i1 * H + h) * nkb * kKVBlock};
+  if (uni[0] && uni[1]) {  // block-uniform
+    tri_uniform_row<T, 1>(KV + kvoff[0], vblk, nv, N, out, i0, so0, so1, h, D, 32 * qt, lane);
+    if (i1v < N) tri_uniform_row<T, 1>(KV + kvoff[1], vblk, nv, N, out, i1, so0, so1, h, D, 32 * qt, lane);
+    return;
+  }
+
+  // ---- per-row operands: Q^T (scaled, d-permuted); the identity of the bias MFMAs ----
   int q = 32 * qt + col;
   q = q < N ? q : N - 1;
-  V8 qop[2][2], ident[2][2];
+  V8 qop[2][2], ident[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const T* qr = Qp + (((int64_t)irow[r] * H + h) * ldn + q) * D + 8 * hl;
-    qop[r][0] = uni[r] ? V8{} : ldg<V8>(qr);
-    qop[r][1] = uni[r] ? V8{} : ldg<V8>(qr + 16);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ident[r][j][e] = (T)((!uni[r] && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
+    qop[r][0] = ldg<V8>(qr);
+    qop[r][1] = ldg<V8>(qr + 16);
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ident[j][e] = (T)(col == 16 * j + 8 * hl + e ? 1.f : 0.f);
   const int qtc = qt < nqt ? qt : nqt - 1;
   const T* bq = bias + ((int64_t)h * nqt + qtc) * nkt * 1024 + (32 * hl + col) * 8;
 
   // ---- KV block copy: wave w moves (row w >> 1, part w & 1 = K or V^T), 4 KB in four 1 KB
   // ---- instructions; lane l of instruction s fills LDS chunk p = 64 s + l of the part with the
-  // ---- global chunk that the swizzle places there.  Inline asm: the compiler does not count
-  // ---- these loads, so it adds no waits of its own for them (the waits before the barriers are
-  // ---- explicit), and no copy is ever issued between a bias load and that load's first use, so
-  // ---- the compiler's own waits for the bias loads stay exact.
+  // ---- global chunk that the swizzle places there.
   const int crow = wave >> 1, cpart = wave & 1;
-  const char* kvsrc = reinterpret_cast<const char*>(KV + ((int64_t)irow[crow] * H + h) * nkb * kKVBlock + cpart * 2048);
+  const char* kvsrc = reinterpret_cast<const char*>(KV + kvoff[crow] + cpart * 2048);
   uint32_t gofs[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -882,22 +896,10 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   }
   auto dma = [&](int vj, auto sc) {
     const int kb = vblk[vj < nv ? vj : nv - 1];
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(
-        (uint32_t)reinterpret_cast<uintptr_t>(&slot(sc)[crow][cpart * 4096]));
-    const uint64_t a = (uint64_t)reinterpret_cast<uintptr_t>(kvsrc + (int64_t)kb * kKVBlock * (int64_t)sizeof(T));
-    // (readfirstlane returns int: each half goes through uint32_t so the low half is not
-    // sign-extended into the high one)
-    const char* src = reinterpret_cast<const char*>(
-        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
-        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a));
+    const char* src = kvsrc + (int64_t)kb * kKVBlock * (int64_t)sizeof(T);
+    char* dst = &slot(sc)[crow][cpart * 4096];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint32_t va = gofs[s], ma = dst + 1024u * s;
-      // s_nop 4: the base address comes from v_readfirstlane (a VALU write of the SGPRs), and a
-      // VMEM instruction may read an SGPR written by VALU only 5 wait states later; the compiler
-      // inserts those for its own instructions but not for inline asm
-      asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(va), "s"(src), "{m0}"(ma) : "memory");
-    }
+    for (int s = 0; s < 4; ++s) __builtin_amdgcn_global_load_lds(src + gofs[s], (LdsPtr)(dst + 1024 * s), 16, 0, 0);
   };
   // operand reads: K of row r, 32-key tile kt (A operand of S^T, k-steps j = 0, 1); V^T of
   // row r, tile kt (A operand of O^T)
@@ -920,34 +922,30 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     b[1] = ldg<V8>(p + 512);
   };
 
-  f32x16 o[2], cinit[2], S[2];
+  f32x16 o[2], S[2];
   float l[2] = {0.f, 0.f};
-  bool first[2] = {true, true};
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    o[r] = f32x16{};
-    cinit[r] = f32x16{};
-  }
+  for (int r = 0; r < 2; ++r) o[r] = f32x16{};
   V8 P[2][2], vop[2][2];
-  V8 b0[2], b1[2];  // bias operands of the current (or next) visit's 32-key tiles 0 and 1
+  V8 bset[2][2][2];  // bias operands of visits vj, vj + 1 (set vj % 2): [tile][half]
 
   auto scores = [&](int r, const V8* k, const V8* b) {
-    f32x16 s = Mma<T>::m32(ident[r][0], b[0], cinit[r]);
-    s = Mma<T>::m32(ident[r][1], b[1], s);
+    f32x16 s = Mma<T>::m32(ident[0], b[0], f32x16{});
+    s = Mma<T>::m32(ident[1], b[1], s);
     s = Mma<T>::m32(k[0], qop[r][0], s);
     return Mma<T>::m32(k[1], qop[r][1], s);
   };
 
-  // One stage: exponentials of row r's tile (key bits tb) in S[r]; the PV MFMAs of the other
-  // row's previous tile (P[1 - r], vop[1 - r]) and the score MFMAs of the next tile (row rn,
-  // K operands kn, bias bn, into S[rn]) are interleaved with them.
+  // One stage: weights of row r's tile (key bits tb) from S[r]; the PV MFMAs of the other row's
+  // previous tile (P[1 - r], vop[1 - r]) and the score MFMAs of the next tile (row rn, K operands
+  // kn, bias bn, into S[rn]) are interleaved with its exponentials.
   auto stage = [&](int r, unsigned int tb, bool pv, int rn, const V8* kn, const V8* bn) {
     if (pv) {
       o[1 - r] = Mma<T>::m32(vop[1 - r][0], P[1 - r][0], o[1 - r]);
       o[1 - r] = Mma<T>::m32(vop[1 - r][1], P[1 - r][1], o[1 - r]);
     }
     f32x16 s = S[r];
-    if (tb != 0xffffffffu) {  // partial tile (wave-uniform): masked keys get probability 0
+    if (tb != 0xffffffffu) {  // partial tile (wave-uniform): masked keys get weight 0
       const unsigned int lb = tb >> (4 * hl);
 #pragma unroll
       for (int v = 0; v < 16; ++v) s[v] = ((lb >> (8 * (v / 4) + (v % 4))) & 1u) ? s[v] : -INFINITY;
@@ -967,8 +965,6 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
       for (int v = 0; v < w; ++v) e[v] += e[v + w];
-    float ps = e[0];
-    const bool over = !(ps <= Mma<T>::kMaxP);
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
     __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
@@ -978,109 +974,96 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
     }
-    // ---- rare: the first tile with a valid key sets the exact max; later tiles raise it only
-    // ---- when a probability could overflow the I/O type ----
-    if ((__ballot(over) != 0) | (first[r] & (tb != 0))) {
-      float mr = s[0];
-#pragma unroll
-      for (int v = 1; v < 16; ++v) mr = fmaxf(mr, s[v]);
-      mr = halves_max(mr);
-      const float mt = first[r] ? mr : fmaxf(mr, 0.f);
-      float e2[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) e2[v] = fast_exp2(s[v] - mt);
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        P[r][0][v] = (T)e2[v];
-        P[r][1][v] = (T)e2[8 + v];
-      }
-#pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-        for (int v = 0; v < w; ++v) e2[v] += e2[v + w];
-      ps = e2[0];
-      if (!first[r]) {  // O and l are still zero before the first valid tile
-        const float alpha = fast_exp2(-mt);
-        o[r] *= alpha;
-        l[r] *= alpha;
-      }
-      cinit[r] -= mt;
-      first[r] = false;
-    }
-    l[r] += ps;
+    l[r] += e[0];
   };
 
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  // ---- prologue: KV blocks 0..2 in flight, bias of visit 0, wait for blocks 0 and 1, scores
-  // ---- of the first stage (visit 0, tile 0, row 0) ----
-  dma(0, I0{});
-  dma(1, I1{});
-  dma(2, I2{});
-  load_bias(0, 0, b0);
-  load_bias(0, 1, b1);
-  vmcnt_wait<8>();
-  __builtin_amdgcn_s_barrier();
+  // ---- prologue.  Every global load of the main loop is issued in one place per block, after
+  // ---- the block's barrier: the bias of visit vj + 2 (first needed in the next block's last
+  // ---- stage), then the copy of block vj + 3 (needed two blocks later).  Vector-memory loads
+  // ---- complete in issue order, so a wait for one load also waits for every load issued before
+  // ---- it: the bias load that follows a copy is not needed before the copy itself, so the
+  // ---- copies keep their full lead.  The prologue issues the same sequence from visit 0. ----
+  dma(0, IC<0>{});
+  load_bias(0, 0, bset[0][0]);
+  load_bias(0, 1, bset[0][1]);
+  dma(1, IC<1>{});
+  load_bias(1, 0, bset[1][0]);
+  load_bias(1, 1, bset[1][1]);
+  dma(2, IC<2>{});
+  __builtin_amdgcn_sched_barrier(0);
+  vmcnt_wait<12>();  // this wave's copy of block 0 has landed (12 loads were issued after it)
+  __syncthreads();
   {
     V8 k[2];
-    read_k(I0{}, 0, 0, k);
-    S[0] = scores(0, k, b0);
+    read_k(IC<0>{}, 0, 0, k);
+    S[0] = scores(0, k, bset[0][0]);
   }
 
-  // One 64-key block (visit vj in LDS slot SL = vj % 4): four stages (kt, r).  Each bias
-  // register set is reloaded right after its last use: tile 0 of visit vj + 1 after the first
-  // stage, tile 1 after the last stage's copy of block vj + 3.  So no copy sits between a bias
-  // load and its first use, and behind the copy of block vj + 1 (issued two blocks earlier) there
-  // are exactly 12 memory operations when the last stage waits for it; the barrier that follows
-  // publishes block vj + 1 and frees the slot of block vj - 1 for the copy of block vj + 3.
+  // One 64-key block (visit vj in LDS slot SL = vj % 4 and bias set BS = vj % 2): four stages (kt,
+  // r), each computing the scores of the next.  Bias set BS was last read by the third stage; after
+  // the barrier it takes visit vj + 2, and slot (vj + 3) % 4, whose block vj - 1 was last read
+  // before that barrier, the copy of block vj + 3.  At the barrier this wave's copy of block vj + 1
+  // (issued at the barrier two blocks earlier) has exactly 8 loads behind it: the bias of visit
+  // vj + 1 and the copy of block vj + 2.
   auto block = [&](int vj, auto slc) {
-    constexpr int SL = decltype(slc)::value;
-    using SN = std::integral_constant<int, (SL + 1) % kRing>;
-    using SC = std::integral_constant<int, (SL + 3) % kRing>;
+    constexpr int SL = decltype(slc)::value, BS = SL % 2, BN = (BS + 1) % 2;
+    using SN = IC<(SL + 1) % kRing>;
+    using SC = IC<(SL + 3) % kRing>;
     const int kb = vblk[vj];
     const unsigned long long kv0 = kvalid[0][kb], kv1 = kvalid[1][kb];
     V8 k[2];
     // stage (kt 0, row 0): next = (0, row 1)
     read_k(slc, 1, 0, k);
     read_v(slc, 0, 0, vop[0]);
-    stage(0, (unsigned int)kv0, vj > 0, 1, k, b0);
-    load_bias(vj + 1, 0, b0);
+    stage(0, (unsigned int)kv0, vj > 0, 1, k, bset[BS][0]);
     // stage (kt 0, row 1): next = (1, row 0)
     read_k(slc, 0, 1, k);
     read_v(slc, 1, 0, vop[1]);
-    stage(1, (unsigned int)kv1, true, 0, k, b1);
+    stage(1, (unsigned int)kv1, true, 0, k, bset[BS][1]);
     // stage (kt 1, row 0): next = (1, row 1)
     read_k(slc, 1, 1, k);
     read_v(slc, 0, 1, vop[0]);
-    stage(0, (unsigned int)(kv0 >> 32), true, 1, k, b1);
+    stage(0, (unsigned int)(kv0 >> 32), true, 1, k, bset[BS][1]);
+    __builtin_amdgcn_sched_barrier(0);
+    vmcnt_wait<8>();  // this wave's copy of block vj + 1 has landed
+    __syncthreads();
+    load_bias(vj + 2, 0, bset[BS][0]);
+    load_bias(vj + 2, 1, bset[BS][1]);
+    dma(vj + 3, SC{});
+    __builtin_amdgcn_sched_barrier(0);
     // stage (kt 1, row 1): next = (visit vj + 1, kt 0, row 0)
-    vmcnt_wait<12>();  // this wave's copy of block vj + 1 has landed
-    asm volatile("s_barrier" ::: "memory");
     read_k(SN{}, 0, 0, k);
     read_v(slc, 1, 1, vop[1]);
-    stage(1, (unsigned int)(kv1 >> 32), true, 0, k, b0);
-    __builtin_amdgcn_sched_barrier(0);
-    dma(vj + 3, SC{});
-    load_bias(vj + 1, 1, b1);
+    stage(1, (unsigned int)(kv1 >> 32), true, 0, k, bset[BN][0]);
   };
   for (int vj = 0; vj < nv; vj += 4) {
-    block(vj, I0{});
-    if (vj + 1 < nv) block(vj + 1, I1{});
-    if (vj + 2 < nv) block(vj + 2, I2{});
-    if (vj + 3 < nv) block(vj + 3, I3{});
+    block(vj, IC<0>{});
+    if (vj + 1 < nv) block(vj + 1, IC<1>{});
+    if (vj + 2 < nv) block(vj + 2, IC<2>{});
+    if (vj + 3 < nv) block(vj + 3, IC<3>{});
   }
   // ---- epilogue: PV of the last stage (row 1) ----
   o[1] = Mma<T>::m32(vop[1][0], P[1][0], o[1]);
   o[1] = Mma<T>::m32(vop[1][1], P[1][1], o[1]);
 
-  // ---- normalise and store O[i, q, h*D + d] ----
+  // ---- per row: the uniform average (a row without valid keys), an exact-max recomputation
+  // ---- (a wave whose shift-free row sums left [2^-60, 2^100] or are not finite), or O / l ----
   const int qo = 32 * qt + col;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const float inv = 1.0f / halves_sum(l[r]);
-    if (qo < N && (r == 0 || i1v < N)) {
+    if (r == 1 && i1v >= N) break;  // block-uniform: the pair's second row is past the grid
+    if (uni[r]) {
+      tri_uniform_row<T, 1>(KV + kvoff[r], vblk, nv, N, out, irow[r], so0, so1, h, D, 32 * qt, lane);
+      continue;
+    }
+    const float lt = halves_sum(l[r]);
+    if (__ballot(!(lt >= 0x1p-60f && lt <= 0x1p100f)) != 0) {  // wave-uniform
+      tri_exact_tile<T>(KV + kvoff[r], bq, qop[r][0], qop[r][1], ident[0], ident[1], vblk, kvalid[r], nv, N, out,
+                        irow[r], so0, so1, h, D, qo, lane);
+      continue;
+    }
+    const float inv = 1.0f / lt;
+    if (qo < N) {
       T* dst = out + (int64_t)irow[r] * so0 + (int64_t)qo * so1 + (int64_t)h * D + 4 * hl;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -1091,6 +1074,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     }
   }
 }
+
 
 // ---------------------------------------------------------------------------------------------
 // Repack for the shapes the pre-pass does not cover: the any-shape pre-pass's plain Q / K / V
@@ -1208,17 +1192,6 @@ template <typename T>
 static int tri_attention_t(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0,
                            int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H,
                            int64_t dv, hipStream_t st) {
-#ifdef TOPS_TRI_TWO_ROW  // off: not yet run on the GPU since its wait-state fix
-  if (dv == 32) {
-    const int nqc = (int)((N + 127) / 128), nrp = (int)((N + 1) / 2);
-    const int64_t grid = (int64_t)H * nrp * nqc;
-    if (grid == 0) return TOPS_OK;
-    hipLaunchKernelGGL((tri_attn2_kernel<T>), dim3((unsigned)grid), dim3(256), 0, st, (const T*)Qp, (const T*)KV,
-                       (const T*)bias, (const int8_t*)mask, sm0, sm1, (T*)out, so0, so1, (int)N, (int)ldn, (int)H,
-                       nqc, nrp);
-    return launched("tops_tri_attention");
-  }
-#endif
   const int qt = N <= 128 ? 1 : 2;
   const int nw = N >= TRI_NW8_MIN_N ? 8 : 4;  // waves (query tiles of 32 x qt) per block
   const int64_t per_block = nw * 32 * qt;
@@ -1237,6 +1210,18 @@ static int tri_attention_t(const void* Qp, const void* KV, const void* bias, con
     TOPS_TRI(2, 8);
 #undef TOPS_TRI
   return launched("tops_tri_attention");
+}
+
+// The two-row kernel (bf16, D = 32): 4 waves per (row pair, 128 queries, head).
+static int tri_attention2(const void* Qp, const void* KV, const void* bias, const void* mask, int64_t sm0, int64_t sm1,
+                          void* out, int64_t so0, int64_t so1, int64_t N, int64_t ldn, int64_t H, hipStream_t st) {
+  const int nqc = (int)((N + 127) / 128), nrp = (int)((N + 1) / 2);
+  const int64_t grid = H * nrp * nqc;
+  if (grid == 0) return TOPS_OK;
+  hipLaunchKernelGGL((tri_attn2_kernel<__bf16>), dim3((unsigned)grid), dim3(256), 0, st, (const __bf16*)Qp,
+                     (const __bf16*)KV, (const __bf16*)bias, (const int8_t*)mask, sm0, sm1, (__bf16*)out, so0, so1,
+                     (int)N, (int)ldn, (int)H, nqc, nrp);
+  return launched("tops_tri_attention_two_row");
 }
 
 }  // namespace tops
@@ -1285,6 +1270,21 @@ extern "C" int tops_tri_attention(const void* Qp, const void* KV, const void* bi
   if (dtype == TOPS_DTYPE_F16)
     return tri_attention_t<_Float16>(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, D, st);
   return fail(TOPS_EUNSUPPORTED, "tops_tri_attention: unsupported dtype code %d", dtype);
+}
+
+extern "C" int tops_tri_attention_two_row(const void* Qp, const void* KV, const void* bias, const void* mask,
+                                          int64_t sm0, int64_t sm1, void* out, int64_t so0, int64_t so1, int64_t N,
+                                          int64_t ldn, int64_t H, int64_t D, int dtype, void* stream) {
+  TOPS_REQUIRE(Qp && KV && bias && out, "tops_tri_attention_two_row: null pointer argument");
+  TOPS_REQUIRE(dtype == TOPS_DTYPE_BF16 && D == 32,
+               "tops_tri_attention_two_row: bf16 with D = 32 only (got dtype %d, D=%lld)", dtype, (long long)D);
+  TOPS_REQUIRE(H >= 1 && H <= 64 && N >= 0 && N <= kMaxN,
+               "tops_tri_attention_two_row: supports H <= 64 and N <= %d (got H=%lld N=%lld)", kMaxN, (long long)H,
+               (long long)N);
+  TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_attention_two_row: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
+               (long long)tri_ldn(N), (long long)ldn);
+  TOPS_REQUIRE(so0 % 4 == 0 && so1 % 4 == 0, "tops_tri_attention_two_row: out strides must be multiples of 4");
+  return tri_attention2(Qp, KV, bias, mask, sm0, sm1, out, so0, so1, N, ldn, H, (hipStream_t)stream);
 }
 
 extern "C" int tops_tri_repack(const void* q, const void* k, const void* v, const float* bias, void* Qp, void* KV,
