@@ -8,7 +8,6 @@ Large configurations are checked on a sample of output rows (rows are independen
 """
 
 import math
-import os
 
 import pytest
 import torch
@@ -414,10 +413,8 @@ def _two_row_mask(N, seed):
 # tri_attn2_kernel faulted the GPU in an earlier build, whose copies were inline-asm global_load_lds
 # with a base address rebuilt from v_readfirstlane halves.  Its copies now go through the compiler's
 # global_load_lds builtin (the compiler sets M0 and inserts the wait states), and its index
-# arithmetic is checked on the CPU by tests/test_tri_two_row_model.py.  The test stays off until
-# its one GPU run (TOPS_RUN_TWO_ROW=1) has passed.
-@pytest.mark.skipif(os.environ.get("TOPS_RUN_TWO_ROW") != "1",
-                    reason="two-row attention kernel: pending its first GPU run after the copy rewrite")
+# arithmetic is checked on the CPU by tests/test_tri_two_row_model.py; these tests passed on their
+# first GPU run after that rewrite.
 @pytest.mark.parametrize("N,mask", [(8, "two_row"), (33, "pad"), (130, "two_row"), (256, "pad"), (520, "two_row"),
                                     (1024, "pad")])
 def test_tri_two_row_kernel(device, N, mask):
@@ -475,8 +472,6 @@ def test_tri_two_row_kernel(device, N, mask):
         assert torch.equal(o3[valid_rows.to(device)], o2[valid_rows.to(device)]), "masked keys changed the output"
 
 
-@pytest.mark.skipif(os.environ.get("TOPS_RUN_TWO_ROW") != "1",
-                    reason="two-row attention kernel: pending its first GPU run after the copy rewrite")
 @pytest.mark.parametrize("shift", [150.0, -200.0])
 def test_tri_two_row_fallback(device, shift):
     """The two-row kernel's exact-max recomputation: shifted bias tiles (see

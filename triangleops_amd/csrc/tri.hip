@@ -984,11 +984,15 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   // ---- it: the bias load that follows a copy is not needed before the copy itself, so the
   // ---- copies keep their full lead.  The prologue issues the same sequence from visit 0. ----
   dma(0, IC<0>{});
+  __builtin_amdgcn_sched_barrier(0);  // (each group issues in program order)
   load_bias(0, 0, bset[0][0]);
   load_bias(0, 1, bset[0][1]);
+  __builtin_amdgcn_sched_barrier(0);
   dma(1, IC<1>{});
+  __builtin_amdgcn_sched_barrier(0);
   load_bias(1, 0, bset[1][0]);
   load_bias(1, 1, bset[1][1]);
+  __builtin_amdgcn_sched_barrier(0);
   dma(2, IC<2>{});
   __builtin_amdgcn_sched_barrier(0);
   vmcnt_wait<12>();  // this wave's copy of block 0 has landed (12 loads were issued after it)
@@ -1029,6 +1033,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     __syncthreads();
     load_bias(vj + 2, 0, bset[BS][0]);
     load_bias(vj + 2, 1, bset[BS][1]);
+    __builtin_amdgcn_sched_barrier(0);  // the bias loads before the copy
     dma(vj + 3, SC{});
     __builtin_amdgcn_sched_barrier(0);
     // stage (kt 1, row 1): next = (visit vj + 1, kt 0, row 0)
