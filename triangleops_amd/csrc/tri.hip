@@ -826,6 +826,19 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   const int nkb = ldn / 64, nqt = (N + 31) / 32, nkt = ldn / 32;
   const int qt = qc * NW + wave;
 
+  // ---- Q^T operands of both rows (scaled, d-permuted), loaded before the key-validity pass and
+  // ---- waited for after it, before the main loop's loads (which the compiler does not track) ----
+  const int irow[2] = {i0, i1};
+  int q = 32 * qt + col;
+  q = q < N ? q : N - 1;
+  V8 qop[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const T* qr = Qp + (((int64_t)irow[r] * H + h) * ldn + q) * D + 8 * hl;
+    qop[r][0] = ldg<V8>(qr);
+    qop[r][1] = ldg<V8>(qr + 16);
+  }
+
   // ---- key validity of both rows per 64-key block; the visit list is their union ----
   if (tid < 2) row_any[tid] = 0;
   __syncthreads();
@@ -854,11 +867,21 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   }
   __syncthreads();
   const int nv = nvblk;  // >= 1 whenever N >= 1
+  // visit j's block and its valid-key bits of both rows, held by lane j of every wave (nv <= 64,
+  // N <= 4096) and read with v_readlane in the loop: no LDS reads there besides the K / V operands
+  // (the compiler orders LDS reads it cannot separate from the asynchronous copies behind them)
+  const int mj = lane < nv ? lane : nv - 1;
+  const int vb_l = vblk[mj];
+  const unsigned long long kv0_l = kvalid[0][vb_l], kv1_l = kvalid[1][vb_l];
+  auto visit = [&](int vj) { return __builtin_amdgcn_readlane(vb_l, vj < nv ? vj : nv - 1); };
+  auto bits64 = [&](unsigned long long v, int vj) {
+    return ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), vj) << 32) |
+           (unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, vj);
+  };
 
   // ---- rows without a valid key take the uniform average of V over the N keys (PV products
   // ---- alone, tri_uniform_row): a pair of such rows skips the main loop; in a mixed pair the
   // ---- main loop's result for the uniform row is replaced at the end ----
-  const int irow[2] = {i0, i1};
   const int64_t kvoff[2] = {((int64_t)i0 * H + h) * nkb * kKVBlock, ((int64_t)i1 * H + h) * nkb * kKVBlock};
   if (uni[0] && uni[1]) {  // block-uniform
     tri_uniform_row<T, 1>(KV + kvoff[0], vblk, nv, N, out, i0, so0, so1, h, D, 32 * qt, lane);
@@ -866,16 +889,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     return;
   }
 
-  // ---- per-row operands: Q^T (scaled, d-permuted); the identity of the bias MFMAs ----
-  int q = 32 * qt + col;
-  q = q < N ? q : N - 1;
-  V8 qop[2][2], ident[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const T* qr = Qp + (((int64_t)irow[r] * H + h) * ldn + q) * D + 8 * hl;
-    qop[r][0] = ldg<V8>(qr);
-    qop[r][1] = ldg<V8>(qr + 16);
-  }
+  // ---- the identity of the bias MFMAs ----
+  V8 ident[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -894,12 +909,21 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     const int p = 64 * s + lane;
     gofs[s] = 16u * (uint32_t)(cpart == 0 ? ((p & ~3) | ((p & 3) ^ ((p >> 4) & 3))) : ((p & ~7) | ((p & 7) ^ ((p >> 4) & 7))));
   }
+  // The copies and the bias loads of the main loop are inline asm, so the compiler neither sees
+  // nor waits for them: with copies in flight its own wait counts would not be exact (it falls
+  // back to waiting for every load), and every wait of the loop is written out below.  The copy
+  // takes a 64-bit per-lane address in VGPRs (no SGPR base), and its `s_nop 4` puts 5 wait states
+  // between the write of M0 (the slot address, which the compiler moves there) and the load.
   auto dma = [&](int vj, auto sc) {
-    const int kb = vblk[vj < nv ? vj : nv - 1];
+    const int kb = visit(vj);
     const char* src = kvsrc + (int64_t)kb * kKVBlock * (int64_t)sizeof(T);
-    char* dst = &slot(sc)[crow][cpart * 4096];
+    const uint32_t dst = (uint32_t)reinterpret_cast<uintptr_t>(&slot(sc)[crow][cpart * 4096]);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) __builtin_amdgcn_global_load_lds(src + gofs[s], (LdsPtr)(dst + 1024 * s), 16, 0, 0);
+    for (int s = 0; s < 4; ++s) {
+      const char* a = src + gofs[s];
+      const uint32_t m = dst + 1024u * s;
+      asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(a), "{m0}"(m) : "memory");
+    }
   };
   // operand reads: K of row r, 32-key tile kt (A operand of S^T, k-steps j = 0, 1); V^T of
   // row r, tile kt (A operand of O^T)
@@ -916,10 +940,19 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
       v[j] = *reinterpret_cast<const V8*>(base + (((4 * kt + 2 * j + hl) ^ ((col >> 1) & 7)) << 4));
   };
   auto load_bias = [&](int vj, int kt, V8* b) {
-    const int kb = vblk[vj < nv ? vj : nv - 1];
+    const int kb = visit(vj);
     const T* p = bq + (int64_t)(2 * kb + kt) * 1024;
-    b[0] = ldg<V8>(p);
-    b[1] = ldg<V8>(p + 512);
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(b[0]) : "v"(p) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(b[1]) : "v"(p + 512) : "memory");
+  };
+  // after the explicit wait for a bias set: redefine its registers, so that no use of them can
+  // be scheduled above the wait
+  auto ready = [&](V8 (*b)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      pin(b[t][0]);
+      pin(b[t][1]);
+    }
   };
 
   f32x16 o[2], S[2];
@@ -983,6 +1016,13 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   // ---- complete in issue order, so a wait for one load also waits for every load issued before
   // ---- it: the bias load that follows a copy is not needed before the copy itself, so the
   // ---- copies keep their full lead.  The prologue issues the same sequence from visit 0. ----
+  vmcnt_wait<0>();  // Q (and the validity pass's mask loads) have landed
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    pin(qop[r][0]);
+    pin(qop[r][1]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   dma(0, IC<0>{});
   __builtin_amdgcn_sched_barrier(0);  // (each group issues in program order)
   load_bias(0, 0, bset[0][0]);
@@ -995,7 +1035,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   __builtin_amdgcn_sched_barrier(0);
   dma(2, IC<2>{});
   __builtin_amdgcn_sched_barrier(0);
-  vmcnt_wait<12>();  // this wave's copy of block 0 has landed (12 loads were issued after it)
+  vmcnt_wait<12>();  // this wave's copy of block 0 and bias set 0 have landed (12 loads behind them)
+  ready(bset[0]);
   __syncthreads();
   {
     V8 k[2];
@@ -1013,8 +1054,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     constexpr int SL = decltype(slc)::value, BS = SL % 2, BN = (BS + 1) % 2;
     using SN = IC<(SL + 1) % kRing>;
     using SC = IC<(SL + 3) % kRing>;
-    const int kb = vblk[vj];
-    const unsigned long long kv0 = kvalid[0][kb], kv1 = kvalid[1][kb];
+    const unsigned long long kv0 = bits64(kv0_l, vj), kv1 = bits64(kv1_l, vj);
     V8 k[2];
     // stage (kt 0, row 0): next = (0, row 1)
     read_k(slc, 1, 0, k);
@@ -1029,12 +1069,13 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     read_v(slc, 0, 1, vop[0]);
     stage(0, (unsigned int)(kv0 >> 32), true, 1, k, bset[BS][1]);
     __builtin_amdgcn_sched_barrier(0);
-    vmcnt_wait<8>();  // this wave's copy of block vj + 1 has landed
+    vmcnt_wait<8>();  // this wave's copy of block vj + 1 has landed (behind it: bias vj + 1, copy vj + 2)
     __syncthreads();
     load_bias(vj + 2, 0, bset[BS][0]);
     load_bias(vj + 2, 1, bset[BS][1]);
-    __builtin_amdgcn_sched_barrier(0);  // the bias loads before the copy
     dma(vj + 3, SC{});
+    vmcnt_wait<12>();  // bias set of visit vj + 1 has landed (behind it: copy vj + 2, bias vj + 2, copy vj + 3)
+    ready(bset[BN]);
     __builtin_amdgcn_sched_barrier(0);
     // stage (kt 1, row 1): next = (visit vj + 1, kt 0, row 0)
     read_k(SN{}, 0, 0, k);
@@ -1047,6 +1088,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     if (vj + 2 < nv) block(vj + 2, IC<2>{});
     if (vj + 3 < nv) block(vj + 3, IC<3>{});
   }
+  vmcnt_wait<0>();  // no copy may still be writing the block's LDS when its waves finish
   // ---- epilogue: PV of the last stage (row 1) ----
   o[1] = Mma<T>::m32(vop[1][0], P[1][0], o[1]);
   o[1] = Mma<T>::m32(vop[1][1], P[1][1], o[1]);
@@ -1283,8 +1325,8 @@ extern "C" int tops_tri_attention_two_row(const void* Qp, const void* KV, const 
   TOPS_REQUIRE(Qp && KV && bias && out, "tops_tri_attention_two_row: null pointer argument");
   TOPS_REQUIRE(dtype == TOPS_DTYPE_BF16 && D == 32,
                "tops_tri_attention_two_row: bf16 with D = 32 only (got dtype %d, D=%lld)", dtype, (long long)D);
-  TOPS_REQUIRE(H >= 1 && H <= 64 && N >= 0 && N <= kMaxN,
-               "tops_tri_attention_two_row: supports H <= 64 and N <= %d (got H=%lld N=%lld)", kMaxN, (long long)H,
+  TOPS_REQUIRE(H >= 1 && H <= 64 && N >= 0 && N <= 4096,
+               "tops_tri_attention_two_row: supports H <= 64 and N <= 4096 (got H=%lld N=%lld)", (long long)H,
                (long long)N);
   TOPS_REQUIRE(ldn == tri_ldn(N), "tops_tri_attention_two_row: ldn must be max(64, round_up(N, 64)) = %lld (got %lld)",
                (long long)tri_ldn(N), (long long)ldn);
