@@ -306,20 +306,24 @@ __global__ __launch_bounds__(256) void apb_combine_kernel(const float* __restric
 
 // Split merge fused with the gate and output projection of attention_pair_bias
 // (attn_pair_bias/module.py:69-70: out = ((Og * sigmoid(X . Wg^T + bg)) -> io) . Wo^T + bo), C = 128:
-// one block per 32 queries, 4 waves.  Thread t merges the split partials of query t / 8, channels
-// 32 g + 4 (t % 8) + e of every head g, in apb_combine_kernel's arithmetic and order, so the merged
-// Og has the same bits, and stages it in LDS beside the block's 32 rows of X; then wave w computes
-// features [32 w, +32) of both GEMMs for the 32 queries exactly as gate_out_kernel does (weight
-// rows in registers, permuted so each lane holds 16 consecutive features of one query; the gated
-// values overwrite Og in LDS; the output goes through a query-major LDS tile to whole-row stores).
+// one block per 16 queries, 4 waves (the kernel is bound by the latency of its loads, so more,
+// smaller blocks finish sooner).  Thread t merges the split partials of query t / 16, channels
+// 32 g + 8 (t % 4) + e (e < 8) of head g = (t % 16) / 4, in apb_combine_kernel's arithmetic and
+// order, so the merged Og has the same bits, and stages it in LDS beside the block's 16 rows of X;
+// then wave w computes features [32 w, +32) of both GEMMs exactly as gate_out_kernel does (weight
+// rows in registers, permuted so each lane holds 16 consecutive features of one query; the 32
+// MFMA columns hold the 16 queries twice; the gated values overwrite Og in LDS; the output goes
+// through a query-major LDS tile to whole-row stores).
 // RES: out = res + result, the single-representation residual of a Pairformer block, rounded once.
+constexpr int kApbMergeTok = 16;  // queries per block of apb_merge_gate_kernel
+
 template <typename T, bool RES>
 __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __restrict__ ws, const T* __restrict__ X,
                                                             const T* __restrict__ Wg, const T* __restrict__ bg,
                                                             const T* __restrict__ Wo, const T* __restrict__ bo,
                                                             const T* __restrict__ res, T* __restrict__ out,
                                                             int64_t M, int nsplit) {
-  constexpr int C = 128, H = 4, TOK = 32, ROW = C * 2, KS = C / 16;
+  constexpr int C = 128, H = 4, TOK = kApbMergeTok, ROW = C * 2, KS = C / 16;
   using V8 = vec<T, 8>;
   __shared__ __attribute__((aligned(16))) char og_s[TOK * ROW];  // merged Og, then the gated values
   __shared__ __attribute__((aligned(16))) char x_s[TOK * ROW];   // gate input X
@@ -336,9 +340,8 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     cst[1][i] = bo ? (float)bo[i] : 0.f;
   }
   // X rows of the block's queries (rows past M repeat row M - 1; their results are not stored)
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int ci = k * 256 + tid, t = ci >> 4, c = ci & 15;
+  {
+    const int t = tid >> 4, c = tid & 15;
     const int64_t q = q0 + t < M ? q0 + t : M - 1;
     *reinterpret_cast<V8*>(&x_s[t * ROW + swz(t, c)]) = ldg<V8>(X + q * C + 8 * c);
   }
@@ -354,80 +357,63 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     }
   }
   // ---- merge the split partials ----
-  // thread t: query t / 8, channels 32 g + 4 (t % 8) + e of head g (g, e < 4): the 8 threads of a
-  // query read one whole 128-byte line of head g per load instruction, and each thread needs the
-  // (m, l) pairs of all four heads (32 contiguous bytes per split, broadcast to the 8 threads)
+  // thread t: query t / 16, head g = (t % 16) / 4, channels 32 g + 8 (t % 4) + e: each thread reads
+  // its head's (m, l) pair and 32 contiguous bytes of O per split
   {
-    const int t = tid >> 3, j = tid & 7;
+    const int t = tid >> 4, j = tid & 15, g = j >> 2;
     const int64_t q = q0 + t < M ? q0 + t : M - 1;
-    const float* ml = ws + (int64_t)nsplit * M * C + q * H * 2;  // split s: + s * M * H * 2
-    const float* op = ws + q * C + 4 * j;                         // split s: + s * M * C; head g: + 32 g
+    const float* ml = ws + (int64_t)nsplit * M * C + (q * H + g) * 2;  // split s: + s * M * H * 2
+    const float* op = ws + q * C + 32 * g + 8 * (j & 3);                // split s: + s * M * C
     const int64_t sml = M * H * 2, so = M * C;
     // batches of 16 splits with every load of a batch issued before its first use; per element the
     // sums run in split order with apb_combine_kernel's arithmetic, so Og gets the same bits
     constexpr int SB = 16;
-    float mx[H];
-#pragma unroll
-    for (int g = 0; g < H; ++g) mx[g] = -INFINITY;
+    using F2 = vec<float, 2>;
+    float mx = -INFINITY;
     for (int s0 = 0; s0 < nsplit; s0 += SB) {
-      f32x4 mb[SB][2];
+      F2 mb[SB];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int s = s0 + i < nsplit ? s0 + i : s0;  // past the batch: split s0 again (unused)
-        mb[i][0] = ldg<f32x4>(ml + s * sml);
-        mb[i][1] = ldg<f32x4>(ml + s * sml + 4);
+        mb[i] = ldg<F2>(ml + s * sml);
       }
 #pragma unroll
       for (int i = 0; i < SB; ++i)
-        if (s0 + i < nsplit) {
-          mx[0] = fmaxf(mx[0], mb[i][0][0]);
-          mx[1] = fmaxf(mx[1], mb[i][0][2]);
-          mx[2] = fmaxf(mx[2], mb[i][1][0]);
-          mx[3] = fmaxf(mx[3], mb[i][1][2]);
-        }
+        if (s0 + i < nsplit) mx = fmaxf(mx, mb[i][0]);
     }
-    float mu[H], lt[H], ot[H][4];
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float lt = 0.f, ot[8];
 #pragma unroll
-    for (int g = 0; g < H; ++g) {
-      mu[g] = mx[g] == -INFINITY ? 0.f : mx[g];
-      lt[g] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ot[g][e] = 0.f;
-    }
+    for (int e = 0; e < 8; ++e) ot[e] = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += SB) {
-      f32x4 mb[SB][2], ob[SB][H];
+      F2 mb[SB];
+      f32x4 ob[SB][2];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int s = s0 + i < nsplit ? s0 + i : s0;
-        mb[i][0] = ldg<f32x4>(ml + s * sml);
-        mb[i][1] = ldg<f32x4>(ml + s * sml + 4);
-#pragma unroll
-        for (int g = 0; g < H; ++g) ob[i][g] = ldg<f32x4>(op + s * so + 32 * g);
+        mb[i] = ldg<F2>(ml + s * sml);
+        ob[i][0] = ldg<f32x4>(op + s * so);
+        ob[i][1] = ldg<f32x4>(op + s * so + 4);
       }
 #pragma unroll
       for (int i = 0; i < SB; ++i)
         if (s0 + i < nsplit) {
+          const float w = fast_exp2((mb[i][0] - mu) * kLog2e);
+          lt += w * mb[i][1];
 #pragma unroll
-          for (int g = 0; g < H; ++g) {
-            const float m = mb[i][g >> 1][2 * (g & 1)], l = mb[i][g >> 1][2 * (g & 1) + 1];
-            const float w = fast_exp2((m - mu[g]) * kLog2e);
-            lt[g] += w * l;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ot[g][e] += w * ob[i][g][e];
-          }
+          for (int e = 0; e < 8; ++e) ot[e] += w * ob[i][e >> 2][e & 3];
         }
     }
+    V8 r;
 #pragma unroll
-    for (int g = 0; g < H; ++g) {  // channels 32 g + 4 j .. + 3: half of 16-byte chunk 4 g + j / 2
-      vec<T, 4> r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = (T)(ot[g][e] / lt[g]);
-      *reinterpret_cast<vec<T, 4>*>(&og_s[t * ROW + swz(t, 4 * g + (j >> 1)) + 8 * (j & 1)]) = r;
-    }
+    for (int e = 0; e < 8; ++e) r[e] = (T)(ot[e] / lt);
+    *reinterpret_cast<V8*>(&og_s[t * ROW + swz(t, 4 * g + (j & 3))]) = r;
   }
   __syncthreads();  // cst, X and Og staged
 
-  const int tok = col, f0 = 32 * wave + 16 * hl;
+  // MFMA column col holds query col % TOK (the block's queries twice; both copies write the same
+  // values to the same LDS locations)
+  const int tok = col % TOK, f0 = 32 * wave + 16 * hl;
   {  // GEMM 1, sigmoid gate, Og * gate -> in place over the Og tile
     const char* grow = &x_s[tok * ROW];
     char* orow = &og_s[tok * ROW];
@@ -466,26 +452,28 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     }
   }
   __syncthreads();  // output tile complete
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int ci = k * 256 + tid, t = ci >> 4, c = ci & 15;
+  {
+    const int t = tid >> 4, c = tid & 15;
     const int64_t q = q0 + t;
-    if (q >= M) continue;
-    V8 v = *reinterpret_cast<const V8*>(&o_s[t * C + ((c ^ row_key<C>(t)) << 3)]);
-    if constexpr (RES) {
-      const V8 r = ldg<V8>(res + q * C + 8 * c);
+    if (q < M) {
+      V8 v = *reinterpret_cast<const V8*>(&o_s[t * C + ((c ^ row_key<C>(t)) << 3)]);
+      if constexpr (RES) {
+        const V8 rr = ldg<V8>(res + q * C + 8 * c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (T)((float)r[e] + (float)v[e]);
+        for (int e = 0; e < 8; ++e) v[e] = (T)((float)rr[e] + (float)v[e]);
+      }
+      stg<V8>(out + q * C + 8 * c, v);
     }
-    stg<V8>(out + q * C + 8 * c, v);
   }
 }
 
 // Q / K / V pre-pass at the tuned shape (C = H*D = 128, H = 4, D = 32): 32 tokens per block,
-// wave h computes head h's 32 channels of q, k and v (8 MFMA k-steps each; lane col holds 16 of
-// the 32 channels of token q0 + col, the other 16 in lane col + 32).  With QKN the per-token
-// LayerNorm over all 128 channels of q and k takes its sums from the four head waves through LDS
-// (two passes: mean, then centred squares).  q is scaled by qscale last.
+// wave h computes head h's 32 channels (8 MFMA k-steps each; lane col holds 16 of the 32 channels
+// of token q0 + col, the other 16 in lane col + 32).  Without QKN each block computes one of q, k,
+// v (blockIdx.x % 3) for its 32 tokens: three times the blocks, each with a third of the weight
+// loads and MFMA chain, so the latency-bound pass finishes sooner.  With QKN a block computes all
+// three, and the per-token LayerNorm over all 128 channels of q and k takes its sums from the four
+// head waves through LDS (two passes: mean, then centred squares).  q is scaled by qscale last.
 template <typename T, bool QKN>
 __global__ __launch_bounds__(256) void apb_qkv_kernel(const T* __restrict__ X, const T* __restrict__ wqkv,
                                                      const T* __restrict__ bq, const T* __restrict__ gq,
@@ -499,13 +487,34 @@ __global__ __launch_bounds__(256) void apb_qkv_kernel(const T* __restrict__ X, c
   __shared__ float red[2][4][32];  // [q / k][head][token]: per-head partial sums
   const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
-  const int64_t q0 = (int64_t)blockIdx.x * 32;
+  const int64_t q0 = (int64_t)(QKN ? blockIdx.x : blockIdx.x / 3) * 32;
   int64_t tok = q0 + col;
   tok = tok < M ? tok : M - 1;
   V8 xs[8];
 #pragma unroll
   for (int s = 0; s < 8; ++s) xs[s] = ldg<V8>(X + tok * C + 16 * s + 8 * hl);
   const T* wh = wqkv + (int64_t)h * 3 * D * C;
+  // slot v of acc[t]: channel h*D + dch(v) of token q0 + col
+  auto dch = [&](int v) { return 8 * (v >> 2) + 4 * hl + (v & 3); };
+  if constexpr (!QKN) {  // one of q, k, v: t = blockIdx.x % 3
+    const int t = (int)(blockIdx.x % 3);
+    f32x16 acc = {};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc = Mma<T>::m32(ldg<V8>(wh + (int64_t)(t * D + col) * C + 16 * s + 8 * hl), xs[s], acc);
+    if (t == 0 && bq) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[v] += (float)bq[h * D + dch(v)];
+    }
+    if (q0 + col >= M) return;
+    T* dst = (t == 0 ? qo : t == 1 ? ko : vo) + (q0 + col) * HD + h * D;
+    const float f = t == 0 ? qscale : 1.0f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      V4 r = {(T)(acc[4 * g] * f), (T)(acc[4 * g + 1] * f), (T)(acc[4 * g + 2] * f), (T)(acc[4 * g + 3] * f)};
+      stg<V4>(dst + 8 * g + 4 * hl, r);
+    }
+    return;
+  }
   f32x16 acc[3];
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
@@ -513,8 +522,6 @@ __global__ __launch_bounds__(256) void apb_qkv_kernel(const T* __restrict__ X, c
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc[t] = Mma<T>::m32(ldg<V8>(wh + (int64_t)(t * D + col) * C + 16 * s + 8 * hl), xs[s], acc[t]);
   }
-  // slot v of acc[t]: channel h*D + dch(v) of token q0 + col
-  auto dch = [&](int v) { return 8 * (v >> 2) + 4 * hl + (v & 3); };
   if (bq) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[0][v] += (float)bq[h * D + dch(v)];
@@ -590,7 +597,7 @@ static int apb_qkv_t(const void* X, const void* wqkv, const void* bq, int qkn, c
                        (const T*)wqkv, (const T*)bq, (const T*)gq, (const T*)bqn, (const T*)gk, (const T*)bkn, (T*)q,
                        (T*)k, (T*)v, M, qscale, eps);
   else
-    hipLaunchKernelGGL((apb_qkv_kernel<T, false>), dim3((unsigned)blocks), dim3(256), 0, st, (const T*)X,
+    hipLaunchKernelGGL((apb_qkv_kernel<T, false>), dim3((unsigned)(3 * blocks)), dim3(256), 0, st, (const T*)X,
                        (const T*)wqkv, (const T*)bq, (const T*)gq, (const T*)bqn, (const T*)gk, (const T*)bkn, (T*)q,
                        (T*)k, (T*)v, M, qscale, eps);
   return launched("apb_qkv_kernel");
@@ -747,7 +754,7 @@ extern "C" int64_t tops_apb_gated_workspace_bytes(int64_t M, int64_t H, int64_t 
 template <typename T>
 static int apb_merge_gate_t(const float* part, const void* X, const void* Wg, const void* bg, const void* Wo,
                             const void* bo, const void* res, void* out, int64_t M, int nsplit, hipStream_t st) {
-  const int64_t blocks = (M + 31) / 32;
+  const int64_t blocks = (M + kApbMergeTok - 1) / kApbMergeTok;
   if (res)
     hipLaunchKernelGGL((apb_merge_gate_kernel<T, true>), dim3((unsigned)blocks), dim3(256), 0, st, part, (const T*)X,
                        (const T*)Wg, (const T*)bg, (const T*)Wo, (const T*)bo, (const T*)res, (T*)out, M, nsplit);
