@@ -9,6 +9,7 @@ the library's message.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 
 import torch
@@ -116,27 +117,40 @@ def load(path: str = LIB_PATH):
     return lib
 
 
+_fns: dict = {}
+
+
 def call(name: str, *args) -> None:
     """Calls C entry point `name`; raises RuntimeError with the library's message on failure."""
-    lib = _lib if _lib is not None else load()
-    rc = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        lib = _lib if _lib is not None else load()
+        fn = _fns[name] = getattr(lib, name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.tops_last_error().decode(errors="replace")
+        msg = _lib.tops_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed (code {rc}): {msg}")
 
 
+@functools.lru_cache(maxsize=256)
 def apb_workspace_bytes(M: int, H: int, D: int) -> int:
     lib = _lib if _lib is not None else load()
     return int(lib.tops_apb_workspace_bytes(M, H, D))
 
 
+@functools.lru_cache(maxsize=256)
 def apb_gated_workspace_bytes(M: int, H: int, D: int) -> int:
     lib = _lib if _lib is not None else load()
     return int(lib.tops_apb_gated_workspace_bytes(M, H, D))
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """Raw hipStream_t of torch's current stream on `t`'s device."""
+    """Raw hipStream_t of torch's current stream on `t`'s device (without building a Stream object)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
