@@ -10,6 +10,8 @@ symbolic data: every LDS chunk of a slot is written exactly once, and the swizzl
 return the K row / V^T row chunk the MFMA layout asks for.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -195,3 +197,57 @@ def test_global_accesses_in_bounds(N, kind):
     hs = np.concatenate([h, h])
     np.add.at(cover, (rows[:, None], qcs[:, None] * 128 + np.arange(128)[None, :], hs[:, None]), 1)
     assert (cover[:N, :N] == 1).all()
+
+
+def _hipcc():
+    import shutil
+
+    for c in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if c and os.path.exists(c):
+            return c
+    return None
+
+
+@pytest.mark.skipif(_hipcc() is None, reason="hipcc not available")
+def test_two_row_copy_asm_hazards(tmp_path):
+    """The two-row kernel's inline-asm loads, in the gfx950 assembly the build produces: every
+    global_load_lds takes a 64-bit per-lane VGPR address (no SGPR base, so no VALU-written SGPR is
+    read by the load) and sits right behind an `s_nop 4` or longer (the M0 write that precedes it
+    gets at least 5 wait states); and no register a bias load writes is read before the next
+    vmcnt wait (no copy of an in-flight load)."""
+    import re
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    src = os.path.join(root, "triangleops_amd", "csrc", "tri.hip")
+    asm = tmp_path / "tri.s"
+    cmd = [_hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", "-o", str(asm), src]
+    subprocess.run(cmd, check=True, capture_output=True)
+    text = asm.read_text()
+    m = re.search(r"\n(_ZN4tops16tri_attn2_kernel\w*):(.*?)s_endpgm", text, re.S)
+    assert m, "tri_attn2_kernel not found in the assembly"
+    body = [ln.strip() for ln in m.group(2).splitlines()
+            if ln.strip() and not ln.strip().startswith((";", "."))]
+    ndma = 0
+    pending = set()
+    for idx, ln in enumerate(body):
+        op = ln.split()[0]
+        if op == "global_load_lds_dwordx4":
+            ndma += 1
+            assert re.search(r"v\[\d+:\d+\], off$", ln), f"copy without a VGPR address: {ln}"
+            prev = body[idx - 1]
+            assert re.match(r"s_nop ([4-9]|1[0-5])$", prev), f"copy not behind s_nop >= 4: {prev} / {ln}"
+            continue
+        if op.startswith("s_waitcnt") and "vmcnt" in ln:
+            pending.clear()
+            continue
+        if pending and " " in ln:
+            for part in ln.split(None, 1)[1].split(",")[1:]:
+                for mm in re.finditer(r"v\[(\d+):(\d+)\]|v(\d+)\b", part):
+                    regs = range(int(mm.group(1)), int(mm.group(2)) + 1) if mm.group(1) else [int(mm.group(3))]
+                    assert not (set(regs) & pending), f"in-flight load register read early: {ln}"
+        if op == "global_load_dwordx4":
+            mm = re.match(r"global_load_dwordx4 v\[(\d+):(\d+)\]", ln)
+            pending.update(range(int(mm.group(1)), int(mm.group(2)) + 1))
+    assert ndma >= 8
