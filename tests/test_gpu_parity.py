@@ -367,6 +367,16 @@ def test_tri_padded_heads_not_multiple_of_8(device):
     _check(_tri_call(inp, device), _tri_ref(inp), torch.bfloat16, "tri D=12")
 
 
+def _bias_rows_below_n(bias, N):
+    """The pre-pass bias tiles (H, ceil(N/32), ldn/32, 1024) as fp32 with the rows of queries >= N
+    (in the last query tile; the pre-pass never writes them and the attention never reads them) set
+    to zero.  Element (q, k) = (32 qt + c, ...) of a tile sits at (64 j + 32 hl + c) * 8 + e."""
+    b = bias.float()
+    c = (torch.arange(1024, device=b.device) // 8) % 32
+    q = 32 * torch.arange(b.shape[1], device=b.device)[:, None] + c[None, :]  # (qt, 1024)
+    return torch.where((q < N)[None, :, None, :], b, torch.zeros_like(b))
+
+
 @pytest.mark.parametrize("N,shift", [(200, 150.0), (200, -200.0), (520, 150.0), (2100, -200.0)])
 def test_tri_shift_free_softmax_fallback(device, N, shift):
     """bf16 triangle attention takes the weights as 2^s without the row max and recomputes a wave's
@@ -384,7 +394,7 @@ def test_tri_shift_free_softmax_fallback(device, N, shift):
                                         inp["B_proj_z"], 4, 32)
     Qp, KV, bias, ldn = prep_forward(inp["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"],
                                      scale=inp["scale"])
-    b0 = bias.float().round()
+    b0 = _bias_rows_below_n(bias, N).round()
     b1 = b0.clone()
     b1[0] += shift
     b1[2, 2:4] += shift
@@ -485,7 +495,7 @@ def test_tri_two_row_fallback(device, shift):
                                         d["B_proj_z"], 4, 32)
     Qp, KV, bias, ldn = prep_forward(d["X"], pre["W_ln"], pre["B_ln"], pre["wqkv_hm"], pre["WZ_c"], pre["BZ"],
                                      scale=d["scale"])
-    b0 = bias.float().round()
+    b0 = _bias_rows_below_n(bias, N).round()
     b1 = b0.clone()
     b1[0] += shift
     b1[2, 2:4] += shift
