@@ -275,13 +275,14 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 // Per (32-key tile, query tile) a wave runs
 //     S^T  = C0 + I . bias^T          2 MFMAs, A = identity, B = 16 bias bytes per lane
 //          + K . Q^T                  2 MFMAs, K from LDS, Q^T in registers
-//     P    = exp2(S^T), l += rowsum   16 v_exp per lane, no max / subtract per element
+//     P    = exp2(S^T)                16 v_exp per lane, no max / subtract per element
 //     O^T += V^T . P^T                2 MFMAs, V^T from LDS, P^T = S^T's D registers
+//     l   += 1 . P^T                  2 16x16x32 MFMAs on the same P^T (bf16; row_sum_selector)
 // Softmax is invariant to a per-row shift m of the scores; m only keeps exp2 in range.
 //   bf16 (OPT): m = 0 throughout.  bf16 has fp32's exponent range, so P = 2^s, the row sums and
 //   O stay exact in relative terms for scores s in about (-60, 100) (log2 units); the row sum l
-//   (fp32 adds of the unrounded weights, as the reference's l += sum(p)) is checked once at the
-//   end, and a wave whose l left [2^-60, 2^100] (or is not finite) recomputes its query tiles
+//   (fp32 sums of the rounded weights the PV product uses, by the matrix cores) is checked once
+//   at the end, and a wave whose l left [2^-60, 2^100] (or is not finite) recomputes its tiles
 //   with an exact running max (tri_exact_tile, out of line).  The loop itself then has no max,
 //   no subtraction, no per-tile overflow test and no accumulator initialiser (C0 = 0).
 //   fp16: C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m is
@@ -337,7 +338,7 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
       acc = Mma<T>::m32(ldg<V8>(vt + 32 * kt + 16), pone[1], acc);
     }
   }
-  // O = acc / N for every query of the wave (l = N, as halves_sum gives it in the main loop)
+  // O = acc / N for every query of the wave (l = N: N weights of exactly 1)
   const float inv = 1.0f / (float)N;
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
@@ -353,6 +354,23 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
       }
     }
   }
+}
+
+// Row sums of the weights on the matrix cores.  One v_mfma_f32_16x16x32 per 16-key half takes the
+// P^T operand of the PV product as its B (as a 32x32x16 B, lane L holds keys 8 (L / 32) + e of
+// query L % 32; read as a 16x16x32 B, rows 8 (L / 16) + e of column L % 16) against this 0/1
+// selector as A: its rows 0 and 8 add up the B rows that belong to queries 0-15 (L / 16 even),
+// rows 4 and 12 those of queries 16-31 (L / 16 odd).  The D element in row 4 (L / 16), column
+// L % 16 -- slot 0 of lane L -- then accumulates the sum of query L % 32's rounded weights, in
+// every lane, with fp32 adds inside the matrix core and no VALU work.
+template <typename T>
+__device__ inline vec<T, 8> row_sum_selector(int lane) {
+  const int m = lane & 15, g = lane >> 4;  // A row m, k rows 8 g .. 8 g + 7
+  const bool one = ((m == 0 || m == 8) && (g & 1) == 0) || ((m == 4 || m == 12) && (g & 1) == 1);
+  vec<T, 8> a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = (T)(one ? 1.f : 0.f);
+  return a;
 }
 
 // One query tile (32 queries of row i, head h) recomputed with an exact running max: the
@@ -558,14 +576,17 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
     for (int e = 0; e < 8; ++e) ident[j][e] = (T)((!uniform && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
 
   f32x16 o[QT], cinit[QT];
-  float l[QT];
+  float l[QT];   // fp16: row sums (lanes l and l ^ 32 hold halves)
+  f32x4 ls[QT];  // bf16: row sums accumulated by the matrix cores, slot 0 = the query's whole sum
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     o[t] = f32x16{};
     cinit[t] = f32x16{};
     l[t] = 0.f;
+    ls[t] = f32x4{};
   }
   bool first = true;
+  const V8 lsel = row_sum_selector<T>(lane);  // bf16: row sums on the matrix cores
 
   // scores of one 32-key tile for all query tiles
   auto scores = [&](const V8* kop, V8 (*bb)[2], f32x16* s) {
@@ -610,21 +631,13 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
       if constexpr (OPT) {
-        // weights 2^s and their row sum: fp32 adds of the unrounded weights (full-rate VALU,
-        // which co-issues with the MFMAs; packed dot products stall them)
-        float e[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) e[v] = fast_exp2(s[t][v]);
+        // weights 2^s; their row sums go to the matrix cores with the PV product below
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-          p[t][0][v] = (T)e[v];
-          p[t][1][v] = (T)e[8 + v];
+          p[t][0][v] = (T)fast_exp2(s[t][v]);
+          p[t][1][v] = (T)fast_exp2(s[t][8 + v]);
         }
-#pragma unroll
-        for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-          for (int v = 0; v < w; ++v) e[v] += e[v + w];
-        ps[t] = e[0];
+        ps[t] = 0.f;
       } else {
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
@@ -638,7 +651,7 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
       pin(p[t][0]);
       pin(p[t][1]);
     }
-    constexpr int VPM = OPT ? 10 : 9;  // VALU instructions per score MFMA in the interleave
+    constexpr int VPM = OPT ? (NW == 4 ? 8 : 6) : 9;  // VALU instructions per score MFMA in the interleave
     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
     for (int m = 0; m < 2 * QT; ++m) {
@@ -680,9 +693,14 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
     }
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      l[t] += ps[t];
       o[t] = Mma<T>::m32(vop[0], p[t][0], o[t]);
       o[t] = Mma<T>::m32(vop[1], p[t][1], o[t]);
+      if constexpr (OPT) {
+        ls[t] = Mma<T>::m16(lsel, p[t][0], ls[t]);
+        ls[t] = Mma<T>::m16(lsel, p[t][1], ls[t]);
+      } else {
+        l[t] += ps[t];
+      }
     }
   };
 
@@ -731,7 +749,7 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
     bool bad = false;
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      const float lt = halves_sum(l[t]);
+      const float lt = ls[t][0];
       bad |= !(lt >= 0x1p-60f && lt <= 0x1p100f);
     }
     if (__ballot(bad) != 0) {  // wave-uniform
@@ -747,7 +765,7 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int64_t q = qbase + 32 * t + col;
-    const float inv = 1.0f / halves_sum(l[t]);
+    const float inv = 1.0f / (OPT ? ls[t][0] : halves_sum(l[t]));
     if (q < N) {
       T* dst = out + i * so0 + q * so1 + (int64_t)h * dv + 4 * hl;
 #pragma unroll
@@ -765,8 +783,8 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
 // 128 queries of one head; wave w owns query tile qt = 4 qc + w of both rows.  Per 32-key tile the
 // wave runs, for row r = 0 then 1 (a "stage" each):
 //     S_r^T = I . B^T + K_r . Q_r^T              4 MFMAs
-//     P_r   = 2^(S_r^T), l_r += sum P_r          16 v_exp, 8 packed converts, 15 fp32 adds
-//     O_r^T += V_r^T . P_r^T                     2 MFMAs
+//     P_r   = 2^(S_r^T)                          16 v_exp, 8 packed converts
+//     O_r^T += V_r^T . P_r^T, l_r += 1 . P_r^T    2 MFMAs + 2 16x16x32 MFMAs (row_sum_selector)
 // with the one-row kernel's shift-free softmax (weights 2^s, row sums l checked once at the end;
 // a wave whose l left [2^-60, 2^100] recomputes its tiles with an exact running max).  The bias
 // operand B (16 bytes per lane and half) is loaded once per tile for both rows, so a bias tile costs
@@ -956,9 +974,13 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   };
 
   f32x16 o[2], S[2];
-  float l[2] = {0.f, 0.f};
+  f32x4 ls[2];  // row sums by the matrix cores (slot 0 = the query's sum), as in tri_attn_kernel
+  const vec<T, 8> lsel = row_sum_selector<T>(lane);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) o[r] = f32x16{};
+  for (int r = 0; r < 2; ++r) {
+    o[r] = f32x16{};
+    ls[r] = f32x4{};
+  }
   V8 P[2][2], vop[2][2];
   V8 bset[2][2][2];  // bias operands of visits vj, vj + 1 (set vj % 2): [tile][half]
 
@@ -976,6 +998,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     if (pv) {
       o[1 - r] = Mma<T>::m32(vop[1 - r][0], P[1 - r][0], o[1 - r]);
       o[1 - r] = Mma<T>::m32(vop[1 - r][1], P[1 - r][1], o[1 - r]);
+      ls[1 - r] = Mma<T>::m16(lsel, P[1 - r][0], ls[1 - r]);
+      ls[1 - r] = Mma<T>::m16(lsel, P[1 - r][1], ls[1 - r]);
     }
     f32x16 s = S[r];
     if (tb != 0xffffffffu) {  // partial tile (wave-uniform): masked keys get weight 0
@@ -984,30 +1008,23 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
       for (int v = 0; v < 16; ++v) s[v] = ((lb >> (8 * (v / 4) + (v % 4))) & 1u) ? s[v] : -INFINITY;
     }
     S[rn] = scores(rn, kn, bn);
-    float e[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) e[v] = fast_exp2(s[v]);
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
-      P[r][0][v] = (T)e[v];
-      P[r][1][v] = (T)e[8 + v];
+      P[r][0][v] = (T)fast_exp2(s[v]);
+      P[r][1][v] = (T)fast_exp2(s[8 + v]);
     }
     pin(P[r][0]);
     pin(P[r][1]);
 #pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int v = 0; v < w; ++v) e[v] += e[v + w];
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
+    for (int m = 0; m < 2; ++m) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 5, 0);
     }
-    l[r] += e[0];
   };
 
   // ---- prologue.  Every global load of the main loop is issued in one place per block, after
@@ -1092,6 +1109,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   // ---- epilogue: PV of the last stage (row 1) ----
   o[1] = Mma<T>::m32(vop[1][0], P[1][0], o[1]);
   o[1] = Mma<T>::m32(vop[1][1], P[1][1], o[1]);
+  ls[1] = Mma<T>::m16(lsel, P[1][0], ls[1]);
+  ls[1] = Mma<T>::m16(lsel, P[1][1], ls[1]);
 
   // ---- per row: the uniform average (a row without valid keys), an exact-max recomputation
   // ---- (a wave whose shift-free row sums left [2^-60, 2^100] or are not finite), or O / l ----
@@ -1103,7 +1122,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
       tri_uniform_row<T, 1>(KV + kvoff[r], vblk, nv, N, out, irow[r], so0, so1, h, D, 32 * qt, lane);
       continue;
     }
-    const float lt = halves_sum(l[r]);
+    const float lt = ls[r][0];
     if (__ballot(!(lt >= 0x1p-60f && lt <= 0x1p100f)) != 0) {  // wave-uniform
       tri_exact_tile<T>(KV + kvoff[r], bq, qop[r][0], qop[r][1], ident[0], ident[1], vblk, kvalid[r], nv, N, out,
                         irow[r], so0, so1, h, D, qo, lane);
