@@ -164,12 +164,13 @@ def check_device(*tensors) -> None:
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        d = t.get_device()  # device index, -1 off the GPU
+        if d < 0:
             raise ValueError(f"triangleops_amd kernels need GPU tensors (got a tensor on {t.device})")
         if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"all tensors must be on one device (got {dev} and {t.device})")
+            dev = d
+        elif d != dev:
+            raise ValueError(f"all tensors must be on one device (got cuda:{dev} and {t.device})")
 
 
 def vec16_ok(t: torch.Tensor) -> bool:

@@ -89,47 +89,62 @@ def apb_forward_gated(X, Z, W_combined, sum_W_combined, B_const, wqkv_hm, W_g, b
     the attention with the gate and output projection of attn_pair_bias/module.py:69-70 fused.  With
     split keys: tops_apb_forward (Og = NULL) then tops_apb_merge_gate (the split merge, gate and W_o in
     one kernel); otherwise tops_apb_forward_gated.  Requires gated_ok(...); returns (M, 128)."""
-    M, C = X.shape
-    H = W_combined.shape[0]
-    D = wqkv_hm.shape[2]
-    assert gated_ok(X, Z, W_combined, W_g, W_o, residual) and D == 32
-    code = io_dtype_code(X.dtype)
-    _native.check_device(X, Z, wqkv_hm, W_combined, W_g, W_o, mask, residual)
-    X = _native.dense(X)  # X, the weights, biases and residual are indexed without strides
-    Z = _native.vec16(Z)  # Z's strides are passed
+    assert gated_ok(X, Z, W_combined, W_g, W_o, residual) and wqkv_hm.shape[2] == 32
+    return gated_forward(X, Z, W_combined, sum_W_combined, B_const, wqkv_hm, W_g, b_g, W_o, b_o, scale, eps, mask,
+                         residual)
+
+
+def _dense_as(t, dt):
+    """_native.dense(t, dt) with the common case (already dense, aligned, of dtype dt) tested inline."""
+    if t is None or (t.dtype is dt and t.is_contiguous() and t.data_ptr() % 16 == 0):
+        return t
+    return _native.dense(t, dt)
+
+
+def gated_forward(X, Z, Wc, sWc, Bc, wqkv_hm, W_g, b_g, W_o, b_o, scale, eps, mask, residual):
+    """apb_forward_gated after gated_ok(...) has been established by the caller.  Everything the
+    first launch reads is checked and prepared before it; the gate's operands (W_g, b_g, W_o, b_o,
+    residual) while the attention runs."""
+    M = X.shape[0]
     dt = X.dtype
-    cast = lambda t: _native.dense(t, dt)  # noqa: E731  (dense rows, 16-byte aligned)
-    wqkv_hm = cast(wqkv_hm)
-    Wc = _native.dense(W_combined, torch.float32)
-    sWc = _native.dense(sum_W_combined, torch.float32)
-    Bc = _native.dense(B_const, torch.float32)
+    code = io_dtype_code(dt)
+    f32 = torch.float32
+    _native.check_device(X, Z, wqkv_hm, Wc, sWc, Bc, mask)
+    X = _dense_as(X, dt)  # X, the weights, biases and residual are indexed without strides
+    Z = _native.vec16(Z)  # Z's strides are passed
+    wqkv_hm = _dense_as(wqkv_hm, dt)
+    Wc, sWc, Bc = _dense_as(Wc, f32), _dense_as(sWc, f32), _dense_as(Bc, f32)
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
     st = _native.stream_of(X)
-    nqkv = (3 * M * H * D * 2 + 255) // 256 * 256
-    nbytes = _native.apb_workspace_bytes(M, H, D)
+    nqkv = (3 * M * 4 * 32 * 2 + 255) // 256 * 256
+    nbytes = _native.apb_workspace_bytes(M, 4, 32)
     if nbytes > nqkv:
         # split keys: the pre-pass and attention are launched first (tops_apb_forward with Og = NULL
         # leaves the split partials after Q / K / V), the gate's arguments are prepared while they
         # run, then tops_apb_merge_gate; the same kernels as tops_apb_forward_gated
         work = torch.empty(nbytes, device=X.device, dtype=torch.uint8)
         _native.call("tops_apb_forward", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
-                     Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), _native.ptr(m8), None, work.data_ptr(), M, C,
-                     Z.shape[2], H, D, float(scale), float(eps), code, st)
-        W_g, b_g, W_o, b_o, res = (cast(t) for t in (W_g, b_g, W_o, b_o, residual))
+                     Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), None if m8 is None else m8.data_ptr(), None,
+                     work.data_ptr(), M, 128, 128, 4, 32, float(scale), float(eps), code, st)
+        _native.check_device(X, W_g, b_g, W_o, b_o, residual)
+        W_g, b_g, W_o, b_o, res = (_dense_as(W_g, dt), _dense_as(b_g, dt), _dense_as(W_o, dt), _dense_as(b_o, dt),
+                                   _dense_as(residual, dt))
         out = torch.empty(M, 128, device=X.device, dtype=dt)
         _native.call("tops_apb_merge_gate", work.data_ptr() + nqkv, X.data_ptr(), W_g.data_ptr(), _native.ptr(b_g),
-                     W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), M, H, D, code, st)
+                     W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), M, 4, 32, code, st)
         return out
-    W_g, b_g, W_o, b_o, res = (cast(t) for t in (W_g, b_g, W_o, b_o, residual))
+    _native.check_device(X, W_g, b_g, W_o, b_o, residual)
+    W_g, b_g, W_o, b_o, res = (_dense_as(W_g, dt), _dense_as(b_g, dt), _dense_as(W_o, dt), _dense_as(b_o, dt),
+                               _dense_as(residual, dt))
     out = torch.empty(M, 128, device=X.device, dtype=dt)
-    nbytes = _native.apb_gated_workspace_bytes(M, H, D)
+    nbytes = _native.apb_gated_workspace_bytes(M, 4, 32)
     work = torch.empty(max(nbytes, 1), device=X.device, dtype=torch.uint8) if nbytes else None
     _native.call("tops_apb_forward_gated", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
                  Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), _native.ptr(m8), W_g.data_ptr(), _native.ptr(b_g),
-                 W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), _native.ptr(work), M, C,
-                 Z.shape[2], H, D, 128, float(scale), float(eps), code, st)
+                 W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), _native.ptr(work), M, 128,
+                 128, 4, 32, 128, float(scale), float(eps), code, st)
     return out
 
 

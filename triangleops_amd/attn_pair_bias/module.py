@@ -25,7 +25,7 @@ import torch
 from .._common.layouts import interleave_qkv, qkv_head_major
 from .._common.ln_absorption import absorb_ln_matmul
 from ..triangle_attn.kernel import gate_out_forward
-from .kernel import apb_forward, apb_forward_gated, apb_forward_qkv, apb_qkn_prep, gated_ok
+from .kernel import apb_forward, apb_forward_qkv, apb_qkn_prep, gated_forward, gated_ok
 
 
 def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
@@ -47,13 +47,13 @@ def precompute(WQ, WK, WV, W_ln, B_ln, W_proj_z, B_proj_z, H, D):
 def forward(X, Z, pre, *, scale=1.0, eps=1e-5, W_proj_g, B_proj_g, W_proj_o, B_proj_o, mask=None, residual=None):
     """Per-call forward.  X (M, C_s), Z (M, M, C_z) -> (M, C_out); `residual` (M, C_out) returns
     residual + result, the add fused into the gate kernel's store (Pairformer single update)."""
+    wq, Wc = pre.get("wqkv_hm"), pre["W_combined"]
+    if wq is not None and wq.shape[2] == 32 and gated_ok(X, Z, Wc, W_proj_g, W_proj_o, residual):
+        return gated_forward(X, Z, Wc, pre["sum_W_combined"], pre["B_const"], wq, W_proj_g, B_proj_g, W_proj_o,
+                             B_proj_o, scale, eps, mask, residual)
     M = X.shape[0]
     H = pre["sum_W_combined"].shape[0]
     D = pre["W_QKV"].shape[1] // (3 * H)
-    if D == 32 and pre.get("wqkv_hm") is not None and gated_ok(X, Z, pre["W_combined"], W_proj_g, W_proj_o, residual):
-        return apb_forward_gated(X, Z, pre["W_combined"], pre["sum_W_combined"], pre["B_const"], pre["wqkv_hm"],
-                                 W_proj_g, B_proj_g, W_proj_o, B_proj_o, scale=scale, eps=eps, mask=mask,
-                                 residual=residual)
     Og = torch.empty(M, H * D, device=X.device, dtype=X.dtype)
     apb_forward(
         X,
