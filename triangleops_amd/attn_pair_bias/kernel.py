@@ -109,33 +109,48 @@ def gated_forward(X, Z, Wc, sWc, Bc, wqkv_hm, W_g, b_g, W_o, b_o, scale, eps, ma
     dt = X.dtype
     code = io_dtype_code(dt)
     f32 = torch.float32
-    _native.check_device(X, Z, wqkv_hm, Wc, sWc, Bc, mask)
-    X = _dense_as(X, dt)  # X, the weights, biases and residual are indexed without strides
-    Z = _native.vec16(Z)  # Z's strides are passed
+    nqkv = (3 * M * 4 * 32 * 2 + 255) // 256 * 256
+    nbytes = _native.apb_workspace_bytes(M, 4, 32)
+    if nbytes > nqkv:
+        # split keys: three launches, each issued once its own operands are checked, the next one's
+        # prepared while the previous runs: the Q / K / V pre-pass (tops_apb_qkn_prep without Q bias
+        # or norm runs tops_apb_forward's first kernel), the attention (tops_apb_forward_qkv with
+        # Og = NULL leaves the split partials after Q / K / V, where tops_apb_forward leaves them),
+        # then tops_apb_merge_gate; the same kernels and bits as tops_apb_forward_gated
+        _native.check_device(X, wqkv_hm)
+        X = _dense_as(X, dt)  # X, the weights, biases and residual are indexed without strides
+        wqkv_hm = _dense_as(wqkv_hm, dt)
+        st = _native.stream_of(X)
+        work = torch.empty(nbytes, device=X.device, dtype=torch.uint8)
+        w0 = work.data_ptr()
+        q, k, v = w0, w0 + M * 256, w0 + 2 * M * 256
+        _native.call("tops_apb_qkn_prep", X.data_ptr(), wqkv_hm.data_ptr(), None, 0, None, None, None, None, q, k, v,
+                     M, 128, 4, 32, float(scale), float(eps), code, st)
+        _native.check_device(X, Z, Wc, sWc, Bc, mask)
+        Z = _native.vec16(Z)  # Z's strides are passed
+        Wc, sWc, Bc = _dense_as(Wc, f32), _dense_as(sWc, f32), _dense_as(Bc, f32)
+        m8 = _native.mask_i8(mask)
+        if m8 is not None:
+            assert m8.numel() == M, "mask must be (M,)"
+        _native.call("tops_apb_forward_qkv", q, k, v, Z.data_ptr(), Z.stride(0), Z.stride(1), Wc.data_ptr(),
+                     sWc.data_ptr(), Bc.data_ptr(), None if m8 is None else m8.data_ptr(), None, w0 + nqkv, M, 128,
+                     128, 4, 32, 1.0, float(eps), code, st)
+        _native.check_device(X, W_g, b_g, W_o, b_o, residual)
+        W_g, b_g, W_o, b_o, res = (_dense_as(W_g, dt), _dense_as(b_g, dt), _dense_as(W_o, dt), _dense_as(b_o, dt),
+                                   _dense_as(residual, dt))
+        out = torch.empty(M, 128, device=X.device, dtype=dt)
+        _native.call("tops_apb_merge_gate", w0 + nqkv, X.data_ptr(), W_g.data_ptr(), _native.ptr(b_g),
+                     W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), M, 4, 32, code, st)
+        return out
+    _native.check_device(X, Z, wqkv_hm, Wc, sWc, Bc, mask, W_g, b_g, W_o, b_o, residual)
+    X = _dense_as(X, dt)
+    Z = _native.vec16(Z)
     wqkv_hm = _dense_as(wqkv_hm, dt)
     Wc, sWc, Bc = _dense_as(Wc, f32), _dense_as(sWc, f32), _dense_as(Bc, f32)
     m8 = _native.mask_i8(mask)
     if m8 is not None:
         assert m8.numel() == M, "mask must be (M,)"
     st = _native.stream_of(X)
-    nqkv = (3 * M * 4 * 32 * 2 + 255) // 256 * 256
-    nbytes = _native.apb_workspace_bytes(M, 4, 32)
-    if nbytes > nqkv:
-        # split keys: the pre-pass and attention are launched first (tops_apb_forward with Og = NULL
-        # leaves the split partials after Q / K / V), the gate's arguments are prepared while they
-        # run, then tops_apb_merge_gate; the same kernels as tops_apb_forward_gated
-        work = torch.empty(nbytes, device=X.device, dtype=torch.uint8)
-        _native.call("tops_apb_forward", X.data_ptr(), wqkv_hm.data_ptr(), Z.data_ptr(), Z.stride(0), Z.stride(1),
-                     Wc.data_ptr(), sWc.data_ptr(), Bc.data_ptr(), None if m8 is None else m8.data_ptr(), None,
-                     work.data_ptr(), M, 128, 128, 4, 32, float(scale), float(eps), code, st)
-        _native.check_device(X, W_g, b_g, W_o, b_o, residual)
-        W_g, b_g, W_o, b_o, res = (_dense_as(W_g, dt), _dense_as(b_g, dt), _dense_as(W_o, dt), _dense_as(b_o, dt),
-                                   _dense_as(residual, dt))
-        out = torch.empty(M, 128, device=X.device, dtype=dt)
-        _native.call("tops_apb_merge_gate", work.data_ptr() + nqkv, X.data_ptr(), W_g.data_ptr(), _native.ptr(b_g),
-                     W_o.data_ptr(), _native.ptr(b_o), _native.ptr(res), out.data_ptr(), M, 4, 32, code, st)
-        return out
-    _native.check_device(X, W_g, b_g, W_o, b_o, residual)
     W_g, b_g, W_o, b_o, res = (_dense_as(W_g, dt), _dense_as(b_g, dt), _dense_as(W_o, dt), _dense_as(b_o, dt),
                                _dense_as(residual, dt))
     out = torch.empty(M, 128, device=X.device, dtype=dt)
