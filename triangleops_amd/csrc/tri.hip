@@ -306,11 +306,13 @@ constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
 // A row whose keys are all masked: with Q and the bias identity zeroed, every score of the main
-// loop is C0 = 0, so each key k < N gets weight exp2(0) = 1 and each key >= N weight 0, in every
-// query column alike.  The PV products alone, over the same visited tiles in the main loop's order
-// with the same P operands, give the main loop's O bit for bit (and l = N exactly), without the
-// score MFMAs, exponentials, LDS staging and barriers.  Kept out of line so the main loop's
-// register allocation does not see it.
+// loop would be C0 = 0, so each key k < N weighs exactly 1 and each key >= N 0, in every query
+// column alike: O[q] = (sum over k < N of V[k]) / N, one vector for the whole row.  The waves of the
+// block split the visited blocks (wave w takes w, w + nw, ...; up to four blocks' loads in flight
+// per lane), each lane (d = lane % 32, key half lane / 32) adds its 32 positions of the block's V^T
+// row d in fp32, the halves and waves are added through LDS, and each wave writes its query tiles.
+// Every wave of the block calls this (one block barrier inside).  Kept out of line so the main
+// loop's register allocation does not see it.
 template <typename T, int QT>
 __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const short* vblk, int nv, int64_t N,
                                              T* __restrict__ out, int64_t i, int64_t so0, int64_t so1, int h,
@@ -318,28 +320,46 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
   constexpr int D = 32;
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
+  __shared__ __attribute__((aligned(16))) float usum[16][D];  // per wave (<= 16 waves), per d
+  const int nw = (int)(blockDim.x >> 6), wave = (int)(threadIdx.x >> 6);
   const int hl = lane >> 5, col = lane & 31;
-  f32x16 acc = {};
-  for (int j = 0; j < nv; ++j) {
-    const int kb = vblk[j];
-    const T* vt = kvrow + (int64_t)kb * kKVBlock + 64 * D + col * 64 + 8 * hl;  // V^T row col
+  float acc = 0.f;
+  for (int j0 = wave; j0 < nv; j0 += 4 * nw) {
+    V8 r[4][4];
+    int kbs[4];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int64_t nk = N - 64LL * kb - 32 * kt;  // keys < N in this 32-key tile (may be <= 0)
-      V8 pone[2];
+    for (int b = 0; b < 4; ++b) {
+      const int j = j0 + b * nw;
+      kbs[b] = j < nv ? (int)vblk[j] : -1;
+      const T* vt = kvrow + (int64_t)(kbs[b] < 0 ? 0 : kbs[b]) * kKVBlock + 64 * D + col * 64 + 8 * hl;
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj)
+      for (int c = 0; c < 4; ++c) r[b][c] = ldg<V8>(vt + 16 * c);  // positions 16 c + 8 hl + e
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (kbs[b] < 0) continue;  // wave-uniform
+      const int64_t nk = N - 64LL * kbs[b];  // keys < N in this block (>= 1: it was visited)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int v = 8 * jj + e;  // D slot v of the score tile: key 8 (v / 4) + 4 hl + v % 4
-          pone[jj][e] = (T)(8 * (v / 4) + 4 * hl + (v % 4) < nk ? 1.0f : 0.0f);
+          // V^T position 32 kt + 16 jj + 8 hl + e (c = 2 kt + jj) holds key 32 kt + 16 jj + 8 (e / 4) + 4 hl + e % 4
+          const int key = 16 * c + 8 * (e / 4) + 4 * hl + (e % 4);
+          acc += key < nk ? (float)r[b][c][e] : 0.f;
         }
-      acc = Mma<T>::m32(ldg<V8>(vt + 32 * kt), pone[0], acc);
-      acc = Mma<T>::m32(ldg<V8>(vt + 32 * kt + 16), pone[1], acc);
     }
   }
-  // O = acc / N for every query of the wave (l = N: N weights of exactly 1)
+  acc = halves_sum(acc);
+  if (hl == 0) usum[wave][col] = acc;
+  __syncthreads();
+  // O = sum / N for every query of the wave; lane (query col, half hl) stores d = 8 g + 4 hl + x
   const float inv = 1.0f / (float)N;
+  f32x4 m[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    m[g] = f32x4{};
+    for (int w = 0; w < nw; ++w) m[g] += *reinterpret_cast<const f32x4*>(&usum[w][8 * g + 4 * hl]);
+  }
 #pragma unroll
   for (int t = 0; t < QT; ++t) {
     const int64_t q = qbase + 32 * t + col;
@@ -348,8 +368,7 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         if (8 * g >= dv) break;
-        V4 w4 = {(T)(acc[4 * g] * inv), (T)(acc[4 * g + 1] * inv), (T)(acc[4 * g + 2] * inv),
-                 (T)(acc[4 * g + 3] * inv)};
+        V4 w4 = {(T)(m[g][0] * inv), (T)(m[g][1] * inv), (T)(m[g][2] * inv), (T)(m[g][3] * inv)};
         stg<V4>(dst + 8 * g, w4);
       }
     }
