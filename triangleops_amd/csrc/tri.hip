@@ -916,9 +916,9 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
            (unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, vj);
   };
 
-  // ---- rows without a valid key take the uniform average of V over the N keys (PV products
-  // ---- alone, tri_uniform_row): a pair of such rows skips the main loop; in a mixed pair the
-  // ---- main loop's result for the uniform row is replaced at the end ----
+  // ---- rows without a valid key take the uniform average of V over the N keys (tri_uniform_row):
+  // ---- a pair of such rows skips the main loop; in a mixed pair the main loop's result for the
+  // ---- uniform row is replaced at the end ----
   const int64_t kvoff[2] = {((int64_t)i0 * H + h) * nkb * kKVBlock, ((int64_t)i1 * H + h) * nkb * kKVBlock};
   if (uni[0] && uni[1]) {  // block-uniform
     tri_uniform_row<T, 1>(KV + kvoff[0], vblk, nv, N, out, i0, so0, so1, h, D, 32 * qt, lane);
