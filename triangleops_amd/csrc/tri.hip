@@ -815,9 +815,10 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
 // operand reads are free of bank conflicts without padding.  A ring of 4 LDS slots of 64-key
 // blocks, one barrier per block, copies issued three blocks ahead.  Stages are software-pipelined:
 // stage (row r, tile t) issues the PV MFMAs of the previous stage and the score MFMAs of the next
-// one (the other row) between its own exponentials.  A row without valid keys runs with Q and the
-// identity zeroed: every score is 0 and each key < N gets weight exactly 1, the uniform average of
-// V the reference's -1e9 add gives.  Masked keys get weight exactly 0.
+// one (the other row) between its own exponentials.  A row without valid keys (the uniform average
+// of V over the N keys, as the reference's -1e9 add gives) runs in the loop with Q and the identity
+// zeroed when its pair partner has valid keys, and its O is then written by tri_uniform_row.
+// Masked keys get weight exactly 0.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRing = 4;  // LDS slots of 64-key KV blocks (per block: 2 rows x 8 KB each)
 template <int V>
