@@ -370,13 +370,25 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     constexpr int SB = 16;
     using F2 = vec<float, 2>;
     float mx = -INFINITY;
-    for (int s0 = 0; s0 < nsplit; s0 += SB) {
-      F2 mb[SB];
+    F2 mb[SB];
+    f32x4 ob[SB][2];
+    auto batch = [&](int s0, bool with_o) {
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int s = s0 + i < nsplit ? s0 + i : s0;  // past the batch: split s0 again (unused)
         mb[i] = ldg<F2>(ml + s * sml);
+        if (with_o) {
+          ob[i][0] = ldg<f32x4>(op + s * so);
+          ob[i][1] = ldg<f32x4>(op + s * so + 4);
+        }
       }
+    };
+    // up to SB splits (every M from 2 * SB * 32 CUs' worth of query blocks on): one batch of loads
+    // serves the maximum and the sums; more splits take a first pass for the maximum
+    const bool one = nsplit <= SB;
+    if (one) batch(0, true);
+    for (int s0 = 0; s0 < nsplit; s0 += SB) {
+      if (!one) batch(s0, false);
 #pragma unroll
       for (int i = 0; i < SB; ++i)
         if (s0 + i < nsplit) mx = fmaxf(mx, mb[i][0]);
@@ -386,15 +398,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
 #pragma unroll
     for (int e = 0; e < 8; ++e) ot[e] = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += SB) {
-      F2 mb[SB];
-      f32x4 ob[SB][2];
-#pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const int s = s0 + i < nsplit ? s0 + i : s0;
-        mb[i] = ldg<F2>(ml + s * sml);
-        ob[i][0] = ldg<f32x4>(op + s * so);
-        ob[i][1] = ldg<f32x4>(op + s * so + 4);
-      }
+      if (!one) batch(s0, true);
 #pragma unroll
       for (int i = 0; i < SB; ++i)
         if (s0 + i < nsplit) {
