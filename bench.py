@@ -920,7 +920,8 @@ TRAFFIC_PROFILES = [os.path.join(os.path.dirname(os.path.abspath(__file__)), "pr
 
 def measured_traffic(kernel, n):
     """HBM bytes per launch of `kernel` at size 1024, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summaries (calibrated against a copy of known size); None otherwise."""
+    WRITE_SIZE summaries (2 x FETCH_SIZE + WRITE_SIZE, checked on kernels whose bytes are fixed);
+    None otherwise."""
     if n != 1024:
         return None
     for path in TRAFFIC_PROFILES:
@@ -971,8 +972,10 @@ def _op_call(op, n, dev):
 
 def traffic_run(n, op="tmu2"):
     """Workload of the HBM-traffic counter runs (no timing): a 256 MiB bf16 negation whose bytes are
-    known (calibration), then two calls of `op` at size n (default: two tmu steps, outgoing +
-    incoming; `tri` / `apb`: two calls of triangle attention / attention_pair_bias)."""
+    known (a reference point: FETCH_SIZE counts 64 bytes per 128-byte read request, so its reading
+    depends on the access width torch picks for it), then two calls of `op` at size n (default: two
+    tmu steps, outgoing + incoming; `tri` / `apb`: two calls of triangle attention /
+    attention_pair_bias)."""
     dev = torch.device("cuda:0")
     src = torch.randn(128 * 1024 * 1024, device=dev).to(torch.bfloat16)
     dst = torch.empty_like(src)

@@ -308,8 +308,8 @@ constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kS
 // A row whose keys are all masked: with Q and the bias identity zeroed, every score of the main
 // loop would be C0 = 0, so each key k < N weighs exactly 1 and each key >= N 0, in every query
 // column alike: O[q] = (sum over k < N of V[k]) / N, one vector for the whole row.  The waves of the
-// block split the visited blocks (wave w takes w, w + nw, ...; up to four blocks' loads in flight
-// per lane), each lane (d = lane % 32, key half lane / 32) adds its 32 positions of the block's V^T
+// block split the visited blocks (wave w takes w, w + nw, ...; two blocks' loads in flight per
+// lane), each lane (d = lane % 32, key half lane / 32) adds its 32 positions of the block's V^T
 // row d in fp32, the halves and waves are added through LDS, and each wave writes its query tiles.
 // Every wave of the block calls this (one block barrier inside).  Kept out of line so the main
 // loop's register allocation does not see it.
@@ -323,12 +323,13 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
   __shared__ __attribute__((aligned(16))) float usum[16][D];  // per wave (<= 16 waves), per d
   const int nw = (int)(blockDim.x >> 6), wave = (int)(threadIdx.x >> 6);
   const int hl = lane >> 5, col = lane & 31;
+  constexpr int NB = 2;  // blocks whose loads are in flight together per lane
   float acc = 0.f;
-  for (int j0 = wave; j0 < nv; j0 += 4 * nw) {
-    V8 r[4][4];
-    int kbs[4];
+  for (int j0 = wave; j0 < nv; j0 += NB * nw) {
+    V8 r[NB][4];
+    int kbs[NB];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const int j = j0 + b * nw;
       kbs[b] = j < nv ? (int)vblk[j] : -1;
       const T* vt = kvrow + (int64_t)(kbs[b] < 0 ? 0 : kbs[b]) * kKVBlock + 64 * D + col * 64 + 8 * hl;
@@ -336,7 +337,7 @@ __device__ __noinline__ void tri_uniform_row(const T* __restrict__ kvrow, const 
       for (int c = 0; c < 4; ++c) r[b][c] = ldg<V8>(vt + 16 * c);  // positions 16 c + 8 hl + e
     }
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < NB; ++b) {
       if (kbs[b] < 0) continue;  // wave-uniform
       const int64_t nk = N - 64LL * kbs[b];  // keys < N in this block (>= 1: it was visited)
 #pragma unroll
