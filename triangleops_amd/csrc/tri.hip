@@ -501,6 +501,19 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
   const T* kvrow = KV + ((int64_t)i * H + h) * nkb * kKVBlock;
   const int64_t nqt = (N + 31) / 32;
 
+  // ---- the mask bytes of the wave's first kMaskU key blocks (wave + u NW), loaded first: vector
+  // ---- loads complete in issue order, so their wait does not include the Q, bias and KV loads
+  // ---- issued after them (a loop with one load per block waited for all of those each time) ----
+  constexpr int kMaskU = 8;
+  int mval[kMaskU];
+#pragma unroll
+  for (int u = 0; u < kMaskU; ++u) {
+    const int64_t k = (int64_t)(wave + u * NW) * 64 + lane;
+    mval[u] = 0;
+    if (wave + u * NW < nkb && k < N) mval[u] = mask ? (int)mask[i * sm0 + k * sm1] : 1;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) and bias pointers, loaded
   // ---- before the key-validity pass so the loads overlap it (a row without valid keys zeroes
   // ---- Q and the identity below, so its scores are all C0) ----
@@ -548,7 +561,13 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
   load_bias(0, 1, bB);
 
   // ---- key validity per 64-key block ----
-  for (int kb = wave; kb < nkb; kb += NW) {
+#pragma unroll
+  for (int u = 0; u < kMaskU; ++u) {
+    const int kb = wave + u * NW;
+    const unsigned long long bits = __ballot(mval[u] != 0);
+    if (kb < nkb && lane == 0) kvalid[kb] = bits;
+  }
+  for (int kb = wave + kMaskU * NW; kb < nkb; kb += NW) {  // N > 64 kMaskU NW
     const int64_t k = (int64_t)kb * 64 + lane;
     bool ok = k < N;
     if (ok && mask) ok = mask[i * sm0 + k * sm1] != 0;
