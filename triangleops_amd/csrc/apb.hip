@@ -111,15 +111,16 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
 
   const int64_t kbeg = (int64_t)sp * keys_per_split;
   const int64_t kend = kbeg + keys_per_split < M ? kbeg + keys_per_split : M;
+  // key validity of a 32-key block (same in every wave); the next block's mask bytes are loaded
+  // at the start of this one, so no block waits for its own
+  auto mload = [&](int64_t kb0) {
+    const int64_t k = kb0 + (lane & 31);
+    return k < kend && lane < 32 ? (mask ? (int)mask[k] : 1) : 0;
+  };
+  int mcur = mload(kbeg);
   for (int64_t k0 = kbeg; k0 < kend; k0 += 32) {
-    // key validity of this 32-key block (same in every wave)
-    unsigned int kbits;
-    {
-      const int64_t k = k0 + (lane & 31);
-      bool ok = k < kend;
-      if (ok && mask) ok = mask[k] != 0;
-      kbits = (unsigned int)__ballot(ok && lane < 32);
-    }
+    const unsigned int kbits = (unsigned int)__ballot(mcur != 0);
+    mcur = mload(k0 + 32);
     if (kbits == 0) continue;  // block-uniform
 
     // ---- pair bias for the 32 x 32 (query, key) tile: wave w -> queries 8w .. 8w+7 ----
