@@ -72,6 +72,24 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
   // the identity in operand layout (lane: row col, channels 16 s + 8 hl + e), so A . eye^T and
   // eye . B^T reproduce the rows exactly in the MFMA output layout
   const int s0 = 2 * h;
+  const int64_t q0 = (int64_t)qb * 32;
+  const int64_t kbeg = (int64_t)sp * keys_per_split;
+  const int64_t kend = kbeg + keys_per_split < M ? kbeg + keys_per_split : M;
+  // Z slice of pair-bias step u of the 32-key block at kb0: query 8 w + u / 2, keys 16 (u % 2) .. +15
+  auto zload = [&](int64_t kb0, int u, V8* za) {
+    const int lq = 8 * wave + (u >> 1), kh = u & 1;
+    int64_t q = q0 + lq;
+    q = q < M ? q : M - 1;
+    int64_t key = kb0 + 16 * kh + l16;
+    key = key < M ? key : M - 1;
+    const T* zr = Z + q * sz0 + key * sz1 + 8 * g16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) za[s] = ldg<V8>(zr + 32 * s);
+  };
+  // the first block's first Z slice is loaded before everything else (the kernel runs as about
+  // one round of blocks, so each block's first HBM round trip is on the critical path)
+  V8 za[4], zb[4];
+  zload(kbeg, 0, za);
   V8 eye[2];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
@@ -79,7 +97,6 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
     for (int e = 0; e < 8; ++e) eye[s][e] = (T)(16 * s + 8 * hl + e == col ? 1.0f : 0.0f);
 
   // ---- Q^T for the block's 32 queries, head h (B operand of S^T = K . Q^T) ----
-  const int64_t q0 = (int64_t)qb * 32;
   V8 qop[2];
   {
     int64_t q = q0 + col;
@@ -109,8 +126,6 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
   f32x16 o = {};
   float m = -INFINITY, l = 0.f;
 
-  const int64_t kbeg = (int64_t)sp * keys_per_split;
-  const int64_t kend = kbeg + keys_per_split < M ? kbeg + keys_per_split : M;
   // key validity of a 32-key block (same in every wave); the next block's mask bytes are loaded
   // at the start of this one, so no block waits for its own
   auto mload = [&](int64_t kb0) {
@@ -126,16 +141,6 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
     // ---- pair bias for the 32 x 32 (query, key) tile: wave w -> queries 8w .. 8w+7 ----
     // step u covers query 8w + u / 2 and keys 16 (u % 2) .. +15; the Z slice of step u + 1 is
     // loaded while step u is reduced (two register sets, so a load is always in flight)
-    auto zload = [&](int u, V8* za) {
-      const int lq = 8 * wave + (u >> 1), kh = u & 1;
-      int64_t q = q0 + lq;
-      q = q < M ? q : M - 1;
-      int64_t key = k0 + 16 * kh + l16;
-      key = key < M ? key : M - 1;
-      const T* zr = Z + q * sz0 + key * sz1 + 8 * g16;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) za[s] = ldg<V8>(zr + 32 * s);
-    };
     auto zbias = [&](int u, const V8* za) {
       const int lq = 8 * wave + (u >> 1), kh = u & 1;
       // LayerNorm statistics in one pass, sum and sum of squares with clamped variance, as the
@@ -172,13 +177,12 @@ __global__ __launch_bounds__(256, 2) void apb_attn_kernel(const T* __restrict__ 
       }
     };
     {
-      V8 za[4], zb[4];
-      zload(0, za);
+      if (k0 != kbeg) zload(k0, 0, za);  // (the first block's was loaded at the start)
 #pragma unroll 1
       for (int u = 0; u < 16; u += 2) {
-        zload(u + 1, zb);
+        zload(k0, u + 1, zb);
         zbias(u, za);
-        if (u + 2 < 16) zload(u + 2, za);
+        if (u + 2 < 16) zload(k0, u + 2, za);
         zbias(u + 1, zb);
       }
     }
