@@ -135,17 +135,23 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
       V8 x[4];
       int mb[4];  // raw mask bytes, converted when the stage is consumed
     };
+    // token of position c0 + d of a tile: tok0 + d * sc (sc = L when incoming, 1 when outgoing);
+    // the tile's base is wave-uniform, the lane parts are 32-bit offsets from 24-bit products
+    // (d < 64, L * 2C < 2^24: the launcher admits L < 2^15) (no mask: the dummy byte read is x's
+    // first)
+    const uint32_t sc = transpose ? (uint32_t)L : 1u, msc = mask ? sc : 0u, xsc = sc * (uint32_t)(C * sizeof(T));
     auto fetch = [&](uint32_t tt, Stage& sg) {
       tt = tt < ntiles ? tt : ntiles - 1;
       const GridTile g = grid_tile_fast(tt, tpr, Ld);
+      const int64_t tok0 = transpose ? (g.b * L + g.c0) * L + g.r : (g.b * L + g.r) * L + g.c0;
+      const char* xb = reinterpret_cast<const char*>(x + tok0 * C);
+      const int8_t* mbase = mask ? mask + tok0 : reinterpret_cast<const int8_t*>(x);
+      const int lim = (int)(L - 1 - g.c0);  // positions >= L reload position L - 1
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        int64_t c = g.c0 + 16 * k + tq;
-        c = c < L ? c : L - 1;
-        const int64_t i = transpose ? c : g.r, j = transpose ? g.r : c;
-        const int64_t tok = (g.b * L + i) * L + j;
-        sg.x[k] = ldg<V8>(x + tok * C + 8 * ch);
-        sg.mb[k] = *(mask ? mask + tok : reinterpret_cast<const int8_t*>(x));
+        const uint32_t d = (uint32_t)min(16 * k + tq, lim);
+        sg.x[k] = ldg<V8>(xb + (__umul24(d, xsc) + 16u * ch));
+        sg.mb[k] = mbase[__umul24(d, msc)];
       }
     };
     auto step = [&](uint32_t tt, int bb, Stage& sg) {
@@ -914,12 +920,15 @@ __global__ __launch_bounds__(256, 2) void tmu_einsum_f32_kernel(const float* __r
 // Output phase (C = C_out = 128).  64-token tiles, 12 waves in two roles:
 //   waves 0-3 (loaders) fetch y and x three tiles ahead and stage them in LDS (double-buffered):
 //   y (channel-major in HBM) is read 8 lanes per 128-byte channel row and transposed in
-//   registers (4 channels x 8 tokens per thread) into a token-major tile; x (token-major) is
-//   normalised on the way in (16 lanes per token, `ln_stats16`: one pass for bf16, two for fp16);
+//   registers (4 channels x 8 tokens per thread) into a token-major tile, and each loader wave
+//   sums y and y^2 of every token over its 32 channels (fp32, reduced across the 8 lanes of a
+//   token group with lane swaps); x (token-major) is normalised on the way in (16 lanes per
+//   token, `ln_stats16`: one pass for bf16, two for fp16);
 //   waves 4-11 (writers) compute features [32 (w & 3), +32) for the 32 tokens [32 (w >> 2), +32)
 //   (w = wave - 4) with their Wp / Wg rows in registers (rows permuted so each lane ends up with
-//   16 consecutive features of one token), take the LN statistics of y from LDS and apply them
-//   in the epilogue, and write a token-major output tile (double-buffered); tile n is stored,
+//   16 consecutive features of one token), add the loaders' four partial sums of y into its LN
+//   statistics and apply them in the epilogue (once per token instead of once per writer wave),
+//   and write a token-major output tile (double-buffered); tile n is stored,
 //   whole 256-byte rows per 16 lanes, after the barrier of tile n + 1, when every writer has
 //   finished it.  One barrier per tile.
 // ---------------------------------------------------------------------------------------------
@@ -937,15 +946,15 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
   constexpr int ROW = C * 2;  // LDS bytes per token row (16 chunks of 16 bytes)
   constexpr int KS = C / 16;
   constexpr int NL = 256;  // loader threads (waves 0-3); the writers are the other 512
-  constexpr int PD = 3;    // loader register stages in flight
   using V8 = vec<T, 8>;
   using V4 = vec<T, 4>;
-  using V2 = vec<T, 2>;
 
   __shared__ __attribute__((aligned(16))) char ys[2][64 * ROW];  // raw y, token-major
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x
   __shared__ __attribute__((aligned(16))) T os[2][64 * COUT];    // gated output, token-major
   __shared__ __attribute__((aligned(16))) float cst[3][COUT];    // sum(Wp_c), Bp, -log2(e) Bg
+  // LN statistics of y per token and loader wave: (sum, sum of squares) over the wave's 32 channels
+  __shared__ __attribute__((aligned(16))) float2 ystat[2][64][4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < COUT; i += 768) {
@@ -969,21 +978,26 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
     struct Stage {
       V8 y[4], x[4];
     };
-    // same loads on every call (past the end: the last tile; tokens >= L read token L - 1)
+    // same loads on every call (past the end: the last tile; tokens >= L read token L - 1).  Lane
+    // parts of the addresses are loop-invariant (y: one 64-bit pointer per channel row; x: token
+    // (16 k + tid / 16) of the tile, chunk tid % 16, as 32-bit offsets from the tile's first token)
+    const T* yl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) yl[r] = y + (int64_t)(4 * cq + r) * cstride + 8 * tg;
     auto fetch = [&](uint32_t tt, Stage& sg) {
       tt = tt < ntiles ? tt : ntiles - 1;
       const GridTile g = grid_tile_fast(tt, tpr, Ld);
       const int64_t rowbase = g.b * L + g.r;
-      const T* ysrc = y + rowbase * ldy + g.c0 + 8 * tg;
+      const int64_t yoff = rowbase * ldy + g.c0;
 #pragma unroll
       for (int r = 0; r < 4; ++r)  // y is read once: non-temporal, so it does not displace x in the caches
-        sg.y[r] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(ysrc + (int64_t)(4 * cq + r) * cstride));
+        sg.y[r] = __builtin_nontemporal_load(reinterpret_cast<const V8*>(yl[r] + yoff));
+      const char* xb = reinterpret_cast<const char*>(x + (rowbase * L + g.c0) * C);
+      const int lim = (int)(L - 1 - g.c0);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int ci = k * NL + tid;  // token ci / 16, chunk ci % 16
-        int64_t j = g.c0 + (ci >> 4);
-        j = j < L ? j : L - 1;
-        sg.x[k] = ldg<V8>(x + (rowbase * L + j) * C + 8 * (ci & 15));
+        const uint32_t d = (uint32_t)min(16 * k + (tid >> 4), lim);
+        sg.x[k] = ldg<V8>(xb + (d * (uint32_t)(C * sizeof(T)) + 16u * (tid & 15)));
       }
     };
     auto step = [&](int bb, Stage& sg, uint32_t tnext) {
@@ -998,12 +1012,40 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
         for (int e = 0; e < 8; ++e) h[e] = (T)fmaf((float)sg.x[k][e], rstd, nb);
         *reinterpret_cast<V8*>(&xs[bb][xt * ROW + ((ch ^ (xt & 15)) << 4)]) = h;
       }
+      float st16[16];  // (sum, sum of squares) of this lane's 4 channels of token 8 tg + e at 2 e, 2 e + 1
 #pragma unroll
       for (int e = 0; e < 8; ++e) {  // y: 4 x 8 register transpose -> token-major rows
         const int tk = 8 * tg + e;
         const V4 q4 = {sg.y[0][e], sg.y[1][e], sg.y[2][e], sg.y[3][e]};
         *reinterpret_cast<V4*>(&ys[bb][tk * ROW + (((cq >> 1) ^ yswz(tk)) << 4) + ((cq & 1) << 3)]) = q4;
+        float a[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = (float)q4[r];
+        st16[2 * e] = (a[0] + a[1]) + (a[2] + a[3]);
+        st16[2 * e + 1] = fmaf(a[0], a[0], fmaf(a[1], a[1], fmaf(a[2], a[2], a[3] * a[3])));
       }
+      // sum over the 8 lanes that hold token group tg (lane bits 3-5, this wave's 32 channels):
+      // each swap-and-add step halves what a lane keeps, so lane bits (5, 4, 3) end with token
+      // 4 b5 + 2 b4 + b3 of the group (v_permlane32 / 16_swap exchange the upper half / odd rows of
+      // the first operand with the lower half / even rows of the second; DPP row_ror:8 reads l ^ 8)
+      float st8[8], st4[4], st2[2];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(st16[i]), __float_as_uint(st16[i + 8]), false, false);
+        st8[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(st8[i]), __float_as_uint(st8[i + 4]), false, false);
+        st4[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+      const bool b3 = (lane >> 3) & 1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float keep = b3 ? st4[i + 2] : st4[i], send = b3 ? st4[i] : st4[i + 2];
+        st2[i] = keep + dpp<0x128>(send);
+      }
+      ystat[bb][8 * tg + ((lane >> 3) & 7)][wave] = make_float2(st2[0], st2[1]);
       __syncthreads();  // tile staged
       fetch(tnext, sg);  // refill this stage
       __builtin_amdgcn_sched_barrier(0);
@@ -1101,23 +1143,11 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
         __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      // LN statistics of y for this token: this lane sums chunks [8 hl, 8 hl + 8), its partner the rest
-      float s1 = 0.f, s2 = 0.f;
-      {
-        const V2 one = {(T)1.f, (T)1.f};
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const V8 v = *reinterpret_cast<const V8*>(yrow + (((8 * hl + c) ^ yswz(tok)) << 4));
-#pragma unroll
-          for (int k = 0; k < 8; k += 2) {
-            const V2 pr = {v[k], v[k + 1]};
-            s1 = Mma<T>::dot2(pr, one, s1);
-            s2 = Mma<T>::dot2(pr, pr, s2);
-          }
-        }
-      }
-      const float mean = halves_sum(s1) * (1.0f / C);
-      const float var = fmaxf(halves_sum(s2) * (1.0f / C) - mean * mean, 0.f);
+      // LN statistics of y for this token: the loader waves' partial sums over 32 channels each
+      const float4 p01 = *reinterpret_cast<const float4*>(&ystat[bb][tok][0]);
+      const float4 p23 = *reinterpret_cast<const float4*>(&ystat[bb][tok][2]);
+      const float mean = ((p01.x + p01.z) + (p23.x + p23.z)) * (1.0f / C);
+      const float var = fmaxf(((p01.y + p01.w) + (p23.y + p23.w)) * (1.0f / C) - mean * mean, 0.f);
       const float ra = rsqrtf(var + eps), rb = -mean * ra;
       V8 o[2];
 #pragma unroll
@@ -1226,7 +1256,8 @@ extern "C" int tops_tmu_input_phase(const void* x, const void* mask, const void*
                "tops_tmu_input_phase: bad sizes B=%lld L=%lld ld=%lld (ld must be a multiple of 64)", (long long)B,
                (long long)L, (long long)ld);
   TOPS_REQUIRE(B * L * (ld / 64) < (1LL << 31), "tops_tmu_input_phase: too many tokens");
-  if (C != 128 || (C_out != 128 && C_out != 256) || dtype == TOPS_DTYPE_F32)  // any-shape kernels
+  // any-shape kernels (and L >= 2^15, where the tuned kernel's 24-bit lane offsets would not hold)
+  if (C != 128 || (C_out != 128 && C_out != 256) || dtype == TOPS_DTYPE_F32 || L >= (1 << 15))
     return tmu_generic_input_phase(x, mask, Wp, Wg, Bp, Bg, ab, B, L, C, C_out, ld, transpose, eps, dtype,
                                    (hipStream_t)stream);
   (void)sWp;  // the kernel normalises x before the GEMM: the column sums of the folded weights
