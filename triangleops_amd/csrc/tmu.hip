@@ -41,7 +41,8 @@ __device__ inline GridTile grid_tile(int64_t t, int64_t L, int tiles_per_row) {
 // LayerNorm statistics of a C-element token held as 8 elements by each of 16 consecutive lanes.
 // bf16: one pass of packed dot products (sum and sum of squares, fp32 products and sums; 8 instead
 // of 16 converts + 24 fp32 ops per lane), variance clamped at 0.  The output phase's loaders use it
-// (measured 2 % faster there); the input phase keeps two passes, which measured faster there.  For
+// (measured 2 % faster there, and faster than fp32 sums); the input phase, which converts x to fp32
+// anyway, takes the same one-pass statistics from fp32 sums (faster there than both).  For
 // bf16 (8 significant bits) the fp32 cancellation in E[x^2] - mean^2 has relative error about
 // (mean / std)^2 * 2^-22 in the variance, at most 2^-6 where a token's mean exceeds its deviation by
 // 2^8, the ratio at which bf16 already quantises the deviation to about one step.  fp16 resolves
@@ -90,13 +91,15 @@ __device__ inline GridTile grid_tile_fast(uint32_t t, const FastDiv& tpr, const 
 // store grid), 8 waves in two roles:
 //   waves 0-3 (loaders) fetch x four tiles ahead (16 lanes per 256-byte token row; positions
 //   c >= L reload position L - 1 and get mask 0, so every fetch issues the same loads), take
-//   each token's LayerNorm statistics (two-pass, fp32) and stage the normalised tile and the
-//   mask in LDS (double-buffered);
+//   each token's LayerNorm statistics (fp32; one pass of sum and sum of squares for bf16, two
+//   passes for fp16, as in ln_stats16) and stage the normalised tile and the mask in LDS
+//   (double-buffered);
 //   waves 4 .. 4 + NWR - 1 (writers, NWR = C_out / 32) each own 32 output features: P and G weight rows in
 //   registers as the MFMA B operand, D = x . W^T with the A operand read in a permuted token
-//   order so each lane ends up with 16 consecutive tokens of one feature, the bias add, gate
-//   and mask in the epilogue, and a private feature-major LDS tile that the same wave stores
-//   with whole 128-byte rows (8 features x 64 tokens per store instruction).
+//   order so each lane ends up with 16 consecutive tokens of one feature (P's bias added by one
+//   more MFMA k-step), the gate and mask in the epilogue, and a private feature-major LDS tile
+//   that the same wave stores with whole 128-byte rows (8 features x 64 tokens per store
+//   instruction).
 // No wave has loads and stores in flight together; one barrier per tile, and the loaders'
 // LayerNorm of tile n + 1 overlaps the writers' GEMM of tile n.  The LN affine is folded into
 // the weights, so the GEMM of the normalised x gives LN(x) . W^T directly.  The loaders also
@@ -163,17 +166,32 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (float)sg.x[k][e];
-        float s = 0.f;
+        float mean, rstd;
+        if constexpr (std::is_same<T, _Float16>::value) {  // two passes (see ln_stats16)
+          float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s += v[e];
-        const float mean = group_sum<16>(s) * (1.0f / C);
-        float q = 0.f;
+          for (int e = 0; e < 8; ++e) s += v[e];
+          mean = group_sum<16>(s) * (1.0f / C);
+          float q = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
-        const float rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+          for (int e = 0; e < 8; ++e) q = fmaf(v[e] - mean, v[e] - mean, q);
+          rstd = rsqrtf(group_sum<16>(q) * (1.0f / C) + eps);
+        } else {  // one pass of fp32 sums (two independent lane reductions)
+          float s = 0.f, q = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            s += v[e];
+            q = fmaf(v[e], v[e], q);
+          }
+          s = group_sum<16>(s);
+          q = group_sum<16>(q);
+          mean = s * (1.0f / C);
+          rstd = rsqrtf(fmaxf(q * (1.0f / C) - mean * mean, 0.f) + eps);
+        }
+        const float nb = -mean * rstd;
         V8 o;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (T)((v[e] - mean) * rstd);
+        for (int e = 0; e < 8; ++e) o[e] = (T)fmaf(v[e], rstd, nb);
         *reinterpret_cast<V8*>(&xs[bb][tk * ROW + ((ch ^ key(tk)) << 4)]) = o;
         // every lane of the token stores the same value: no divergent branch in the loop
         const float mv = g.c0 + tk < L ? (mask ? (float)(sg.mb[k] != 0) : 1.f) : 0.f;
@@ -220,7 +238,19 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
       wp[s] = ldg<V8>(Wp + (int64_t)f * C + 16 * s + 8 * hl);
       wg[s] = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
     }
-    const float cbp = Bp[f], cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
+    const float cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
+    // P's bias enters through one more MFMA k-step: A = 1 at k = 0, 1 for every token, B = the
+    // feature's fp32 bias as two 16-bit parts (hi + lo equal to it within ~2^-16 relative)
+    V8 one_a, bias_b;
+    {
+      const float cbp = Bp[f];
+      const T bhi = (T)cbp, blo = (T)(cbp - (float)bhi);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        one_a[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
+        bias_b[e] = hl == 0 && e == 0 ? bhi : (hl == 0 && e == 1 ? blo : (T)0.f);
+      }
+    }
     // token of MFMA row r: 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3), so D slot v of lane
     // half hl is token 16 hl + v of the 32-token sub-tile
     const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
@@ -246,7 +276,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[0][e] = o[1][e] = (T)0.0f;
           } else {
-            f32x16 accP = {}, accG = {};
+            f32x16 accP = Mma<T>::m32(one_a, bias_b, f32x16{}), accG = {};
 #pragma unroll
             for (int k = 0; k < KS; ++k) {
               const V8 xa = *reinterpret_cast<const V8*>(&xs[bb][tok * ROW + (((2 * k + hl) ^ key(tok)) << 4)]);
@@ -257,7 +287,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 #pragma unroll
               for (int v = 0; v < 16; ++v) {
                 const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
-                o[v / 8][v % 8] = (T)((accP[v] + cbp) * gate);
+                o[v / 8][v % 8] = (T)(accP[v] * gate);
               }
             } else {
 #pragma unroll
@@ -267,7 +297,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
                 for (int j = 0; j < 4; ++j) {
                   const int v = 4 * gq + j;
                   const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
-                  o[v / 8][v % 8] = (T)((accP[v] + cbp) * gate * rm[j]);
+                  o[v / 8][v % 8] = (T)(accP[v] * gate * rm[j]);
                 }
               }
             }
