@@ -268,6 +268,12 @@ def torch_pair_stack(z, m, w_out, w_in, ts, te, eps=1e-5):
 # --------------------------------------------------------------------------- #
 # timing helpers
 # --------------------------------------------------------------------------- #
+# per-call timing of the reference's benchmark harness (benchmarks/harness.py:18-40: 12 warmup
+# calls, then 30 calls each bracketed by events and a synchronize, the median); the op entries use
+# it where a call is short enough, so clocks have settled as they have in the reference's runs
+REF_ITERS, REF_WARMUP = 30, 12
+
+
 def time_ms(fn, iters, warmup):
     """Median per-call ms via HIP events on the current stream; NaN on OOM."""
     try:
@@ -599,7 +605,7 @@ def op_entry_tri(N, dev, iters, warmup, cpu):
          "roofline": {"kernel": "tri_attention", "bound": "mfma", "achieved": ka["achieved"], "peak": ka["peak"],
                       "unit": ka["unit"], "frac": ka["frac"], "traffic": measured_traffic("tri_attention", N)},
          "kernels": kern}
-    e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), 3, 1), 4)
+    e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), REF_ITERS, REF_WARMUP), 4)
     del d, pre
     torch.cuda.empty_cache()
     e["cpu_baseline"] = cpu_baseline_tri(d_c, N) if cpu else None
@@ -625,7 +631,7 @@ def op_entry_apb(M, dev, iters, warmup, cpu):
          "roofline": {"kernel": "apb_attention (apb_attn_kernel)", "bound": "hbm", "achieved": ka["achieved"], "peak": ka["peak"],
                       "unit": ka["unit"], "frac": ka["frac"], "traffic": measured_traffic("apb_attention", M)},
          "kernels": kern}
-    e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)
+    e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), REF_ITERS, REF_WARMUP), 4)
     del d, pre
     torch.cuda.empty_cache()
     e["cpu_baseline"] = cpu_baseline_apb(d_c, M) if cpu else None
@@ -655,7 +661,7 @@ def size_sweep_entries(dev):
         x, m, w = tmu_inputs(L)
         x, m, w = x.to(dev), m.to(dev), {k: v.to(dev) for k, v in w.items()}
         pre = tops.triangle_mul.precompute(*[w[k] for k in TMU_KEYS])
-        it, wu = (20, 5) if L <= 1024 else (8, 3)
+        it, wu = (REF_ITERS, REF_WARMUP) if L <= 1024 else (10, 4)
         e = {"op": "triangle_multiplicative_update", "size": L}
         for direction in ("outgoing", "incoming"):
             e[f"ms_per_call_{direction}"] = round(time_ms(
@@ -663,7 +669,7 @@ def size_sweep_entries(dev):
         work = tmu_work(L)
         ph = run_phases([tmu_phases(x, m, pre, "outgoing"), tmu_phases(x, m, pre, "incoming")], list(work), it, wu)
         e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
-        e["torch_path_ms"] = round(time_ms(lambda: torch_tmu(x, "outgoing", m, **w), 5 if L <= 1024 else 3, 1), 4)
+        e["torch_path_ms"] = round(time_ms(lambda: torch_tmu(x, "outgoing", m, **w), it, wu), 4)
         if L <= 512:
             e["ms_graph"] = round(graph_ms(lambda xx: tops.triangle_mul.forward(xx, pre, direction="outgoing",
                                                                                 mask=m), x), 4)
@@ -676,7 +682,7 @@ def size_sweep_entries(dev):
         pre = tops.triangle_attn.precompute(d["W_ln"], d["B_ln"], d["WQ"], d["WK"], d["WV"], d["W_proj_z"],
                                             d["B_proj_z"], H, D)
         kw = dict(scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=None, W_proj_o=d["W_proj_o"], B_proj_o=None)
-        it, wu = (20, 5) if N <= 1024 else (6, 2)
+        it, wu = REF_ITERS, REF_WARMUP
         e = {"op": "triangle_attention", "size": N,
              "ms_per_call": round(time_ms(lambda: tops.triangle_attn.forward(d["X"], pre, mask=d["mask"], **kw), it,
                                           wu), 4),
@@ -685,9 +691,9 @@ def size_sweep_entries(dev):
         work = tri_work(N)
         ph = run_phases([tri_phases(d, pre)], list(work), it, wu)
         e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
-        # N = 2048: the (N, H, N, N) bf16 scores are 64 GiB per intermediate; timed once after one
-        # warmup call (out of memory is reported as NaN, not skipped)
-        e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), 3 if N <= 1024 else 1, 1), 4)
+        # N = 2048: the (N, H, N, N) bf16 scores are 64 GiB per intermediate; timed 5 times after two
+        # warmup calls (out of memory is reported as NaN, not skipped)
+        e["torch_path_ms"] = round(time_ms(lambda: torch_tri(d), *((it, wu) if N <= 1024 else (5, 2))), 4)
         torch.cuda.empty_cache()
         if N <= 512:
             e["ms_graph"] = round(graph_ms(lambda X: tops.triangle_attn.forward(X, pre, mask=d["mask"], **kw),
@@ -703,11 +709,12 @@ def size_sweep_entries(dev):
         kw = dict(scale=D**-0.5, W_proj_g=d["W_proj_g"], B_proj_g=d["B_proj_g"], W_proj_o=d["W_proj_o"],
                   B_proj_o=d["B_proj_o"], mask=d["mask"])
         e = {"op": "attention_pair_bias", "size": M,
-             "ms_per_call": round(time_ms(lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, **kw), 20, 5), 4)}
+             "ms_per_call": round(time_ms(lambda: tops.attn_pair_bias.forward(d["X"], d["Z"], pre, **kw), REF_ITERS,
+                                          REF_WARMUP), 4)}
         work = apb_work(M)
         ph = run_phases([apb_phases(d, pre)], list(work), 20, 5)
         e.update(_compact({n: kernel_entry(n, ph[n], *work[n]) for n in ph}))
-        e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), 10, 2), 4)
+        e["torch_path_ms"] = round(time_ms(lambda: torch_apb(d), REF_ITERS, REF_WARMUP), 4)
         if M <= 512:
             e["ms_graph"] = round(graph_ms(lambda X, Z: tops.attn_pair_bias.forward(X, Z, pre, **kw), d["X"], d["Z"]),
                                   4)
@@ -1101,8 +1108,8 @@ def main():
     # the other two ops of the metric at their BASELINE configurations (size 1024)
     if not args.no_ops:
         out["ops"] = {
-            "triangle_attention": op_entry_tri(args.ops_size, dev, 10, 3, cpu),
-            "attention_pair_bias": op_entry_apb(args.ops_size, dev, 20, 5, cpu),
+            "triangle_attention": op_entry_tri(args.ops_size, dev, REF_ITERS, REF_WARMUP, cpu),
+            "attention_pair_bias": op_entry_apb(args.ops_size, dev, REF_ITERS, REF_WARMUP, cpu),
         }
         out["config0"] = config0_entry(dev, cpu)
     if not args.no_size_sweep:
