@@ -784,7 +784,11 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
   Frags fa, fb;
   uint32_t t = blockIdx.x;
   bool has_next = false;
-  auto ktile = [&](int kt, auto S, auto first) {
+  // stores_out: the previous block tile's 16 output stores per wave were issued after this k-tile's
+  // loads; vector memory operations count down in issue order (the compiler's own waits assume the
+  // same), so vmcnt(16) waits for the loads alone and the stores drain during this k-tile
+  // (0.263 -> 0.261 ms at L = 1024, same bits)
+  auto ktile = [&](int kt, auto S, auto first, bool stores_out = false) {
     using N = std::integral_constant<int, 1 - decltype(S)::value>;
     using NO = std::false_type;
     mfmas(fa, first);
@@ -796,7 +800,10 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
     mfmas(fa, NO{});
     frags(S, 3, fb);
     interleave();
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (stores_out)
+      asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     // the copy of k-tile kt + 2 into the stage just drained: A now, B after this k-step's MFMAs
     int lk = -1;
     if (kt + 2 < nk) {
@@ -819,7 +826,7 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
   frags(S0{}, 0, fa);
   for (; t < total; t += G) {
     has_next = t + G < total;
-    ktile(0, S0{}, std::true_type{});
+    ktile(0, S0{}, std::true_type{}, t != blockIdx.x);
     ktile(1, S1{}, std::false_type{});
     for (int kt = 2; kt < nk; kt += 2) {
       ktile(kt, S0{}, std::false_type{});
