@@ -690,6 +690,8 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
 
   __shared__ __attribute__((aligned(16))) T As0[TILE], As1[TILE];
   __shared__ __attribute__((aligned(16))) T Bs0[TILE], Bs1[TILE];
+  // per wave: 32 rows x 64 columns of its output slice on the way to HBM (the rest of the 160 KiB)
+  __shared__ __attribute__((aligned(16))) T Os[8][32 * 64];
   auto abuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? As0 : As1; };
   auto bbuf = [&](auto S) -> T* { return decltype(S)::value == 0 ? Bs0 : Bs1; };
 
@@ -832,31 +834,42 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
       ktile(kt, S0{}, std::false_type{});
       ktile(kt + 1, S1{}, std::false_type{});
     }
-    // ---- Y[i][j0 .. j0 + 15] per lane: two 16-byte stores (columns [L, ldy) get finite filler) ----
+    // ---- the wave's 128 x 64 slice of Y through its LDS buffer, 32 rows at a time: lane (c, h)
+    // ---- writes its 16 columns of row c of each 32-row group (chunks 4 j + 2 h, + 1 of the row's
+    // ---- 8, XOR-swizzled by (row >> 1) & 7: conflict-free), then each group of 8 lanes reads one
+    // ---- whole 128-byte row segment back and stores it (L % 256 == 0: every row and column of
+    // ---- the block tile lies inside Y) ----
     int64_t slab;
     int tm, tn;
     coords(t, slab, tm, tn);
-    T* Yb = Y + slab * L * ldy;
+    T* Yw = Y + slab * L * ldy + (int64_t)(tm * BM + wm * 128) * ldy + tn * BM + wn * 64;
+    T* ob = Os[wave];
     unsigned t2 = threadIdx.x;
     asm volatile("" : "+v"(t2));
     const int ecol = (int)(t2 & 31), ehl = (int)((t2 >> 5) & 1);
+    const int rrow = (int)((t2 & 63) >> 3), rch = (int)(t2 & 7);
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      const int64_t ii = (int64_t)tm * BM + wm * 128 + i * 32 + ecol;
-      if (ii < L) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-          const int64_t j0 = (int64_t)tn * BM + wn * 64 + j * 32 + 16 * ehl;
-          if (j0 >= ldy) continue;  // ldy % 64 == 0: j0 < ldy implies j0 + 16 <= ldy
-          V8 o0, o1;
+      for (int j = 0; j < NJ; ++j) {
+        V8 o0, o1;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            o0[e] = (T)acc[j][i][e];
-            o1[e] = (T)acc[j][i][8 + e];
-          }
-          stg<V8>(Yb + ii * ldy + j0, o0);
-          stg<V8>(Yb + ii * ldy + j0 + 8, o1);
+        for (int e = 0; e < 8; ++e) {
+          o0[e] = (T)acc[j][i][e];
+          o1[e] = (T)acc[j][i][8 + e];
         }
+        const int c0 = 4 * j + 2 * ehl, sw = (ecol >> 1) & 7;
+        *reinterpret_cast<V8*>(&ob[ecol * 64 + ((c0 ^ sw) << 3)]) = o0;
+        *reinterpret_cast<V8*>(&ob[ecol * 64 + (((c0 + 1) ^ sw) << 3)]) = o1;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = 8 * q + rrow;
+        const V8 v = *reinterpret_cast<const V8*>(&ob[r * 64 + ((rch ^ ((r >> 1) & 7)) << 3)]);
+        stg<V8>(Yw + (int64_t)(i * 32 + r) * ldy + 8 * rch, v);
       }
     }
   }
