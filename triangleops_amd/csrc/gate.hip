@@ -9,10 +9,10 @@
 // Both weights are read in their (out, in) nn.Linear layout: no per-call transposes.
 //
 // Tiles of 8192 / C tokens (64 at C = 128, 128 at C = 64: 16 KB of each input), 8 waves.  Waves
-// 0-3 fetch the o and gate-input tiles two tiles ahead (two register stages; C / 8 lanes per
-// token row) and stage them in LDS, normalising the gate input on the way; waves 4-7 write the
-// results, so no wave has loads and stores in flight together and each stage is waited for only
-// when consumed.  All waves compute: wave w owns features [32 (w % (C / 32)), +32) of both GEMMs
+// 0-3 fetch the gate-input tile two tiles ahead (two register stages; C / 8 lanes per token row)
+// and stage it in LDS, normalised; waves 4-7 fetch and stage the o tile the same way and write
+// the results (splitting the loads between the two roles balances them: the loaders' LayerNorm
+// had kept every other wave waiting at the first barrier; 3 % faster at N = 1024).  All waves compute: wave w owns features [32 (w % (C / 32)), +32) of both GEMMs
 // for tokens [32 (w / (C / 32)), +32), weight rows in registers (permuted so each lane ends up
 // with 16 consecutive features of one token).  The gated activations overwrite the o tile in LDS
 // and are the second GEMM's operand; the output goes through a token-major LDS tile so each
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
       if (b_ln) lnb = ldg<V8>(b_ln + 8 * ch);
     }
     struct Stage {
-      V8 o[4], g[4];
+      V8 g[4];
     };
     // same loads on every call (past the end: the last tile; tokens >= M read token M - 1)
     auto fetch = [&](uint32_t tt, Stage& sg) {
@@ -136,7 +136,6 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
         uint32_t m = tt * TOK + (k * NL + tid) / LPT;
         m = m < M ? m : M - 1;
         const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
-        sg.o[k] = ldg<V8>(o + m1 * so0 + m2 * so1 + 8 * ch);
         sg.g[k] = ldg<V8>(gin + m1 * sg0 + m2 * sg1 + 8 * ch);
       }
     };
@@ -161,7 +160,6 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
           for (int e = 0; e < 8; ++e) g[e] = (T)(((float)g[e] - mean) * rstd * (float)lnw[e] + (float)lnb[e]);
         }
         *reinterpret_cast<V8*>(&gs[tk * ROW + swz(tk, ch)]) = g;
-        *reinterpret_cast<V8*>(&ots[tk * ROW + swz(tk, ch)]) = sg.o[k];
       }
       __syncthreads();
       fetch(tt + PD * G, sg);  // refill this stage
@@ -186,19 +184,28 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
     }
     if (n > 0) step(t, s0);
   } else {
-    // ================= writers =================
+    // ================= writers: also fetch o two tiles ahead and stage it =================
     const int wt = tid - NL;
-    for (; t < ntiles; t += G) {
-      __syncthreads();  // tile staged by the loaders
-      compute1();
-      __syncthreads();  // gated tile complete
-      compute2();
-      __syncthreads();  // output tile complete
+    const int wch = wt % LPT;
+    struct OStage {
+      V8 o[4];
+    };
+    auto ofetch = [&](uint32_t tt, OStage& sg) {
+      tt = tt < ntiles ? tt : ntiles - 1;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t m = tt * TOK + (k * NL + wt) / LPT;
+        m = m < M ? m : M - 1;
+        const uint32_t m1 = M2.div(m), m2 = m - m1 * M2.d;
+        sg.o[k] = ldg<V8>(o + m1 * so0 + m2 * so1 + 8 * wch);
+      }
+    };
+    auto wstore = [&](uint32_t tt) {
 #pragma unroll
       for (int k = 0; k < TOK * C / 8 / NL; ++k) {
         const int ci = k * NL + wt;  // token ci / LPT, chunk ci % LPT
         const int tk = ci / LPT, c = ci % LPT;
-        const uint32_t m = t * TOK + tk;
+        const uint32_t m = tt * TOK + tk;
         if (m >= M) continue;
         V8 v = *reinterpret_cast<const V8*>(&os[tk * C + ((c ^ row_key<C>(tk)) << 3)]);
         if constexpr (RES) {
@@ -211,7 +218,33 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
           stg<V8>(out + (int64_t)m * C + 8 * c, v);
         }
       }
+    };
+    auto wstep = [&](uint32_t tt, OStage& sg) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int tk = (k * NL + wt) / LPT;
+        *reinterpret_cast<V8*>(&ots[tk * ROW + swz(tk, wch)]) = sg.o[k];
+      }
+      __syncthreads();  // tile staged
+      ofetch(tt + PD * G, sg);  // refill this stage
+      __builtin_amdgcn_sched_barrier(0);
+      compute1();
+      __syncthreads();  // gated tile complete
+      compute2();
+      __syncthreads();  // output tile complete
+      wstore(tt);
+    };
+    OStage o0, o1;
+    ofetch(t, o0);
+    __builtin_amdgcn_sched_barrier(0);
+    ofetch(t + G, o1);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t n = t < ntiles ? (ntiles - t + G - 1) / G : 0;
+    for (; n >= 2; n -= 2, t += 2 * G) {
+      wstep(t, o0);
+      wstep(t + G, o1);
     }
+    if (n > 0) wstep(t, o0);
   }
 }
 
