@@ -677,6 +677,12 @@ __global__ __launch_bounds__(512) void tmu_einsum_large_kernel(const T* __restri
 // halves, the A operand right after the barrier and the B operand after the k-step that follows
 // (one burst of all eight copy instructions per wave measured 2 % / 6 % slower at L = 1024 / 2048;
 // quarters spread further, into the next k-tile, leave the late ones too little time).
+// Staggered k order: block tile (tm, tn) runs its k-tiles from (tm + tn) % tiles on, cyclically.
+// The blocks of one slab run in step, so without it the four (L = 1024) blocks that read one A or B
+// k-slice all miss in L2 on it together; with it each slice's readers start at distinct k-tiles,
+// one k-tile apart, and all but the first find the slice in L2 (0.260 -> 0.246 ms at L = 1024,
+// 1.78 -> 1.75 at 2048; a rotation by quarters of the k range lets the slices leave L2 first and is
+// slower).  The k order is the only change: the sum over k is associated per k-tile in this order.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
@@ -729,17 +735,21 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
   }
   const char* abase;
   const char* bbase;
+  int rot = 0;  // the first k-tile of the block tile being loaded (staggered k order)
   auto setup = [&](uint32_t t) {
     int64_t slab;
     int tm, tn;
     coords(t, slab, tm, tn);
     abase = reinterpret_cast<const char*>(A + (slab * L + (int64_t)tm * BM) * ld);
     bbase = reinterpret_cast<const char*>(Bmat + (slab * L + (int64_t)tn * BM) * ld);
+    rot = (tm + tn) % tiles;  // < tiles < nk
   };
   // operand part: 0 = A, 1 = B, 2 = both
   auto gload = [&](int kt, auto S, int part = 2) {
-    const char* ak = abase + (int64_t)kt * BK * sizeof(T);
-    const char* bk = bbase + (int64_t)kt * BK * sizeof(T);
+    int pk = kt + rot;  // k-tile kt of the staggered order
+    pk = pk >= nk ? pk - nk : pk;
+    const char* ak = abase + (int64_t)pk * BK * sizeof(T);
+    const char* bk = bbase + (int64_t)pk * BK * sizeof(T);
     const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 4 * 1024);
     const uint32_t bs = (uint32_t)reinterpret_cast<uintptr_t>(bbuf(S)) + (uint32_t)(wave * 4 * 1024);
 #pragma unroll
