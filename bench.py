@@ -6,7 +6,9 @@ Default workload (the configuration its metric is quot
 triangle_multiplicative_update in bf16 at L = 1024, C = 128, B = 1, pad mask zeroing the last
 10% of rows/cols, random-init LayerNorm / projection weights.  One step = one outgoing call
 plus one incoming call (the two directions a Pairformer block runs).  Inputs are resident in
-HBM before timing; the precompute (weight folding) is outside the timed region.
+HBM before timing; the precompute (weight folding) is outside the timed region.  Before the W
+warmup steps the headline runs untimed steps for SETTLE_S seconds (`settle_steps` in the line), so
+the K timed steps run at the clocks of a loaded chip, not during their ramp from idle.
 
 Prints ONE JSON line with the contract fields plus:
   roofline      dominant kernel of the step (largest average launch time), its algorithmic
@@ -272,6 +274,8 @@ def torch_pair_stack(z, m, w_out, w_in, ts, te, eps=1e-5):
 # calls, then 30 calls each bracketed by events and a synchronize, the median); the op entries use
 # it where a call is short enough, so clocks have settled as they have in the reference's runs
 REF_ITERS, REF_WARMUP = 30, 12
+# seconds of untimed headline steps before its warmup steps (clocks at their loaded level)
+SETTLE_S = 0.25
 
 
 def time_ms(fn, iters, warmup):
@@ -1050,6 +1054,20 @@ def main():
     steps = [tmu_phases(x, m, pre, "outgoing"), tmu_phases(x, m, pre, "incoming")]
     names = list(tmu_work(L))
 
+    # settle: untimed steps until the chip has run the workload for SETTLE_S seconds.  On a GPU that
+    # was idle, the first ~25 ms of this work ran ~8 % slower than every later 20-step block (the
+    # clocks come up under load), so a timed region right after a few warmup steps measured the
+    # ramp instead of the steady state
+    settle_steps, t_settle = 0, time.perf_counter()
+    while True:
+        for _ in range(10):
+            for pl in steps:
+                for ph in pl:
+                    ph()
+        settle_steps += 10
+        torch.cuda.synchronize()
+        if time.perf_counter() - t_settle >= SETTLE_S:
+            break
     # warmup
     for _ in range(args.warmup):
         for pl in steps:
@@ -1087,6 +1105,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_steps": settle_steps,
         "ms_per_step": round(ms_per_step, 4),
         "ms_per_call": round(ms_per_step / 2, 4),
         "higher_is_better": True,
