@@ -677,12 +677,15 @@ __global__ __launch_bounds__(512) void tmu_einsum_large_kernel(const T* __restri
 // halves, the A operand right after the barrier and the B operand after the k-step that follows
 // (one burst of all eight copy instructions per wave measured 2 % / 6 % slower at L = 1024 / 2048;
 // quarters spread further, into the next k-tile, leave the late ones too little time).
-// Staggered k order: block tile (tm, tn) runs its k-tiles from (tm + tn) % tiles on, cyclically.
-// The blocks of one slab run in step, so without it the four (L = 1024) blocks that read one A or B
-// k-slice all miss in L2 on it together; with it each slice's readers start at distinct k-tiles,
-// one k-tile apart, and all but the first find the slice in L2 (0.260 -> 0.246 ms at L = 1024,
-// 1.78 -> 1.75 at 2048; a rotation by quarters of the k range lets the slices leave L2 first and is
-// slower).  The k order is the only change: the sum over k is associated per k-tile in this order.
+// Staggered k order: block tile (tm, tn) takes k-tile kt ^ r at step kt, r = (tm + tn) & (P - 1)
+// (P: the largest power of two <= tiles that divides the k-tile count).  The blocks of one slab run
+// in step, so in the natural order the P blocks that read one A or B k-slice all miss in L2 on it
+// together; with r distinct over those readers (a Latin square over the slab's tiles) they visit the
+// slice at distinct steps of one aligned group of P steps, so all but the first find it in L2, and
+// no reader comes back to a slice long after the others (a cyclic shift by r instead took as long
+// but re-fetched the r slices that wrap around, 1.19x the operand bytes at L = 1024 against 1.007x
+// here).  0.266 -> 0.251 ms at L = 1024, 1.806 -> 1.760 at 2048.  The k order is the only change:
+// the sum over k is associated per k-tile in this order.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __restrict__ A, const T* __restrict__ Bmat,
@@ -735,19 +738,20 @@ __global__ __launch_bounds__(512) void tmu_einsum_persist_kernel(const T* __rest
   }
   const char* abase;
   const char* bbase;
-  int rot = 0;  // the first k-tile of the block tile being loaded (staggered k order)
+  int rot = 0;  // k order of the block tile being loaded: k-tile kt ^ rot at step kt
+  int rmask = 0;  // P - 1
+  while (2 * (rmask + 1) <= tiles && nk % (2 * (rmask + 1)) == 0) rmask = 2 * rmask + 1;
   auto setup = [&](uint32_t t) {
     int64_t slab;
     int tm, tn;
     coords(t, slab, tm, tn);
     abase = reinterpret_cast<const char*>(A + (slab * L + (int64_t)tm * BM) * ld);
     bbase = reinterpret_cast<const char*>(Bmat + (slab * L + (int64_t)tn * BM) * ld);
-    rot = (tm + tn) % tiles;  // < tiles < nk
+    rot = (tm + tn) & rmask;
   };
   // operand part: 0 = A, 1 = B, 2 = both
   auto gload = [&](int kt, auto S, int part = 2) {
-    int pk = kt + rot;  // k-tile kt of the staggered order
-    pk = pk >= nk ? pk - nk : pk;
+    const int pk = kt ^ rot;  // < nk: rmask + 1 divides nk
     const char* ak = abase + (int64_t)pk * BK * sizeof(T);
     const char* bk = bbase + (int64_t)pk * BK * sizeof(T);
     const uint32_t as = (uint32_t)reinterpret_cast<uintptr_t>(abuf(S)) + (uint32_t)(wave * 4 * 1024);
