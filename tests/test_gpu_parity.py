@@ -211,13 +211,17 @@ def test_tmu_fp16_large_offset(device, direction):
 @pytest.mark.parametrize("L,nslab,dtype", [(400, 8, torch.bfloat16), (600, 64, torch.bfloat16),
                                            (768, 4, torch.bfloat16), (1000, 32, torch.bfloat16),
                                            (1024, 40, torch.bfloat16), (600, 64, torch.float16),
-                                           (768, 4, torch.float16)])
+                                           (768, 4, torch.float16), (512, 100, torch.bfloat16),
+                                           (1280, 16, torch.bfloat16), (1536, 12, torch.bfloat16),
+                                           (2048, 6, torch.bfloat16)])
 def test_tmu_einsum_large_kernels(device, L, nslab, dtype):
     """The L > 384 einsum kernels against a torch fp32 product of the same 16-bit operands: odd
     k-tile counts (L = 400), rows past L in the last block tile (L = 600, 1000), and the
     persistent kernel (L % 256 == 0) with fewer block tiles than CUs (L = 768) and with several
-    block tiles per block in an uneven split (L = 1024, 640 tiles).  Each output is the fp32 sum rounded once: within half an ulp of the 16-bit
-    type plus the fp32 summation-order difference."""
+    block tiles per block in an uneven split (L = 1024, 640 tiles), including each width of its
+    staggered k order (k-tile kt ^ r, r < 2 / 4 / 8 at L = 512 / 1024-1536 / 2048; L = 1280 and
+    1536 have 5 and 6 block tiles per slab side, not a power of two).  Each output is the fp32 sum
+    rounded once: within half an ulp of the 16-bit type plus the fp32 summation-order difference."""
     ld = (L + 63) // 64 * 64
     g = torch.Generator().manual_seed(L + nslab)
     ab = torch.zeros(2 * nslab, 1, L, ld, dtype=dtype)
