@@ -7,8 +7,8 @@
 //                       KV  [i][h][kb][4096] per 64-key block: K [64 keys][32 d permuted] then
 //                                            V^T [32 d][64 keys permuted]
 //                       bias[h][qt][kt][1024] log2(e) * bias per 32 x 32 (query, key) tile, in
-//                                            the order of the MFMA B operand (below); keys
-//                                            >= N hold zeros
+//                                            the order of the score MFMA's D registers
+//                                            (below); keys >= N hold zeros
 //   tri_attn_kernel   4 waves per (row i, head h, query chunk): the KV block of each 64 keys is
 //                     copied into LDS (double-buffered, one barrier per block), each wave
 //                     streams its query tiles over it with an online softmax in the exp2
@@ -20,9 +20,11 @@
 // i.e. position 16 j + 8 hl + e (j = 0, 1; hl = lane / 32; e < 8) holds the element that the
 // MFMA D register v = 8 j + e of lane half hl holds (8 (v / 4) + 4 hl + v % 4), so every MFMA
 // operand of the attention kernel is one 16-byte load.
-// Bias tile (query tile qt, key tile kt): element (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e)
-// sits at (64 j + 32 hl + c) * 8 + e, so the B operand of half j for lane (c, hl) is 16 bytes
-// and one load instruction of a wave reads 1 KB contiguous.
+// Bias tile (query tile qt, key tile kt): element (q, k) = (32 qt + c, 32 kt + p) sits at
+// (64 j + 32 hl + c) * 8 + e for the key p = perm(16 j + 8 hl + e) that D register v = 8 j + e of
+// lane (c, hl) holds (the permutation above), so the 16 score slots of a lane are two 16-byte
+// loads, widened to fp32 they are the score MFMAs' accumulator initialiser, and one load
+// instruction of a wave reads 1 KB contiguous.
 //
 // Reference: triangle_attn/module.py:57-125 (forward), triangle_attn/kernel.py:36-98 (bias),
 // :110-253 (attention), :230-238 and :369 (additive -1e9 pair mask, -inf outside the row).
@@ -77,6 +79,7 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
   constexpr int PD = 4;            // loader register stages in flight
   constexpr int PART = 64 * D * 2; // bytes of one head's Q, K or V^T block of a tile
   using V8 = vec<T, 8>;
+  using V4 = vec<T, 4>;
 
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];    // normalised x tiles
   __shared__ __attribute__((aligned(16))) char os[H][3 * PART];   // per writer wave: Q | K | V^T
@@ -256,11 +259,13 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
           stg<V8>(dst + 8 * ci, *reinterpret_cast<const V8*>(oh + part * PART + a));
         }
       }
-      if (lane < 8) {  // bias: 8 positions of this head per lane, 16 bytes
-        const int g = lane;
-        const uint64_t off = (((uint64_t)h * nqt + i / 32) * nkt + 2 * kb + (g >> 2)) * 1024 +
-                             (((g >> 1) & 1) * 64 + (g & 1) * 32 + (i & 31)) * 8;
-        stg<V8>(bias + off, *reinterpret_cast<const V8*>(&bs[bb][h * BSR + 8 * g]));
+      if (lane < 8) {  // bias: lane g stores chunk (j, hl) = ((g >> 1) & 1, g & 1) of query i in key
+        // tile 2 kb + (g >> 2): positions 16 j + 4 hl + 0..3 and + 8 of that tile (16 bytes)
+        const int g = lane, kt = g >> 2, j = (g >> 1) & 1, hh = g & 1;
+        const uint64_t off = (((uint64_t)h * nqt + i / 32) * nkt + 2 * kb + kt) * 1024 + (j * 64 + hh * 32 + (i & 31)) * 8;
+        const T* src = &bs[bb][h * BSR + 32 * kt + 16 * j + 4 * hh];
+        const V4 lo = *reinterpret_cast<const V4*>(src), hi = *reinterpret_cast<const V4*>(src + 8);
+        stg<V8>(bias + off, V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
       }
       bb ^= 1;
     }
@@ -273,8 +278,8 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 // per wave, 64-key blocks of two 32-key tiles.  Both block sizes give the same bits.
 //
 // Per (32-key tile, query tile) a wave runs
-//     S^T  = C0 + I . bias^T          2 MFMAs, A = identity, B = 16 bias bytes per lane
-//          + K . Q^T                  2 MFMAs, K from LDS, Q^T in registers
+//     S^T  = bias + C0 + K . Q^T      2 MFMAs, K from LDS, Q^T in registers; the accumulator
+//                                     starts at the lane's 16 bias values (bias_acc)
 //     P    = exp2(S^T)                16 v_exp per lane, no max / subtract per element
 //     O^T += V^T . P^T                2 MFMAs, V^T from LDS, P^T = S^T's D registers
 //     l   += 1 . P^T                  2 16x16x32 MFMAs on the same P^T (bf16; row_sum_selector)
@@ -284,14 +289,14 @@ __global__ __launch_bounds__(512) void tri_prep_kernel(const T* __restrict__ x, 
 //   (fp32 sums of the rounded weights the PV product uses, by the matrix cores) is checked once
 //   at the end, and a wave whose l left [2^-60, 2^100] (or is not finite) recomputes its tiles
 //   with an exact running max (tri_exact_tile, out of line).  The loop itself then has no max,
-//   no subtraction, no per-tile overflow test and no accumulator initialiser (C0 = 0).
-//   fp16: C0 = -m (the running row max, broadcast) enters as the accumulator initialiser.  m is
+//   no subtraction and no per-tile overflow test (C0 = 0).
+//   fp16: C0 = -m (the running row max, broadcast) is added to the initialiser.  m is
 //   exact from the first tile with a valid key on and is only raised when a tile's
 //   probabilities could overflow fp16 (then O and l are rescaled and the tile recomputed).
 // Masked keys get probability exactly 0 (equal to the reference's exp(-1e9 - m) in fp32
 // whenever the row has a valid key); a row without valid keys takes the uniform average of V
-// over all N keys, as the reference's -1e9 add gives.  The identity MFMA multiplies every bias
-// element of the tile by 0 or 1, so the bias padding must be finite (the pre-pass writes zeros).
+// over all N keys, as the reference's -1e9 add gives.  Keys >= N hold zero bias (the pre-pass and
+// the repack write zeros) and are masked like the others.
 //
 // Each tile is one straight-line phase in which the score MFMAs of the NEXT tile are
 // interleaved (sched_group_barrier) with the exponentials of the current one, so the matrix
@@ -305,9 +310,9 @@ constexpr int kKVLds = 64 * kKPad + 32 * kVPad;
 // scheduling-group masks of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 
-// A row whose keys are all masked: with Q and the bias identity zeroed, every score of the main
-// loop would be C0 = 0, so each key k < N weighs exactly 1 and each key >= N 0, in every query
-// column alike: O[q] = (sum over k < N of V[k]) / N, one vector for the whole row.  The waves of the
+// A row whose keys are all masked: the reference adds -1e9 to every score, which leaves them all
+// equal in fp32, so each key k < N weighs exactly 1 and each key >= N 0, in every query column
+// alike: O[q] = (sum over k < N of V[k]) / N, one vector for the whole row.  The waves of the
 // block split the visited blocks (wave w takes w, w + nw, ...; two blocks' loads in flight per
 // lane), each lane (d = lane % 32, key half lane / 32) adds its 32 positions of the block's V^T
 // row d in fp32, the halves and waves are added through LDS, and each wave writes its query tiles.
@@ -393,6 +398,31 @@ __device__ inline vec<T, 8> row_sum_selector(int lane) {
   return a;
 }
 
+// The 16 fp32 bias values of a lane's score slots (D layout of a 32 x 32 score tile: slot v =
+// 8 j + e is element e of the tile's 16-byte load j), exactly widened from the 16-bit tile; they
+// initialise the score MFMAs' accumulator, so S = bias + K . Q^T with no MFMA spent on the bias.
+template <typename T>
+__device__ inline f32x16 bias_acc(vec<T, 8> b0, vec<T, 8> b1) {
+  f32x16 c;
+  if constexpr (std::is_same<T, __bf16>::value) {  // bf16 -> fp32 is a 16-bit shift
+    const auto w0 = __builtin_bit_cast(vec<uint32_t, 4>, b0), w1 = __builtin_bit_cast(vec<uint32_t, 4>, b1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      c[2 * e] = __uint_as_float(w0[e] << 16);
+      c[2 * e + 1] = __uint_as_float(w0[e] & 0xffff0000u);
+      c[8 + 2 * e] = __uint_as_float(w1[e] << 16);
+      c[8 + 2 * e + 1] = __uint_as_float(w1[e] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      c[e] = (float)b0[e];
+      c[8 + e] = (float)b1[e];
+    }
+  }
+  return c;
+}
+
 // One query tile (32 queries of row i, head h) recomputed with an exact running max: the
 // classic online softmax over the visited tiles in the main loop's order, its operands read from
 // global memory (K and V^T from the row's KV blocks, whose rows are 32 / 64 elements wide there,
@@ -402,7 +432,7 @@ __device__ inline vec<T, 8> row_sum_selector(int lane) {
 // tile (query tile, key tile 0), as the main loop's bq.
 template <typename T>
 __device__ __noinline__ void tri_exact_tile(const T* __restrict__ kvrow, const T* __restrict__ bqt,
-                                            vec<T, 8> q0, vec<T, 8> q1, vec<T, 8> id0, vec<T, 8> id1,
+                                            vec<T, 8> q0, vec<T, 8> q1,
                                             const short* vblk, const unsigned long long* kvalid, int nv, int64_t N,
                                             T* __restrict__ out, int64_t i, int64_t so0, int64_t so1, int h, int dv,
                                             int64_t q, int lane) {
@@ -421,8 +451,7 @@ __device__ __noinline__ void tri_exact_tile(const T* __restrict__ kvrow, const T
       const T* kr = kvrow + (int64_t)kb * kKVBlock + (32 * kt + col) * D + 8 * hl;
       const T* vr = kvrow + (int64_t)kb * kKVBlock + 64 * D + col * 64 + 32 * kt + 8 * hl;
       const T* br = bqt + (int64_t)(2 * kb + kt) * 1024;
-      f32x16 s = Mma<T>::m32(id0, ldg<V8>(br), f32x16{});
-      s = Mma<T>::m32(id1, ldg<V8>(br + 512), s);
+      f32x16 s = bias_acc<T>(ldg<V8>(br), ldg<V8>(br + 512));
       s = Mma<T>::m32(ldg<V8>(kr), q0, s);
       s = Mma<T>::m32(ldg<V8>(kr + 16), q1, s);
       const unsigned int lb = tb >> (4 * hl);
@@ -517,8 +546,8 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- Q^T operands (already scaled by scale * log2 e and d-permuted) and bias pointers, loaded
-  // ---- before the key-validity pass so the loads overlap it (a row without valid keys zeroes
-  // ---- Q and the identity below, so its scores are all C0) ----
+  // ---- before the key-validity pass so the loads overlap it (a row without valid keys skips
+  // ---- the main loop: tri_uniform_row below) ----
   const int64_t qbase = (int64_t)qc * (NW * 32 * QT) + (int64_t)wave * 32 * QT;
   V8 qop[QT][2];
   const T* bq[QT];
@@ -609,13 +638,6 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
     return;
   }
 
-  // identity A operands: (I . B)[key][q] = B[key - 16 j][q] for the keys of half j
-  V8 ident[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ident[j][e] = (T)((!uniform && col == 16 * j + 8 * hl + e) ? 1.f : 0.f);
-
   f32x16 o[QT], cinit[QT];
   float l[QT];   // fp16: row sums (lanes l and l ^ 32 hold halves)
   f32x4 ls[QT];  // bf16: row sums accumulated by the matrix cores, slot 0 = the query's whole sum
@@ -633,9 +655,9 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
   auto scores = [&](const V8* kop, V8 (*bb)[2], f32x16* s) {
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
-      s[t] = Mma<T>::m32(ident[0], bb[t][0], OPT ? f32x16{} : cinit[t]);
-      s[t] = Mma<T>::m32(ident[1], bb[t][1], s[t]);
-      s[t] = Mma<T>::m32(kop[0], qop[t][0], s[t]);
+      f32x16 c = bias_acc<T>(bb[t][0], bb[t][1]);
+      if constexpr (!OPT) c += cinit[t];
+      s[t] = Mma<T>::m32(kop[0], qop[t][0], c);
       s[t] = Mma<T>::m32(kop[1], qop[t][1], s[t]);
     }
   };
@@ -692,16 +714,18 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
       pin(p[t][0]);
       pin(p[t][1]);
     }
-    constexpr int VPM = OPT ? (NW == 4 ? 8 : 6) : 9;  // VALU instructions per score MFMA in the interleave
+    // VALU instructions per score MFMA in the interleave (exponentials, converts and the next
+    // tile's bias widening)
+    constexpr int VPM = OPT ? (NW == 4 ? 24 : 20) : 26;
     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-    for (int m = 0; m < 2 * QT; ++m) {
+    for (int m = 0; m < QT; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedValu, VPM, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 2 * QT, 0);
 #pragma unroll
-    for (int m = 0; m < 2 * QT; ++m) {
+    for (int m = 0; m < QT; ++m) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedValu, VPM, 0);
     }
@@ -796,7 +820,7 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
     if (__ballot(bad) != 0) {  // wave-uniform
 #pragma unroll
       for (int t = 0; t < QT; ++t)
-        tri_exact_tile<T>(kvrow, bq[t], qop[t][0], qop[t][1], ident[0], ident[1], vblk,
+        tri_exact_tile<T>(kvrow, bq[t], qop[t][0], qop[t][1], vblk,
                           kvalid, nv, N, out, i, so0, so1, h, dv, qbase + 32 * t + col, lane);
       return;
     }
@@ -870,8 +894,8 @@ __global__ __launch_bounds__(64 * NW, TRI_WPE(QT, NW)) void tri_attn_kernel(cons
 // blocks, one barrier per block, copies issued three blocks ahead.  Stages are software-pipelined:
 // stage (row r, tile t) issues the PV MFMAs of the previous stage and the score MFMAs of the next
 // one (the other row) between its own exponentials.  A row without valid keys (the uniform average
-// of V over the N keys, as the reference's -1e9 add gives) runs in the loop with Q and the identity
-// zeroed when its pair partner has valid keys, and its O is then written by tri_uniform_row.
+// of V over the N keys, as the reference's -1e9 add gives) runs in the loop when its pair partner
+// has valid keys, its result unused, and its O is then written by tri_uniform_row.
 // Masked keys get weight exactly 0.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRing = 4;  // LDS slots of 64-key KV blocks (per block: 2 rows x 8 KB each)
@@ -981,12 +1005,6 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     return;
   }
 
-  // ---- the identity of the bias MFMAs ----
-  V8 ident[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ident[j][e] = (T)(col == 16 * j + 8 * hl + e ? 1.f : 0.f);
   const int qtc = qt < nqt ? qt : nqt - 1;
   const T* bq = bias + ((int64_t)h * nqt + qtc) * nkt * 1024 + (32 * hl + col) * 8;
 
@@ -1059,8 +1077,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
   V8 bset[2][2][2];  // bias operands of visits vj, vj + 1 (set vj % 2): [tile][half]
 
   auto scores = [&](int r, const V8* k, const V8* b) {
-    f32x16 s = Mma<T>::m32(ident[0], b[0], f32x16{});
-    s = Mma<T>::m32(ident[1], b[1], s);
+    f32x16 s = bias_acc<T>(b[0], b[1]);
     s = Mma<T>::m32(k[0], qop[r][0], s);
     return Mma<T>::m32(k[1], qop[r][1], s);
   };
@@ -1198,7 +1215,7 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
     }
     const float lt = ls[r][0];
     if (__ballot(!(lt >= 0x1p-60f && lt <= 0x1p100f)) != 0) {  // wave-uniform
-      tri_exact_tile<T>(KV + kvoff[r], bq, qop[r][0], qop[r][1], ident[0], ident[1], vblk, kvalid[r], nv, N, out,
+      tri_exact_tile<T>(KV + kvoff[r], bq, qop[r][0], qop[r][1], vblk, kvalid[r], nv, N, out,
                         irow[r], so0, so1, h, D, qo, lane);
       continue;
     }
@@ -1227,7 +1244,8 @@ __global__ __launch_bounds__(256, 2) void tri_attn2_kernel(const T* __restrict__
 //   what 0: Qp    chunk (row r = (i H + h) ldn + p, c < 4): d-permuted elements 8c .. 8c + 7
 //   what 1: KV    chunk (block (i H + h) nkb + kb, m < 512): m < 256 -> K row m / 4, chunk m % 4;
 //                 else V^T row d = (m - 256) / 8, chunk (m - 256) % 8 (keys permuted per 32)
-//   what 2: bias  chunk (tile (h nqt + qt) nkt + kt, ch < 128): elements 8 ch .. 8 ch + 7
+//   what 2: bias  chunk (tile (h nqt + qt) nkt + kt, ch < 128): elements 8 ch .. 8 ch + 7 (keys
+//                 permuted per 32)
 // ---------------------------------------------------------------------------------------------
 __device__ inline int perm32(int x) {  // position x of a permuted group of 32 -> natural index
   const int j = x >> 4, hl = (x >> 3) & 1, e = x & 7;
@@ -1286,10 +1304,12 @@ __global__ __launch_bounds__(256) void tri_repack_kernel(int what, const T* __re
       const int qt = (int)(hq % nqt);
       const int h = (int)(hq / nqt);
       const int j = ch >> 6, hl = (ch >> 5) & 1, c = ch & 31;
-      const int qq = 32 * qt + c, k0 = 32 * kt + 16 * j + 8 * hl;
+      const int qq = 32 * qt + c;
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        out[e] = (qq < N && k0 + e < N) ? (T)(kLog2e * bias[((int64_t)h * N + qq) * N + k0 + e]) : (T)0.f;
+      for (int e = 0; e < 8; ++e) {
+        const int kk = 32 * kt + perm32(16 * j + 8 * hl + e);
+        out[e] = (qq < N && kk < N) ? (T)(kLog2e * bias[((int64_t)h * N + qq) * N + kk]) : (T)0.f;
+      }
     }
     stg<V8>(dst + 8 * idx, out);
   }

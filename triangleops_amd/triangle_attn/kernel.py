@@ -207,7 +207,8 @@ def generic_attention(q, k, v, bias, out, *, scale=1.0, mask=None):
 def untile_bias(bias, N):
     """(H, N, N) view-copy of the pre-pass bias tiles (log2(e)-scaled, see tops_tri_prep)."""
     H, nqt, nkt, _ = bias.shape
-    t = bias.view(H, nqt, nkt, 2, 2, 32, 8).permute(0, 1, 5, 2, 3, 4, 6)  # h, qt, c, kt, j, hl, e
+    # element (32 qt + c, 32 kt + 16 j + 8 u + 4 hl + e) of a tile at (64 j + 32 hl + c) * 8 + 4 u + e
+    t = bias.view(H, nqt, nkt, 2, 2, 32, 2, 4).permute(0, 1, 5, 2, 3, 6, 4, 7)  # h, qt, c, kt, j, u, hl, e
     return t.reshape(H, nqt * 32, nkt * 32)[:, :N, :N]
 
 
