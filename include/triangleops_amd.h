@@ -88,8 +88,9 @@ int tops_tmu_output_phase(const void* y, const void* x, const void* Wp, const vo
  *   KV     io   (N, H, ldn/64, 4096): per 64-key block K (64 keys x 32, d permuted) then
  *               V^T (32 x 64 keys, keys permuted the same way within each 32); zero for d >= D
  *   bias   io   (H, ceil(N/32), ldn/32, 1024): log2(e) * (LN(x)[q,k,:] . WZ[h,:] + BZ[h]) per
- *               32 x 32 (query, key) tile; (q, k) = (32 qt + c, 32 kt + 16 j + 8 hl + e) at
- *               element (64 j + 32 hl + c) * 8 + e of tile (qt, kt); zeros for k >= N
+ *               32 x 32 (query, key) tile; (q, k) = (32 qt + c, 32 kt + 16 j + 8 u + 4 hl + e)
+ *               (u < 2, e < 4) at element (64 j + 32 hl + c) * 8 + 4 u + e of tile (qt, kt),
+ *               i.e. the keys permuted within each 32 as Q's d are; zeros for k >= N
  * C in {128, 64}, H == 4, D in {32, 16} (the default shape and the C_in = 64, D = 16 "Apo" shape
  * of tests/test_triangle_attn.py:137-192, which the reference runs on its tensor-core kernel:
  * triangle_attn/kernel.py:211-213), N <= 16384 (tops_tri_generic_prep serves other shapes).
