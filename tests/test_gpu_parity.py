@@ -649,7 +649,11 @@ def test_tri_tuned_other_shapes(device, N, C, D, mask):
 @pytest.mark.parametrize("C", [64, 128])
 def test_gate_tuned_matches_generic(device, C):
     """The tuned gate (C = 64 and 128) against the any-shape gate on the same inputs: with and without
-    the LayerNorm of its input, with the fused residual add into a transposed destination view."""
+    the LayerNorm of its input, with the fused residual add into a transposed destination view.  The
+    tuned kernel takes the gate's weights times -log2(e) in the 16-bit type (one more rounding than
+    the any-shape kernel's fp32 scaling), so a sum with the residual (values up to ~5 here, one
+    bf16 rounding of the total) may fall on the other side of a rounding step: that comparison
+    allows half an ulp of the largest magnitude beyond the bar, as the Pairformer block check does."""
     from triangleops_amd.triangle_attn.kernel import _gate_out_generic, gate_out_forward
 
     g = torch.Generator().manual_seed(C)
@@ -668,7 +672,10 @@ def test_gate_tuned_matches_generic(device, C):
     dst_a, dst_b = torch.zeros_like(res), torch.zeros_like(res)
     gate_out_forward(o, x, Wg, None, Wo, None, ln=ln, residual=res.transpose(0, 1), out=dst_a.transpose(0, 1))
     _gate_out_generic(o, x, Wg, None, Wo, None, ln=ln, residual=res.transpose(0, 1), out=dst_b.transpose(0, 1))
-    _check(dst_a, dst_b.float().cpu(), torch.bfloat16, f"gate C={C} residual")
+    diff, cos = compare(dst_a, dst_b.float().cpu())
+    tol = TOL_MAX_ABS[torch.bfloat16] + 0.5 * _bf16_ulp(float(dst_b.float().abs().max()))
+    assert torch.isfinite(dst_a.float()).all() and diff <= tol and cos >= TOL_COS, \
+        f"gate C={C} residual: max|d|={diff:.3e} (bar {tol:.3e}) cos={cos:.6f}"
 
 
 @pytest.mark.parametrize("N,C,H,D", [(40, 96, 3, 24), (70, 64, 2, 64), (130, 32, 8, 8), (257, 64, 4, 16)])

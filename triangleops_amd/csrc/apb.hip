@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   __shared__ __attribute__((aligned(16))) char og_s[TOK * ROW];  // merged Og, then the gated values
   __shared__ __attribute__((aligned(16))) char x_s[TOK * ROW];   // gate input X
   __shared__ __attribute__((aligned(16))) T o_s[TOK * C];         // output tile, query-major
-  __shared__ __attribute__((aligned(16))) float cst[2][C];        // -log2(e) bg, bo
+  __shared__ __attribute__((aligned(16))) float cst[C];           // bo
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
@@ -341,8 +341,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   auto swz = [](int t, int chunk) { return (chunk ^ row_key<C>(t)) << 4; };
 
   for (int i = tid; i < C; i += 256) {
-    cst[0][i] = bg ? -kLog2e * (float)bg[i] : 0.f;
-    cst[1][i] = bo ? (float)bo[i] : 0.f;
+    cst[i] = bo ? (float)bo[i] : 0.f;
   }
   // X rows of the block's queries (rows past M repeat row M - 1; their results are not stored)
   {
@@ -352,13 +351,24 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   }
   // weight rows as MFMA A operands: row col of wave w is feature 32 w + prow
   const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
-  V8 wg[KS], wo[KS];
+  // G's rows times -log2(e) and its bias -log2(e) bg as one more MFMA k-step, as in the triangle
+  // gate kernel (the accumulator is the gate's exp2 argument; same bits as that kernel)
+  V8 wg[KS], wo[KS], gb_a, one_b;
   {
     const int64_t frow = (int64_t)(32 * wave + prow) * C;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+      const V8 g = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wg[s][e] = (T)((float)g[e] * -kLog2e);
       wo[s] = ldg<V8>(Wo + frow + 16 * s + 8 * hl);
+    }
+    const float cb = bg ? -kLog2e * (float)bg[32 * wave + prow] : 0.f;
+    const T bhi = (T)cb, blo = (T)(cb - (float)bhi);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      gb_a[e] = hl == 0 && e == 0 ? bhi : (hl == 0 && e == 1 ? blo : (T)0.f);
+      one_b[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
     }
   }
   // ---- merge the split partials ----
@@ -426,7 +436,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   {  // GEMM 1, sigmoid gate, Og * gate -> in place over the Og tile
     const char* grow = &x_s[tok * ROW];
     char* orow = &og_s[tok * ROW];
-    f32x16 acc = {};
+    f32x16 acc = Mma<T>::m32(gb_a, one_b, f32x16{});
 #pragma unroll
     for (int k = 0; k < KS; ++k)
       acc = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(grow + swz(tok, 2 * k + hl)), acc);
@@ -438,7 +448,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
       V8 r;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(acc[8 * h + e], -kLog2e, cst[0][f0 + 8 * h + e])));
+        const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(acc[8 * h + e]));
         r[e] = (T)((float)ov[e] * gate);
       }
       *p = r;
@@ -455,7 +465,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     for (int h = 0; h < 2; ++h) {
       V8 r;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[1][f0 + 8 * h + e]);
+      for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[f0 + 8 * h + e]);
       const int c = f0 / 8 + h;
       *reinterpret_cast<V8*>(&o_s[tok * C + ((c ^ row_key<C>(tok)) << 3)]) = r;
     }

@@ -95,9 +95,10 @@ __device__ inline GridTile grid_tile_fast(uint32_t t, const FastDiv& tpr, const 
 //   passes for fp16, as in ln_stats16) and stage the normalised tile and the mask in LDS
 //   (double-buffered);
 //   waves 4 .. 4 + NWR - 1 (writers, NWR = C_out / 32) each own 32 output features: P and G weight rows in
-//   registers as the MFMA B operand, D = x . W^T with the A operand read in a permuted token
-//   order so each lane ends up with 16 consecutive tokens of one feature (P's bias added by one
-//   more MFMA k-step), the gate and mask in the epilogue, and a private feature-major LDS tile
+//   registers as the MFMA B operand (G's scaled by -log2(e)), D = x . W^T with the A operand read in
+//   a permuted token order so each lane ends up with 16 consecutive tokens of one feature (each
+//   bias added by one more MFMA k-step, so G's accumulator is the gate's exp2 argument), the gate
+//   and mask in the epilogue, and a private feature-major LDS tile
 //   that the same wave stores with whole 128-byte rows (8 features x 64 tokens per store
 //   instruction).
 // No wave has loads and stores in flight together; one barrier per tile, and the loaders'
@@ -238,19 +239,27 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       wp[s] = ldg<V8>(Wp + (int64_t)f * C + 16 * s + 8 * hl);
-      wg[s] = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
+      // G's rows times -log2(e) (one more 16-bit rounding of the weight), so the accumulator is
+      // the gate's exp2 argument: no multiply-add per output (3 % faster, outputs within a bf16
+      // step)
+      const V8 g = ldg<V8>(Wg + (int64_t)f * C + 16 * s + 8 * hl);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wg[s][e] = (T)((float)g[e] * -kLog2e);
     }
     const float cbg2 = -kLog2e * Bg[f];  // gate in the exp2 domain
-    // P's bias enters through one more MFMA k-step: A = 1 at k = 0, 1 for every token, B = the
-    // feature's fp32 bias as two 16-bit parts (hi + lo equal to it within ~2^-16 relative)
-    V8 one_a, bias_b;
+    // P's bias and G's (-log2(e) Bg) enter through one more MFMA k-step each: A = 1 at k = 0, 1
+    // for every token, B = the feature's fp32 bias as two 16-bit parts (hi + lo equal to it
+    // within ~2^-16 relative)
+    V8 one_a, bias_b, biasg_b;
     {
       const float cbp = Bp[f];
       const T bhi = (T)cbp, blo = (T)(cbp - (float)bhi);
+      const T ghi = (T)cbg2, glo = (T)(cbg2 - (float)ghi);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         one_a[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
         bias_b[e] = hl == 0 && e == 0 ? bhi : (hl == 0 && e == 1 ? blo : (T)0.f);
+        biasg_b[e] = hl == 0 && e == 0 ? ghi : (hl == 0 && e == 1 ? glo : (T)0.f);
       }
     }
     // token of MFMA row r: 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3), so D slot v of lane
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[0][e] = o[1][e] = (T)0.0f;
           } else {
-            f32x16 accP = Mma<T>::m32(one_a, bias_b, f32x16{}), accG = {};
+            f32x16 accP = Mma<T>::m32(one_a, bias_b, f32x16{}), accG = Mma<T>::m32(one_a, biasg_b, f32x16{});
 #pragma unroll
             for (int k = 0; k < KS; ++k) {
               const V8 xa = *reinterpret_cast<const V8*>(&xs[bb][tok * ROW + (((2 * k + hl) ^ key(tok)) << 4)]);
@@ -292,7 +301,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
             if (st == 2) {
 #pragma unroll
               for (int v = 0; v < 16; ++v) {
-                const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+                const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(accG[v]));
                 o[v / 8][v % 8] = (T)(accP[v] * gate);
               }
             } else {
@@ -302,7 +311,7 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                   const int v = 4 * gq + j;
-                  const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[v], -kLog2e, cbg2)));
+                  const float gate = __builtin_amdgcn_rcpf(1.0f + fast_exp2(accG[v]));
                   o[v / 8][v % 8] = (T)(accP[v] * gate * rm[j]);
                 }
               }
@@ -1023,7 +1032,7 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
   __shared__ __attribute__((aligned(16))) char ys[2][64 * ROW];  // raw y, token-major
   __shared__ __attribute__((aligned(16))) char xs[2][64 * ROW];  // normalised x
   __shared__ __attribute__((aligned(16))) T os[2][64 * COUT];    // gated output, token-major
-  __shared__ __attribute__((aligned(16))) float cst[3][COUT];    // sum(Wp_c), Bp, -log2(e) Bg
+  __shared__ __attribute__((aligned(16))) float cst[2][COUT];    // sum(Wp_c), Bp
   // LN statistics of y per token and loader wave: (sum, sum of squares) over the wave's 32 channels
   __shared__ __attribute__((aligned(16))) float2 ystat[2][64][4];
 
@@ -1031,7 +1040,6 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
   for (int i = tid; i < COUT; i += 768) {
     cst[0][i] = sWp[i];
     cst[1][i] = Bp[i];
-    cst[2][i] = -kLog2e * Bg[i];
   }
   __syncthreads();  // cst
 
@@ -1154,13 +1162,26 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
     // A operand row r = col holds feature 32 fset + prow: D slot v of lane half hl is then
     // feature 32 fset + 16 hl + v
     const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
-    V8 wp[KS], wg[KS];
+    // G's rows times -log2(e) and its bias -log2(e) Bg as one more MFMA k-step (A: the row's bias
+    // as two 16-bit parts at k = 0, 1; B: 1 there for every token), so the accumulator is the
+    // gate's exp2 argument: no multiply-add per output (0.159 -> 0.149 ms at L = 1024, outputs
+    // within a bf16 step)
+    V8 wp[KS], wg[KS], gb_a, one_b;
     {
       const int64_t frow = (int64_t)(32 * fset + prow) * C;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         wp[s] = ldg<V8>(Wp + frow + 16 * s + 8 * hl);
-        wg[s] = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+        const V8 g = ldg<V8>(Wg + frow + 16 * s + 8 * hl);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wg[s][e] = (T)((float)g[e] * -kLog2e);
+      }
+      const float cb = -kLog2e * Bg[32 * fset + prow];
+      const T bhi = (T)cb, blo = (T)(cb - (float)bhi);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gb_a[e] = hl == 0 && e == 0 ? bhi : (hl == 0 && e == 1 ? blo : (T)0.f);
+        one_b[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
       }
     }
     const int wt = tid - NL;  // store role: 16-byte chunks wt and 512 + wt of the output tile
@@ -1193,7 +1214,7 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
       // the gate's GEMM first, then the P GEMM's MFMAs interleaved with the gate's exponentials and
       // reciprocals (which need only accG), so the matrix core and the VALU of this wave work
       // together (3 % faster than the two chains interleaved at L = 1024 and 2048, same results)
-      f32x16 accP = {}, accG = {};
+      f32x16 accP = {}, accG = Mma<T>::m32(gb_a, one_b, f32x16{});
 #pragma unroll
       for (int k = 0; k < KS; ++k)
         accG = Mma<T>::m32(wg[k], *reinterpret_cast<const V8*>(xrow + (((2 * k + hl) ^ (tok & 15)) << 4)), accG);
@@ -1204,16 +1225,12 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
       for (int k = 0; k < KS; ++k)
         accP = Mma<T>::m32(wp[k], *reinterpret_cast<const V8*>(yrow + (((2 * k + hl) ^ yswz(tok)) << 4)), accP);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 cg = *reinterpret_cast<const f32x4*>(&cst[2][f0 + 4 * q]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) gate[4 * q + j] = __builtin_amdgcn_rcpf(1.0f + fast_exp2(fmaf(accG[4 * q + j], -kLog2e, cg[j])));
-      }
+      for (int v = 0; v < 16; ++v) gate[v] = __builtin_amdgcn_rcpf(1.0f + fast_exp2(accG[v]));
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 6, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
       // LN statistics of y for this token: the loader waves' partial sums over 32 channels each
