@@ -678,6 +678,28 @@ def test_gate_tuned_matches_generic(device, C):
         f"gate C={C} residual: max|d|={diff:.3e} (bar {tol:.3e}) cos={cos:.6f}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gate_saturating_bias(device, dtype):
+    """Gate biases far beyond where the sigmoid saturates (|bg| = 6e4, beyond fp16's range once
+    scaled by log2(e)): the tuned gate clamps the scaled bias before splitting it into two 16-bit
+    parts, so those features gate to exactly 0 or 1, as the any-shape gate's fp32 sigmoid does."""
+    from triangleops_amd.triangle_attn.kernel import _gate_out_generic, gate_out_forward
+
+    C = 128
+    g = torch.Generator().manual_seed(5)
+    o = torch.randn(9, 70, C, generator=g).to(dtype).to(device)
+    x = torch.randn(9, 70, C, generator=g).to(dtype).to(device)
+    Wg = (torch.randn(C, C, generator=g) * C**-0.5).to(dtype).to(device)
+    Wo = (torch.randn(C, C, generator=g) * C**-0.5).to(dtype).to(device)
+    bg = (0.1 * torch.randn(C, generator=g))
+    bg[::4] = 6e4
+    bg[1::4] = -6e4
+    bg = bg.to(dtype).to(device)
+    a = gate_out_forward(o, x, Wg, bg, Wo, None)
+    b = _gate_out_generic(o, x, Wg, bg, Wo, None)
+    _check(a, b.float().cpu(), dtype, f"gate saturating bias {dtype}")
+
+
 @pytest.mark.parametrize("N,C,H,D", [(40, 96, 3, 24), (70, 64, 2, 64), (130, 32, 8, 8), (257, 64, 4, 16)])
 @pytest.mark.parametrize("mask", ["pad", "random"])
 def test_tri_any_shape(device, N, C, H, D, mask):

@@ -75,7 +75,8 @@ __global__ __launch_bounds__(512) void gate_out_kernel(const T* __restrict__ o, 
       for (int e = 0; e < 8; ++e) wg[s][e] = (T)((float)g[e] * -kLog2e);
       wo[s] = ldg<V8>(Wo + frow + 16 * s + 8 * hl);
     }
-    const float cb = bg ? -kLog2e * (float)bg[32 * fset + prow] : 0.f;
+    // (clamped: exp2 saturates long before, and the 16-bit parts of a larger value could overflow)
+    const float cb = fminf(fmaxf(bg ? -kLog2e * (float)bg[32 * fset + prow] : 0.f, -3e4f), 3e4f);
     const T bhi = (T)cb, blo = (T)(cb - (float)bhi);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {

@@ -254,7 +254,9 @@ __global__ __launch_bounds__(64 * (4 + NWR)) void tmu_in_kernel(const T* __restr
     {
       const float cbp = Bp[f];
       const T bhi = (T)cbp, blo = (T)(cbp - (float)bhi);
-      const T ghi = (T)cbg2, glo = (T)(cbg2 - (float)ghi);
+      // (clamped: exp2 saturates long before, and the 16-bit parts of a larger value could overflow)
+      const float cg = fminf(fmaxf(cbg2, -3e4f), 3e4f);
+      const T ghi = (T)cg, glo = (T)(cg - (float)ghi);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         one_a[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
@@ -1176,7 +1178,7 @@ __global__ __launch_bounds__(768) void tmu_out_kernel(const T* __restrict__ y, c
 #pragma unroll
         for (int e = 0; e < 8; ++e) wg[s][e] = (T)((float)g[e] * -kLog2e);
       }
-      const float cb = -kLog2e * Bg[32 * fset + prow];
+      const float cb = fminf(fmaxf(-kLog2e * Bg[32 * fset + prow], -3e4f), 3e4f);  // as in the input phase
       const T bhi = (T)cb, blo = (T)(cb - (float)bhi);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
