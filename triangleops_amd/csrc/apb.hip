@@ -333,16 +333,12 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   __shared__ __attribute__((aligned(16))) char og_s[TOK * ROW];  // merged Og, then the gated values
   __shared__ __attribute__((aligned(16))) char x_s[TOK * ROW];   // gate input X
   __shared__ __attribute__((aligned(16))) T o_s[TOK * C];         // output tile, query-major
-  __shared__ __attribute__((aligned(16))) float cst[C];           // bo
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
   const int64_t q0 = (int64_t)blockIdx.x * TOK;
   auto swz = [](int t, int chunk) { return (chunk ^ row_key<C>(t)) << 4; };
 
-  for (int i = tid; i < C; i += 256) {
-    cst[i] = bo ? (float)bo[i] : 0.f;
-  }
   // X rows of the block's queries (rows past M repeat row M - 1; their results are not stored)
   {
     const int t = tid >> 4, c = tid & 15;
@@ -351,9 +347,10 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   }
   // weight rows as MFMA A operands: row col of wave w is feature 32 w + prow
   const int prow = 16 * ((col >> 2) & 1) + 4 * (col >> 3) + (col & 3);
-  // G's rows times -log2(e) and its bias -log2(e) bg as one more MFMA k-step, as in the triangle
-  // gate kernel (the accumulator is the gate's exp2 argument; same bits as that kernel)
-  V8 wg[KS], wo[KS], gb_a, one_b;
+  // G's rows times -log2(e) and its bias -log2(e) bg as one more MFMA k-step, and bo as W_o's, as
+  // in the triangle gate kernel (the accumulator is the gate's exp2 argument; same bits as that
+  // kernel)
+  V8 wg[KS], wo[KS], gb_a, one_b, ob_a;
   {
     const int64_t frow = (int64_t)(32 * wave + prow) * C;
 #pragma unroll
@@ -370,6 +367,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     for (int e = 0; e < 8; ++e) {
       gb_a[e] = hl == 0 && e == 0 ? bhi : (hl == 0 && e == 1 ? blo : (T)0.f);
       one_b[e] = (T)((hl == 0 && e < 2) ? 1.f : 0.f);
+      ob_a[e] = hl == 0 && e == 0 && bo ? bo[32 * wave + prow] : (T)0.f;  // bo (16-bit) as W_o's bias k-step
     }
   }
   // ---- merge the split partials ----
@@ -429,7 +427,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     for (int e = 0; e < 8; ++e) r[e] = (T)(ot[e] / lt);
     *reinterpret_cast<V8*>(&og_s[t * ROW + swz(t, 4 * g + (j & 3))]) = r;
   }
-  __syncthreads();  // cst, X and Og staged
+  __syncthreads();  // X and Og staged
 
   // MFMA column col holds query col % TOK (the block's queries twice; both copies write the same
   // values to the same LDS locations)
@@ -458,7 +456,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
   __syncthreads();  // gated tile complete
   {  // GEMM 2 on the gated tile -> query-major output tile
     const char* trow = &og_s[tok * ROW];
-    f32x16 acc = {};
+    f32x16 acc = Mma<T>::m32(ob_a, one_b, f32x16{});
 #pragma unroll
     for (int k = 0; k < KS; ++k)
       acc = Mma<T>::m32(wo[k], *reinterpret_cast<const V8*>(trow + swz(tok, 2 * k + hl)), acc);
@@ -466,7 +464,7 @@ __global__ __launch_bounds__(256) void apb_merge_gate_kernel(const float* __rest
     for (int h = 0; h < 2; ++h) {
       V8 r;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r[e] = (T)(acc[8 * h + e] + cst[f0 + 8 * h + e]);
+      for (int e = 0; e < 8; ++e) r[e] = (T)acc[8 * h + e];
       const int c = f0 / 8 + h;
       *reinterpret_cast<V8*>(&o_s[tok * C + ((c ^ row_key<C>(tok)) << 3)]) = r;
     }
