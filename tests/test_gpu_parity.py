@@ -303,6 +303,20 @@ def test_tri_fp16(device):
     _check(_tri_call(inp, device), _tri_ref(inp), torch.float16, "tri fp16")
 
 
+@pytest.mark.parametrize("N,mask,qk", [(260, "pad", 1.0), (520, "random", 1.0), (260, "random", 2.0)])
+def test_tri_fp16_two_query_tiles(device, N, mask, qk):
+    """fp16 triangle attention where each wave holds two query tiles (N > 128): the running row max
+    enters the accumulator initialiser beside the bias, and with Q and K scaled up (qk = 2: scores
+    spread over tens of log2 units, so later tiles' weights would overflow fp16 under the first
+    tile's max) the max is raised mid-row and O / l rescaled.  (Much larger scores put the fp16
+    rounding of Q and K, relative to the score, beyond the fp16 bar against the fp32 oracle, in any
+    16-bit attention.)"""
+    inp = tri_inputs(N, seed=N + 7, mask=mask, dtype=torch.float16, bias_z=True)
+    inp["WQ"] = (inp["WQ"].float() * qk).to(torch.float16)
+    inp["WK"] = (inp["WK"].float() * qk).to(torch.float16)
+    _check(_tri_call(inp, device), _tri_ref(inp), torch.float16, f"tri fp16 N={N} mask={mask} qk={qk}")
+
+
 def test_tri_ending_node(device):
     """Ending node = op on X^T (a strided view, no copy) with mask^T, output transposed back."""
     N = 160
