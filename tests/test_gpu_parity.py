@@ -364,7 +364,7 @@ def _config_rows(n, k=32):
 @pytest.mark.parametrize("N", [512, 1024, 2048])
 def test_tri_config_sizes(device, N):
     """BASELINE configs 3/4 sizes (pad mask), starting and ending node: the whole output at
-    N <= 1024; at 2048 (8-wave blocks) 34 rows spread over the grid, every query of each."""
+    N <= 1024; at 2048 34 rows spread over the grid, every query of each."""
     inp = tri_inputs(N, seed=0, mask="pad")
     rows = None if N <= 1024 else _config_rows(N)
     out = _tri_call(inp, device)
@@ -404,7 +404,7 @@ def test_tri_shift_free_softmax_fallback(device, N, shift):
     exactly up to 256, and head 0's tiles (every query tile) and head 2's tiles of query tiles 2 and 3
     are shifted by +150 (the shift-free weights overflow) or -200 (they underflow): those heads must
     match the unshifted run to the bf16 bar, while heads 1 and 3, which run the shift-free path in the
-    same launch, must match it bitwise.  N = 2100 runs the 8-wave blocks."""
+    same launch, must match it bitwise.  N = 2100 runs the ragged 4-wave blocks."""
     from triangleops_amd.triangle_attn.kernel import attention_core, prep_forward
 
     inp = to_dev(tri_inputs(N, seed=N + 7, mask="random", bias_z=True), device)
@@ -590,14 +590,16 @@ def test_tri_large_n_kernel(device, N, mask):
     _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} mask={mask}")
 
 
-@pytest.mark.parametrize("N,mask", [(2100, "random"), (2049, "pad")])
-def test_tri_eight_wave_blocks(device, N, mask):
-    """From N = 2048 on the attention runs 8-wave blocks of 512 queries: ragged N (the last block's
-    query tiles lie partly or wholly past N), sampled rows and query columns across the last block."""
-    inp = tri_inputs(N, seed=N + 3, mask=mask, bias_z=True)
+@pytest.mark.parametrize("N,mask,C", [(2100, "random", 128), (2049, "pad", 128), (4097, "pad", 64),
+                                      (4100, "random", 64)])
+def test_tri_large_ragged_blocks(device, N, mask, C):
+    """Ragged N (the last block's query tiles lie partly or wholly past N) on sampled rows: 4-wave
+    blocks of 256 queries at N = 2049 / 2100, and 8-wave blocks of 512 queries, which run from
+    N = 4096 on, at N = 4097 / 4100 (C_in = 64 keeps the fp32 oracle's input small)."""
+    inp = tri_inputs(N, C=C, seed=N + 3, mask=mask, bias_z=True)
     out = _tri_call(inp, device)
     rows = torch.tensor([0, N // 2, N - N // 10 - 1, N - 1])
-    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri 8-wave N={N} mask={mask}")
+    _check(out[rows].cpu(), _tri_ref(inp, rows=rows), torch.bfloat16, f"tri N={N} C={C} mask={mask}")
 
 
 @pytest.mark.parametrize("masked", [False, True])

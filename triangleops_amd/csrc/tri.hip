@@ -41,7 +41,7 @@ constexpr int kMaxKB = kMaxN / 64;
 
 // The pre-pass buffers' key stride: N rounded up to a multiple of 64 (at least 64).
 #ifndef TRI_NW8_MIN_N
-#define TRI_NW8_MIN_N 2048  // from this N on, 8-wave attention blocks (half the KV block copies per query)
+#define TRI_NW8_MIN_N 4096  // from this N on, 8-wave attention blocks (half the KV block copies per query)
 #endif
 static inline int64_t tri_ldn(int64_t N) { return N <= 64 ? 64 : (N + 63) / 64 * 64; }
 #ifndef TRI_WPE
