@@ -224,6 +224,10 @@ def attention_core(Qp, KV, bias, out, *, N, ldn, mask=None):
     sm0 = sm1 = 0
     if mask is not None:
         m8 = mask.view(torch.int8) if mask.dtype in (torch.bool, torch.uint8) else mask.to(torch.int8)
+        if m8.stride(1) != 1:
+            # every block reads its row's whole key mask a byte per key: with keys N bytes apart (the
+            # ending node's mask.T) each byte is its own cache line, so copy to key-contiguous rows
+            m8 = m8.contiguous()
         sm0, sm1 = m8.stride()
     _native.call(
         "tops_tri_attention",
